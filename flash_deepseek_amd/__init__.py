@@ -1,0 +1,167 @@
+"""flash_deepseek_amd -- MI355X (gfx950) MoE expert hot path of flash_deepseek.
+
+The Python layer is a thin host-side mirror of the reference's C operators
+for this path, over the C ABI of libfdm.so (include/fdm.h):
+
+  reference (infer.m / quant.c)            here
+  ---------------------------------------  ----------------------------------
+  metal_init(model_path)        :1276      init(device)
+  dequantize_row_q4_K / _q6_K   quant.c    dequantize_row_q4_K / _q6_K (device)
+  fp16_to_fp32                  quant.c:4  fp16_to_fp32 (device, vectorised)
+  enc_matvec_q + dequant_matvec_q4k/q6k    matvec_q4k / matvec_q6k
+  encode_expert                 :1559      expert_ffn
+  mv(gate_inp) + route()        :1881-1883 router_logits + route
+  load_layer_weights (MoE part) :1794      attach_layer / upload_layer
+  metal_moe_forward             :1604      moe_forward / moe_forward_host
+  layer_forward MoE branch      :1878-1922 moe_layer
+
+Tensors are torch tensors on the GPU (torch provides device memory and the
+current stream; all compute is the library's own HIP kernels).  Every call
+is asynchronous on torch's current stream unless noted.
+"""
+import ctypes
+
+from . import _lib
+from ._lib import (EXPERT_Q4K_BYTES, EXPERT_Q6K_BYTES, HIDDEN, MAX_K, MAX_LAYERS, MAX_TOKENS,
+                   MOE_FFN, N_EXPERTS, Q4K_BLOCK_SIZE, Q6K_BLOCK_SIZE, QK_K, FdmError)
+
+__all__ = [
+    "init", "shutdown", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
+    "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
+    "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
+    "moe_forward_host", "moe_layer", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
+    "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
+]
+
+call = _lib.call
+lib = _lib.lib
+
+
+def _p(t):
+    """Device address of a tensor (or None / an int address)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def _stream(stream=None):
+    if stream is not None:
+        return stream if isinstance(stream, int) else stream.cuda_stream
+    import torch
+    return torch.cuda.current_stream().cuda_stream
+
+
+# ---- lifecycle -----------------------------------------------------------------
+def init(device=0):
+    """Select the device and allocate the workspace (metal_init).  Raises
+    FdmError when no gfx950 device is usable."""
+    call("fdm_init", int(device))
+
+
+def shutdown():
+    call("fdm_shutdown")
+
+
+def available():
+    """1 when initialised, 0 otherwise (metal_init's return convention)."""
+    return lib.fdm_available()
+
+
+# ---- quant.h twins ---------------------------------------------------------------
+def fp16_to_fp32(src, dst, n=None, stream=None):
+    n = src.numel() if n is None else n
+    call("fdm_fp16_to_fp32", _p(src), _p(dst), n, _stream(stream))
+
+
+def dequantize_row_q4_K(src, dst, n, stream=None):
+    """quant.c:36-61 on the device: n weights (multiple of 256)."""
+    call("fdm_dequant_q4k", _p(src), _p(dst), n, _stream(stream))
+
+
+def dequantize_row_q6_K(src, dst, n, stream=None):
+    """quant.c:63-92 on the device."""
+    call("fdm_dequant_q6k", _p(src), _p(dst), n, _stream(stream))
+
+
+# ---- matvec / expert -------------------------------------------------------------
+def matvec_q4k(W, x, y, out_dim, in_dim, stream=None):
+    call("fdm_matvec_q4k", _p(W), _p(x), _p(y), out_dim, in_dim, _stream(stream))
+
+
+def matvec_q6k(W, x, y, out_dim, in_dim, stream=None):
+    call("fdm_matvec_q6k", _p(W), _p(x), _p(y), out_dim, in_dim, _stream(stream))
+
+
+def expert_ffn(blob, expert_size, x, out, act=None, stream=None):
+    call("fdm_expert_ffn", _p(blob), expert_size, _p(x), _p(out), _p(act), _stream(stream))
+
+
+# ---- router ----------------------------------------------------------------------
+def router_logits(Wg, x, logits, T=1, stream=None):
+    n_exp, dim = Wg.shape
+    call("fdm_router_logits", _p(Wg), _p(x), n_exp, dim, T, _p(logits), _stream(stream))
+
+
+def route(logits, bias, K, idx, w, T=1, stream=None):
+    call("fdm_route", _p(logits), _p(bias), T, K, _p(idx), _p(w), _stream(stream))
+
+
+# ---- resident layers ---------------------------------------------------------------
+def attach_layer(L, experts, expert_size, Wg, bias, shared=None, n_experts=N_EXPERTS):
+    """Register device-resident buffers as layer L (caller keeps ownership)."""
+    call("fdm_layer_attach", L, _p(experts), expert_size, n_experts, _p(Wg), _p(bias),
+         _p(shared))
+
+
+def upload_layer(L, experts_host, expert_size, Wg_host, bias_host, shared_host=None,
+                 n_experts=N_EXPERTS):
+    """Copy host arrays (numpy) to HBM as layer L (library-owned)."""
+    def hp(a):
+        return None if a is None else a.ctypes.data
+    call("fdm_layer_upload", L, hp(experts_host), expert_size, n_experts, hp(Wg_host),
+         hp(bias_host), hp(shared_host))
+
+
+def release_layer(L):
+    call("fdm_layer_release", L)
+
+
+def layer_info(L):
+    es, q6, ne = ctypes.c_size_t(), ctypes.c_int(), ctypes.c_int()
+    call("fdm_layer_query", L, ctypes.byref(es), ctypes.byref(q6), ctypes.byref(ne))
+    return es.value, bool(q6.value), ne.value
+
+
+# ---- MoE ---------------------------------------------------------------------------
+def moe_forward(L, h_post, exp_idx, exp_w, K, moe_out, stream=None):
+    """metal_moe_forward with device tensors: moe_out = sum_k w_k E_k(h_post)."""
+    call("fdm_moe_forward", L, _p(h_post), _p(exp_idx), _p(exp_w), K, _p(moe_out),
+         _stream(stream))
+
+
+def moe_forward_host(L, h_post, exp_idx, exp_w, K, moe_out):
+    """metal_moe_forward's exact convention: numpy host arrays, synchronous."""
+    call("fdm_moe_forward_host", L, h_post.ctypes.data, exp_idx.ctypes.data,
+         exp_w.ctypes.data, K, moe_out.ctypes.data)
+
+
+def moe_layer(L, h_post, h_in, K, hidden, idx=None, w=None, stream=None):
+    """MoE branch of layer_forward: hidden = h_in + routed + shared."""
+    call("fdm_moe_layer", L, _p(h_post), _p(h_in), K, _p(hidden), _p(idx), _p(w),
+         _stream(stream))
+
+
+# ---- synthetic data ------------------------------------------------------------------
+def synth_q4k(dst, n_blocks, seed, stream=None):
+    call("fdm_synth_q4k", _p(dst), n_blocks, seed, _stream(stream))
+
+
+def synth_q6k(dst, n_blocks, seed, stream=None):
+    call("fdm_synth_q6k", _p(dst), n_blocks, seed, _stream(stream))
+
+
+def synth_normal(dst, n, mean, std, seed, stream=None):
+    call("fdm_synth_normal", _p(dst), n, mean, std, seed, _stream(stream))

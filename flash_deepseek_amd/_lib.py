@@ -1,0 +1,106 @@
+"""ctypes binding of libfdm.so, the C ABI declared in include/fdm.h.
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback for any entry point.
+"""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfdm.so")
+
+FDM_OK = 0
+FDM_E_INVAL = -1
+FDM_E_NODEV = -2
+FDM_E_HIP = -3
+FDM_E_STATE = -4
+FDM_E_NOMEM = -5
+FDM_E_SIZE = -6
+FDM_E_IO = -7
+
+QK_K = 256
+Q4K_BLOCK_SIZE = 144
+Q6K_BLOCK_SIZE = 210
+HIDDEN = 7168
+MOE_FFN = 2048
+N_EXPERTS = 256
+MAX_K = 16
+MAX_LAYERS = 61
+MAX_TOKENS = 512
+EXPERT_Q4K_BYTES = 24772608
+EXPERT_Q6K_BYTES = 28557312
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_sz = ctypes.c_size_t
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_f = ctypes.c_float
+
+# name -> argtypes (all functions return int unless listed in _RESTYPES)
+SIGNATURES = {
+    "fdm_init": [_i],
+    "fdm_shutdown": [],
+    "fdm_available": [],
+    "fdm_strerror": [_i],
+    "fdm_last_error": [],
+    "fdm_device_cus": [],
+    "fdm_malloc": [ctypes.POINTER(_vp), _sz],
+    "fdm_free": [_vp],
+    "fdm_memcpy_h2d": [_vp, _vp, _sz, _vp],
+    "fdm_memcpy_d2h": [_vp, _vp, _sz, _vp],
+    "fdm_stream_sync": [_vp],
+    "fdm_fp16_to_fp32": [_vp, _vp, _sz, _vp],
+    "fdm_dequant_q4k": [_vp, _vp, _sz, _vp],
+    "fdm_dequant_q6k": [_vp, _vp, _sz, _vp],
+    "fdm_matvec_q4k": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "fdm_matvec_q6k": [_vp, _vp, _vp, _u32, _u32, _vp],
+    "fdm_expert_ffn": [_vp, _sz, _vp, _vp, _vp, _vp],
+    "fdm_router_logits": [_vp, _vp, _i, _i, _i, _vp, _vp],
+    "fdm_route": [_vp, _vp, _i, _i, _vp, _vp, _vp],
+    "fdm_layer_attach": [_i, _vp, _sz, _i, _vp, _vp, _vp],
+    "fdm_layer_upload": [_i, _vp, _sz, _i, _vp, _vp, _vp],
+    "fdm_layer_release": [_i],
+    "fdm_layer_query": [_i, ctypes.POINTER(_sz), ctypes.POINTER(_i), ctypes.POINTER(_i)],
+    "fdm_moe_forward": [_i, _vp, _vp, _vp, _i, _vp, _vp],
+    "fdm_moe_forward_host": [_i, _vp, _vp, _vp, _i, _vp],
+    "fdm_moe_layer": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
+    "fdm_synth_q4k": [_vp, _sz, _u64, _vp],
+    "fdm_synth_q6k": [_vp, _sz, _u64, _vp],
+    "fdm_synth_normal": [_vp, _sz, _f, _f, _u64, _vp],
+}
+_RESTYPES = {"fdm_strerror": ctypes.c_char_p, "fdm_last_error": ctypes.c_char_p}
+
+
+class FdmError(RuntimeError):
+    def __init__(self, code, fn, detail):
+        self.code = code
+        super().__init__(f"{fn} failed ({code}): {detail}")
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -m flash_deepseek_amd.build` "
+            "(hipcc, gfx950). There is no CPU fallback.")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, _i)
+    return lib
+
+
+lib = _load()
+
+
+def check(rc, fn="fdm call"):
+    if rc != FDM_OK:
+        detail = lib.fdm_last_error().decode(errors="replace")
+        raise FdmError(rc, fn, detail or lib.fdm_strerror(rc).decode())
+    return rc
+
+
+def call(name, *args):
+    """Call an fdm_* entry point and raise FdmError on a non-zero code."""
+    return check(getattr(lib, name)(*args), name)

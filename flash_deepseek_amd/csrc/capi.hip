@@ -1,0 +1,536 @@
+// capi.hip -- the C ABI declared in include/fdm.h: argument checks, the
+// per-device workspace, the resident-layer table and the kernel sequences.
+// The kernels themselves live in *_kernels.hip.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/fdm.h"
+#include "fdm_internal.h"
+
+namespace fdm {
+
+int g_num_cus = 0;
+
+namespace {
+
+thread_local char t_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(t_err, sizeof t_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(FDM_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define FDM_HIP(call)                                   \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return hip_fail(e_, #call);   \
+  } while (0)
+
+struct Workspace {
+  XGroup* xd = nullptr;       // digits of activations (up to FDM_MAX_TOKENS x 112)
+  float* logits = nullptr;    // FDM_MAX_TOKENS x 256
+  int* idx = nullptr;         // FDM_MAX_TOKENS x 16
+  float* w = nullptr;         // FDM_MAX_TOKENS x 16
+  float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
+  XGroup* act_xd = nullptr;   // (FDM_MAX_K + 1) x 32
+  int* counter = nullptr;     // last-workgroup counter of the router
+  float* stage_x = nullptr;   // host-API staging: h_post
+  float* stage_y = nullptr;   //                   moe_out
+  int* stage_idx = nullptr;   //                   exp_idx
+  float* stage_w = nullptr;   //                   exp_w
+};
+
+struct Layer {
+  bool resident = false;
+  bool owned = false;  // buffers allocated by fdm_layer_upload
+  const uint8_t* experts = nullptr;
+  size_t expert_size = 0;
+  int n_experts = 0;
+  bool down_q6 = false;
+  const float* Wg = nullptr;
+  const float* bias = nullptr;
+  const uint8_t* shared = nullptr;
+};
+
+struct State {
+  bool ready = false;
+  int device = -1;
+  Workspace ws;
+  Layer layers[FDM_MAX_LAYERS];
+};
+
+State g;
+
+constexpr size_t kXdGroups = (size_t)FDM_MAX_TOKENS * (FDM_HIDDEN / 64);
+
+int check_ready() {
+  if (!g.ready) return fail(FDM_E_STATE, "fdm_init has not been called");
+  return FDM_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Down type from the packed expert size, as infer.m:1810-1821.
+int down_type(size_t expert_size, bool* q6) {
+  if (expert_size == FDM_EXPERT_Q4K_BYTES) {
+    *q6 = false;
+    return FDM_OK;
+  }
+  if (expert_size == FDM_EXPERT_Q6K_BYTES) {
+    *q6 = true;
+    return FDM_OK;
+  }
+  return fail(FDM_E_SIZE, "expert size %zu is neither %llu (Q4_K down) nor %llu (Q6_K down)",
+              expert_size, FDM_EXPERT_Q4K_BYTES, FDM_EXPERT_Q6K_BYTES);
+}
+
+void free_workspace() {
+  Workspace& w = g.ws;
+  void* ptrs[] = {w.xd,      w.logits,  w.idx,     w.w,         w.act,     w.act_xd,
+                  w.counter, w.stage_x, w.stage_y, w.stage_idx, w.stage_w};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  g.ws = Workspace();
+}
+
+int alloc_workspace() {
+  Workspace& w = g.ws;
+  FDM_HIP(hipMalloc(&w.xd, kXdGroups * sizeof(XGroup)));
+  FDM_HIP(hipMalloc(&w.logits, (size_t)FDM_MAX_TOKENS * FDM_N_EXPERTS * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.idx, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.w, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.act, (size_t)(FDM_MAX_K + 1) * FDM_MOE_FFN * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.act_xd, (size_t)(FDM_MAX_K + 1) * (FDM_MOE_FFN / 64) * sizeof(XGroup)));
+  FDM_HIP(hipMalloc(&w.counter, 256));
+  FDM_HIP(hipMemset(w.counter, 0, 256));
+  FDM_HIP(hipMalloc(&w.stage_x, FDM_HIDDEN * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.stage_y, FDM_HIDDEN * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.stage_idx, FDM_MAX_K * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.stage_w, FDM_MAX_K * sizeof(float)));
+  return FDM_OK;
+}
+
+void release_layer(Layer& L) {
+  if (L.resident && L.owned) {
+    (void)hipFree(const_cast<uint8_t*>(L.experts));
+    (void)hipFree(const_cast<float*>(L.Wg));
+    if (L.bias) (void)hipFree(const_cast<float*>(L.bias));
+    if (L.shared) (void)hipFree(const_cast<uint8_t*>(L.shared));
+  }
+  L = Layer();
+}
+
+int get_layer(int L, Layer** out) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (!g.layers[L].resident) return fail(FDM_E_STATE, "layer %d is not resident", L);
+  *out = &g.layers[L];
+  return FDM_OK;
+}
+
+int check_K(int K) {
+  if (K < 1 || K > FDM_MAX_K) return fail(FDM_E_INVAL, "K=%d outside 1..%d", K, FDM_MAX_K);
+  return FDM_OK;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+SlotTable slots_for(const Layer& L, const int* idx, const float* w, int K, bool with_shared) {
+  SlotTable t;
+  t.experts = L.experts;
+  t.expert_size = L.expert_size;
+  t.n_experts = L.n_experts;
+  t.shared = with_shared ? L.shared : nullptr;
+  t.idx = idx;
+  t.w = w;
+  t.K = K;
+  t.n_slots = K + ((with_shared && L.shared) ? 1 : 0);
+  return t;
+}
+
+}  // namespace
+}  // namespace fdm
+
+using namespace fdm;
+
+extern "C" {
+
+int fdm_init(int device) {
+  if (g.ready) {
+    if (device == g.device) return FDM_OK;
+    return fail(FDM_E_STATE, "already initialised on device %d", g.device);
+  }
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) return fail(FDM_E_NODEV, "no HIP device available");
+  if (device < 0 || device >= n) return fail(FDM_E_INVAL, "device %d of %d", device, n);
+  FDM_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  FDM_HIP(hipGetDeviceProperties(&prop, device));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(FDM_E_NODEV, "device %d is %s; this build targets gfx950", device,
+                prop.gcnArchName);
+  g_num_cus = prop.multiProcessorCount;
+  if (int rc = alloc_workspace()) {
+    free_workspace();
+    return rc;
+  }
+  g.device = device;
+  g.ready = true;
+  return FDM_OK;
+}
+
+int fdm_shutdown(void) {
+  if (!g.ready) return FDM_OK;
+  (void)hipDeviceSynchronize();
+  for (auto& L : g.layers) release_layer(L);
+  free_workspace();
+  g.ready = false;
+  g.device = -1;
+  return FDM_OK;
+}
+
+int fdm_available(void) { return g.ready ? 1 : 0; }
+
+const char* fdm_strerror(int code) {
+  switch (code) {
+    case FDM_OK: return "ok";
+    case FDM_E_INVAL: return "invalid argument";
+    case FDM_E_NODEV: return "no usable gfx950 device";
+    case FDM_E_HIP: return "HIP runtime error";
+    case FDM_E_STATE: return "not initialised or layer not resident";
+    case FDM_E_NOMEM: return "device allocation failed";
+    case FDM_E_SIZE: return "expert size matches neither R1 layout";
+    case FDM_E_IO: return "file error";
+    default: return "unknown error";
+  }
+}
+
+const char* fdm_last_error(void) { return t_err; }
+
+int fdm_device_cus(void) { return g.ready ? g_num_cus : 0; }
+
+int fdm_malloc(void** d_ptr, size_t bytes) {
+  if (!d_ptr) return fail(FDM_E_INVAL, "null out pointer");
+  if (int rc = check_ready()) return rc;
+  hipError_t e = hipMalloc(d_ptr, bytes);
+  if (e != hipSuccess) return fail(FDM_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  return FDM_OK;
+}
+
+int fdm_free(void* d_ptr) {
+  if (int rc = check_ready()) return rc;
+  FDM_HIP(hipFree(d_ptr));
+  return FDM_OK;
+}
+
+int fdm_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes, void* stream) {
+  if (int rc = check_ready()) return rc;
+  FDM_HIP(hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stream) {
+  if (int rc = check_ready()) return rc;
+  FDM_HIP(hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_stream_sync(void* stream) {
+  if (int rc = check_ready()) return rc;
+  FDM_HIP(hipStreamSynchronize(as_stream(stream)));
+  return FDM_OK;
+}
+
+// ---- quant.h twins --------------------------------------------------------
+int fdm_fp16_to_fp32(const uint16_t* d_src, float* d_dst, size_t n, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_src || !d_dst) return fail(FDM_E_INVAL, "null pointer");
+  if (n == 0) return FDM_OK;
+  FDM_HIP(launch_fp16_to_fp32(d_src, d_dst, n, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_dequant_q4k(const void* d_src, float* d_dst, size_t n, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_src || !d_dst) return fail(FDM_E_INVAL, "null pointer");
+  if (n % FDM_QK_K) return fail(FDM_E_INVAL, "n=%zu is not a multiple of 256", n);
+  if (!aligned(d_src, 4) || !aligned(d_dst, 8))
+    return fail(FDM_E_INVAL, "Q4_K source must be 4-byte and output 8-byte aligned");
+  if (n == 0) return FDM_OK;
+  FDM_HIP(launch_dequant_q4k(static_cast<const uint8_t*>(d_src), d_dst, n / FDM_QK_K,
+                             as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_dequant_q6k(const void* d_src, float* d_dst, size_t n, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_src || !d_dst) return fail(FDM_E_INVAL, "null pointer");
+  if (n % FDM_QK_K) return fail(FDM_E_INVAL, "n=%zu is not a multiple of 256", n);
+  if (!aligned(d_dst, 4)) return fail(FDM_E_INVAL, "output must be 4-byte aligned");
+  if (n == 0) return FDM_OK;
+  FDM_HIP(launch_dequant_q6k(static_cast<const uint8_t*>(d_src), d_dst, n / FDM_QK_K,
+                             as_stream(stream)));
+  return FDM_OK;
+}
+
+// ---- matvec -----------------------------------------------------------------
+static int matvec_common(const void* d_W, const float* d_x, float* d_y, uint32_t out_dim,
+                         uint32_t in_dim, size_t w_align) {
+  if (int rc = check_ready()) return rc;
+  if (!d_W || !d_x || !d_y) return fail(FDM_E_INVAL, "null pointer");
+  if (in_dim == 0 || in_dim % FDM_QK_K || in_dim > 4u * FDM_HIDDEN)
+    return fail(FDM_E_INVAL, "in_dim=%u must be a positive multiple of 256 <= %d", in_dim,
+                4 * FDM_HIDDEN);
+  if (out_dim == 0 || out_dim > (1u << 24)) return fail(FDM_E_INVAL, "out_dim=%u", out_dim);
+  if (!aligned(d_W, w_align) || !aligned(d_x, 4) || !aligned(d_y, 4))
+    return fail(FDM_E_INVAL, "misaligned pointer (W needs %zu bytes)", w_align);
+  return FDM_OK;
+}
+
+int fdm_matvec_q4k(const void* d_W, const float* d_x, float* d_y, uint32_t out_dim,
+                   uint32_t in_dim, void* stream) {
+  if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 4)) return rc;
+  hipStream_t s = as_stream(stream);
+  FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
+  FDM_HIP(launch_matvec_q4k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
+                            (int)in_dim, s));
+  return FDM_OK;
+}
+
+int fdm_matvec_q6k(const void* d_W, const float* d_x, float* d_y, uint32_t out_dim,
+                   uint32_t in_dim, void* stream) {
+  if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 2)) return rc;
+  hipStream_t s = as_stream(stream);
+  FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
+  FDM_HIP(launch_matvec_q6k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
+                            (int)in_dim, s));
+  return FDM_OK;
+}
+
+// ---- one expert -----------------------------------------------------------
+int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, float* d_out,
+                   float* d_act, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_blob || !d_x || !d_out) return fail(FDM_E_INVAL, "null pointer");
+  bool q6 = false;
+  if (int rc = down_type(expert_size, &q6)) return rc;
+  if (!aligned(d_blob, 4) || !aligned(d_x, 16))
+    return fail(FDM_E_INVAL, "blob must be 4-byte and x 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  // the expert runs as the "shared" slot of a zero-routed-expert table
+  SlotTable t;
+  t.experts = nullptr;
+  t.expert_size = expert_size;
+  t.n_experts = 0;
+  t.shared = static_cast<const uint8_t*>(d_blob);
+  t.idx = nullptr;
+  t.w = nullptr;
+  t.K = 0;
+  t.n_slots = 1;
+  FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, g.ws.xd, s));
+  FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+  FDM_HIP(launch_down_combine(t, q6, g.ws.act_xd, nullptr, d_out, nullptr, s));
+  if (d_act)
+    FDM_HIP(hipMemcpyAsync(d_act, g.ws.act, FDM_MOE_FFN * sizeof(float),
+                           hipMemcpyDeviceToDevice, s));
+  return FDM_OK;
+}
+
+// ---- router -----------------------------------------------------------------
+int fdm_router_logits(const float* d_Wg, const float* d_x, int n_exp, int dim, int T,
+                      float* d_logits, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_Wg || !d_x || !d_logits) return fail(FDM_E_INVAL, "null pointer");
+  if (n_exp <= 0 || n_exp > 65535 || dim <= 0 || dim % 4 || T <= 0 || T > 65535 * 8)
+    return fail(FDM_E_INVAL, "n_exp=%d dim=%d T=%d", n_exp, dim, T);
+  if (!aligned(d_Wg, 16) || !aligned(d_x, 16))
+    return fail(FDM_E_INVAL, "Wg and x must be 16-byte aligned");
+  FDM_HIP(launch_router_logits(d_Wg, d_x, n_exp, dim, T, d_logits, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_route(const float* d_logits, const float* d_bias, int T, int K, int* d_idx, float* d_w,
+              void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_logits || !d_idx || !d_w) return fail(FDM_E_INVAL, "null pointer");
+  if (int rc = check_K(K)) return rc;
+  if (T <= 0 || T > (1 << 24)) return fail(FDM_E_INVAL, "T=%d", T);
+  FDM_HIP(launch_route(d_logits, d_bias, T, K, d_idx, d_w, as_stream(stream)));
+  return FDM_OK;
+}
+
+// ---- resident layers ------------------------------------------------------------
+int fdm_layer_attach(int L, const void* d_experts, size_t expert_size, int n_experts,
+                     const float* d_Wg, const float* d_bias, const void* d_shared) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (!d_experts || !d_Wg) return fail(FDM_E_INVAL, "null experts or router weights");
+  if (n_experts != FDM_N_EXPERTS)
+    return fail(FDM_E_INVAL, "n_experts=%d: the router is the R1 256-expert router", n_experts);
+  bool q6 = false;
+  if (int rc = down_type(expert_size, &q6)) return rc;
+  if (!aligned(d_experts, 16) || !aligned(d_Wg, 16) || (d_shared && !aligned(d_shared, 16)))
+    return fail(FDM_E_INVAL, "layer buffers must be 16-byte aligned");
+  release_layer(g.layers[L]);
+  Layer& y = g.layers[L];
+  y.resident = true;
+  y.owned = false;
+  y.experts = static_cast<const uint8_t*>(d_experts);
+  y.expert_size = expert_size;
+  y.n_experts = n_experts;
+  y.down_q6 = q6;
+  y.Wg = d_Wg;
+  y.bias = d_bias;
+  y.shared = static_cast<const uint8_t*>(d_shared);
+  return FDM_OK;
+}
+
+int fdm_layer_upload(int L, const void* h_experts, size_t expert_size, int n_experts,
+                     const float* h_Wg, const float* h_bias, const void* h_shared) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (!h_experts || !h_Wg) return fail(FDM_E_INVAL, "null experts or router weights");
+  if (n_experts != FDM_N_EXPERTS)
+    return fail(FDM_E_INVAL, "n_experts=%d: the router is the R1 256-expert router", n_experts);
+  bool q6 = false;
+  if (int rc = down_type(expert_size, &q6)) return rc;
+  const size_t eb = expert_size * (size_t)n_experts;
+  const size_t wb = (size_t)FDM_N_EXPERTS * FDM_HIDDEN * sizeof(float);
+  void *de = nullptr, *dw = nullptr, *db = nullptr, *ds = nullptr;
+  auto cleanup = [&]() {
+    if (de) (void)hipFree(de);
+    if (dw) (void)hipFree(dw);
+    if (db) (void)hipFree(db);
+    if (ds) (void)hipFree(ds);
+  };
+  if (hipMalloc(&de, eb) != hipSuccess || hipMalloc(&dw, wb) != hipSuccess ||
+      (h_bias && hipMalloc(&db, FDM_N_EXPERTS * sizeof(float)) != hipSuccess) ||
+      (h_shared && hipMalloc(&ds, expert_size) != hipSuccess)) {
+    cleanup();
+    return fail(FDM_E_NOMEM, "cannot allocate %zu bytes for layer %d", eb + wb + expert_size, L);
+  }
+  hipError_t e = hipMemcpy(de, h_experts, eb, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(dw, h_Wg, wb, hipMemcpyHostToDevice);
+  if (e == hipSuccess && h_bias)
+    e = hipMemcpy(db, h_bias, FDM_N_EXPERTS * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess && h_shared) e = hipMemcpy(ds, h_shared, expert_size, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    cleanup();
+    return hip_fail(e, "layer upload");
+  }
+  release_layer(g.layers[L]);
+  Layer& y = g.layers[L];
+  y.resident = true;
+  y.owned = true;
+  y.experts = static_cast<const uint8_t*>(de);
+  y.expert_size = expert_size;
+  y.n_experts = n_experts;
+  y.down_q6 = q6;
+  y.Wg = static_cast<const float*>(dw);
+  y.bias = static_cast<const float*>(db);
+  y.shared = static_cast<const uint8_t*>(ds);
+  return FDM_OK;
+}
+
+int fdm_layer_release(int L) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  (void)hipDeviceSynchronize();
+  release_layer(g.layers[L]);
+  return FDM_OK;
+}
+
+int fdm_layer_query(int L, size_t* expert_size, int* down_is_q6, int* n_experts) {
+  Layer* y = nullptr;
+  if (int rc = get_layer(L, &y)) return rc;
+  if (expert_size) *expert_size = y->expert_size;
+  if (down_is_q6) *down_is_q6 = y->down_q6 ? 1 : 0;
+  if (n_experts) *n_experts = y->n_experts;
+  return FDM_OK;
+}
+
+// ---- MoE ---------------------------------------------------------------------------
+int fdm_moe_forward(int L, const float* d_h_post, const int* d_idx, const float* d_w, int K,
+                    float* d_moe_out, void* stream) {
+  Layer* y = nullptr;
+  if (int rc = get_layer(L, &y)) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (!d_h_post || !d_idx || !d_w || !d_moe_out) return fail(FDM_E_INVAL, "null pointer");
+  hipStream_t s = as_stream(stream);
+  const SlotTable t = slots_for(*y, d_idx, d_w, K, false);
+  FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, g.ws.xd, s));
+  FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+  FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, nullptr, d_moe_out, nullptr, s));
+  return FDM_OK;
+}
+
+int fdm_moe_forward_host(int L, const float* h_post, const int* exp_idx, const float* exp_w,
+                         int K, float* moe_out) {
+  Layer* y = nullptr;
+  if (int rc = get_layer(L, &y)) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (!h_post || !exp_idx || !exp_w || !moe_out) return fail(FDM_E_INVAL, "null pointer");
+  Workspace& w = g.ws;
+  FDM_HIP(hipMemcpy(w.stage_x, h_post, FDM_HIDDEN * sizeof(float), hipMemcpyHostToDevice));
+  FDM_HIP(hipMemcpy(w.stage_idx, exp_idx, K * sizeof(int), hipMemcpyHostToDevice));
+  FDM_HIP(hipMemcpy(w.stage_w, exp_w, K * sizeof(float), hipMemcpyHostToDevice));
+  if (int rc = fdm_moe_forward(L, w.stage_x, w.stage_idx, w.stage_w, K, w.stage_y, nullptr))
+    return rc;
+  FDM_HIP(hipMemcpy(moe_out, w.stage_y, FDM_HIDDEN * sizeof(float), hipMemcpyDeviceToHost));
+  return FDM_OK;
+}
+
+int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, float* d_hidden,
+                  int* d_idx, float* d_w, void* stream) {
+  Layer* y = nullptr;
+  if (int rc = get_layer(L, &y)) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (!d_h_post || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(d_h_post, 16)) return fail(FDM_E_INVAL, "h_post must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  int* idx = d_idx ? d_idx : g.ws.idx;
+  float* w = d_w ? d_w : g.ws.w;
+  FDM_HIP(launch_router_layer(y->Wg, y->bias, d_h_post, K, g.ws.logits, g.ws.xd, idx, w,
+                              g.ws.counter, s));
+  const SlotTable t = slots_for(*y, idx, w, K, true);
+  FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+  FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, d_h_in, d_hidden, nullptr, s));
+  return FDM_OK;
+}
+
+// ---- synthetic data ------------------------------------------------------------------
+int fdm_synth_q4k(void* d_dst, size_t n_blocks, uint64_t seed, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_dst || !aligned(d_dst, 8)) return fail(FDM_E_INVAL, "destination must be 8-byte aligned");
+  if (n_blocks == 0) return FDM_OK;
+  FDM_HIP(launch_synth_q4k(static_cast<uint8_t*>(d_dst), n_blocks, seed, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_synth_q6k(void* d_dst, size_t n_blocks, uint64_t seed, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_dst || !aligned(d_dst, 8)) return fail(FDM_E_INVAL, "destination must be 8-byte aligned");
+  if (n_blocks == 0) return FDM_OK;
+  FDM_HIP(launch_synth_q6k(static_cast<uint8_t*>(d_dst), n_blocks, seed, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_synth_normal(float* d_dst, size_t n, float mean, float std_dev, uint64_t seed,
+                     void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_dst) return fail(FDM_E_INVAL, "null pointer");
+  if (n == 0) return FDM_OK;
+  FDM_HIP(launch_synth_normal(d_dst, n, mean, std_dev, seed, as_stream(stream)));
+  return FDM_OK;
+}
+
+}  // extern "C"

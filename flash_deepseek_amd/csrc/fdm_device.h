@@ -1,0 +1,274 @@
+// fdm_device.h -- device-side building blocks shared by the gfx950 kernels.
+//
+// Activation digits.  A matvec against K-quant weights does, per weight, a
+// nibble (or 6-bit) unpack and a multiply-accumulate.  Done in fp32 that is
+// ~2.4 VALU instructions per weight, which at 8 TB/s of 4.5-bit weights
+// would keep the vector ALUs of all 256 CUs almost fully busy.  Instead the
+// activation vector x is split once per 32-element sub-block j into two
+// int8 "digits":  x ~= s_j * (a + b / 254),  s_j = max|x| / 127, a = rint(x/s_j),
+// b = rint((x/s_j - a) * 254), so |x - x'| <= max|x| / 64516 (about 1.5e-5 of
+// the sub-block's largest element).  The weights' integer quants then meet
+// the digits in v_dot4_i32_i8 (four 8-bit products per instruction, exact
+// int32 sums), and the block scales are applied once per sub-block in fp32.
+// The sub-block sums sum_j x (exact fp32) carry the Q4_K min term.
+//
+// Digits of 64 consecutive elements live in one 144-byte record (XGroup),
+// matching one Q4_K "group" (32 qs bytes = sub-blocks 2g and 2g+1).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fdm {
+
+constexpr int kQK = 256;
+constexpr int kQ4KBlock = 144;
+constexpr int kQ6KBlock = 210;
+constexpr int kHidden = 7168;
+constexpr int kFfn = 2048;
+constexpr int kGateBytes = 57344 * kQ4KBlock;       // 8,257,536
+constexpr int kDownQ4KBytes = 57344 * kQ4KBlock;    // 8,257,536
+constexpr int kDownQ6KBytes = 57344 * kQ6KBlock;    // 12,042,240
+constexpr int kQ4KRowHidden = kHidden / kQK * kQ4KBlock;  // 4032 B: gate/up row
+constexpr int kQ4KRowFfn = kFfn / kQK * kQ4KBlock;        // 1152 B: down row (Q4_K)
+constexpr int kQ6KRowFfn = kFfn / kQK * kQ6KBlock;        // 1680 B: down row (Q6_K)
+
+struct __attribute__((aligned(16))) XGroup {
+  int8_t a[64];    // high digit of elements 0..63
+  int8_t b[64];    // low digit
+  float s[2];      // digit scale of sub-blocks 0 (elements 0-31) and 1 (32-63)
+  float xsum[2];   // exact fp32 sum of the 32 elements of each sub-block
+};
+static_assert(sizeof(XGroup) == 144, "XGroup must be 144 bytes");
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// 4-byte aligned 16-byte vector: legal dwordx4 access at any dword address.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Half bits -> float through the hardware converter (exact for every finite
+// half, subnormals included: f16 denormals are not flushed by default).
+__device__ __forceinline__ float half_to_float(uint32_t bits16) {
+  _Float16 h = __builtin_bit_cast(_Float16, (uint16_t)(bits16 & 0xFFFFu));
+  return (float)h;
+}
+
+// Half bits -> float by integer construction, bit-identical to quant.c:4-24
+// for every input including signalling-NaN payloads.
+__device__ __forceinline__ float half_bits_exact(uint32_t h) {
+  uint32_t sign = (h >> 15) << 31;
+  uint32_t e = (h >> 10) & 0x1Fu;
+  uint32_t f = h & 0x3FFu;
+  uint32_t bits;
+  if (e == 0x1Fu) {
+    bits = sign | 0x7F800000u | (f << 13);
+  } else if (e != 0) {
+    bits = sign | ((e + 112u) << 23) | (f << 13);
+  } else if (f == 0) {
+    bits = sign;
+  } else {
+    // leading one of the 10-bit fraction at bit p: value = f * 2^-24
+    uint32_t p = 31u - __builtin_clz(f);  // 0..9
+    uint32_t shift = 10u - p;
+    bits = sign | ((113u - shift) << 23) | (((f << shift) & 0x3FFu) << 13);
+  }
+  return __builtin_bit_cast(float, bits);
+}
+
+// 6-bit scale and min of sub-blocks 2g and 2g+1 of a Q4_K block
+// (quant.c:26-34).  s0/s1/s2 are the 12 scale bytes as three dwords.
+// Sub-blocks 0-3 (g < 2) keep scale/min in the low six bits of bytes 0-3 /
+// 4-7; sub-blocks 4-7 (g >= 2) take their low nibble from bytes 8-11 and
+// their top two bits from bits 6-7 of bytes 0-3 / 4-7.  Written without
+// branches: a lane's g is fixed, so the selectors below are per-lane
+// constants and every lane runs the same instructions.
+struct Q4KScaleSel {
+  bool lowg;        // g < 2
+  uint32_t width;   // 6 or 4 bits taken from the "low" source
+  uint32_t off_sc;  // bit offset of sc_lo in its source (sc_hi: +8)
+  uint32_t off_m;   // bit offset of m_lo in its source (m_hi: +8)
+  uint32_t sh;      // 16 * (g & 1)
+  uint32_t hmask;   // 0x30 when the top two bits come from bytes 0-7
+};
+
+__device__ __forceinline__ Q4KScaleSel q4k_scale_sel(int g) {
+  Q4KScaleSel t;
+  t.lowg = g < 2;
+  t.sh = (uint32_t)(g & 1) * 16u;
+  t.width = t.lowg ? 6u : 4u;
+  t.off_sc = t.sh;
+  t.off_m = t.lowg ? t.sh : t.sh + 4u;
+  t.hmask = t.lowg ? 0u : 0x30u;
+  return t;
+}
+
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2,
+                                                   const Q4KScaleSel& t, int& sc_lo, int& m_lo,
+                                                   int& sc_hi, int& m_hi) {
+  const uint32_t A = t.lowg ? s0 : s2;
+  const uint32_t B = t.lowg ? s1 : s2;
+  sc_lo = (int)(__builtin_amdgcn_ubfe(A, t.off_sc, t.width) | ((s0 >> (t.sh + 2u)) & t.hmask));
+  m_lo = (int)(__builtin_amdgcn_ubfe(B, t.off_m, t.width) | ((s1 >> (t.sh + 2u)) & t.hmask));
+  sc_hi = (int)(__builtin_amdgcn_ubfe(A, t.off_sc + 8u, t.width) | ((s0 >> (t.sh + 10u)) & t.hmask));
+  m_hi = (int)(__builtin_amdgcn_ubfe(B, t.off_m + 8u, t.width) | ((s1 >> (t.sh + 10u)) & t.hmask));
+}
+
+__device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uint32_t s2, int g,
+                                                   int& sc_lo, int& m_lo, int& sc_hi,
+                                                   int& m_hi) {
+  q4k_scale_min_pair(s0, s1, s2, q4k_scale_sel(g), sc_lo, m_lo, sc_hi, m_hi);
+}
+
+// Dot product of one Q4_K group (qs bytes 32g..32g+31 of a block, i.e.
+// elements 64g..64g+63) with the digits of the matching 64 activations.
+//   hdr = first 16 bytes of the block: d | dmin | scales[0..11]
+//   q0, q1 = the group's 32 qs bytes
+// Returns sum over the 64 elements of (d*sc*q - dmin*m) * x.
+__device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, const u32x4 q1,
+                                               const Q4KScaleSel& sel,
+                                               const XGroup* __restrict__ xg) {
+  const i32x4* av = reinterpret_cast<const i32x4*>(xg->a);
+  const i32x4* bv = reinterpret_cast<const i32x4*>(xg->b);
+  const i32x4 a0 = av[0], a1 = av[1], a2 = av[2], a3 = av[3];
+  const i32x4 b0 = bv[0], b1 = bv[1], b2 = bv[2], b3 = bv[3];
+  const f32x4 meta = *reinterpret_cast<const f32x4*>(xg->s);
+  const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  const uint32_t alo[8] = {(uint32_t)a0.x, (uint32_t)a0.y, (uint32_t)a0.z, (uint32_t)a0.w,
+                           (uint32_t)a1.x, (uint32_t)a1.y, (uint32_t)a1.z, (uint32_t)a1.w};
+  const uint32_t ahi[8] = {(uint32_t)a2.x, (uint32_t)a2.y, (uint32_t)a2.z, (uint32_t)a2.w,
+                           (uint32_t)a3.x, (uint32_t)a3.y, (uint32_t)a3.z, (uint32_t)a3.w};
+  const uint32_t blo[8] = {(uint32_t)b0.x, (uint32_t)b0.y, (uint32_t)b0.z, (uint32_t)b0.w,
+                           (uint32_t)b1.x, (uint32_t)b1.y, (uint32_t)b1.z, (uint32_t)b1.w};
+  const uint32_t bhi[8] = {(uint32_t)b2.x, (uint32_t)b2.y, (uint32_t)b2.z, (uint32_t)b2.w,
+                           (uint32_t)b3.x, (uint32_t)b3.y, (uint32_t)b3.z, (uint32_t)b3.w};
+  int A0 = 0, B0 = 0, A1 = 0, B1 = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = w[i] & 0x0F0F0F0Fu;
+    const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+    A0 = sdot4(lo, alo[i], A0);
+    B0 = sdot4(lo, blo[i], B0);
+    A1 = sdot4(hi, ahi[i], A1);
+    B1 = sdot4(hi, bhi[i], B1);
+  }
+  int sc0, m0, sc1, m1;
+  q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, sel, sc0, m0, sc1, m1);
+  const float d = half_to_float(hdr.x);
+  const float dmin = half_to_float(hdr.x >> 16);
+  const float k254 = 1.0f / 254.0f;
+  const float f0 = meta.x * fmaf((float)B0, k254, (float)A0);
+  const float f1 = meta.y * fmaf((float)B1, k254, (float)A1);
+  const float qx = fmaf((float)sc0, f0, (float)sc1 * f1);
+  const float mx = fmaf((float)m0, meta.z, (float)m1 * meta.w);
+  return fmaf(d, qx, -dmin * mx);
+}
+
+// funnel: the 4 bytes starting `byte_shift` (0..3) bytes into the 8-byte
+// little-endian pair (lo, hi).
+__device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t byte_shift) {
+  return __builtin_amdgcn_alignbyte(hi, lo, byte_shift);
+}
+
+// Dot product of one 128-element half of a Q6_K block (quant.c:63-92) with
+// the digits of its activations.  The half's bytes are passed already
+// realigned: ql[16] (64 bytes), qh[8] (32 bytes), sc[2] (8 int8 scales).
+// x0 covers elements 0..63 of the half, x1 elements 64..127.
+// Returns sum over the 128 elements of d*sc*(q-32) * x, without the d.
+__device__ __forceinline__ float q6k_half_dot(const uint32_t* ql, const uint32_t* qh,
+                                              const uint32_t* sc, const XGroup* __restrict__ x0,
+                                              const XGroup* __restrict__ x1) {
+  const uint32_t* a0 = reinterpret_cast<const uint32_t*>(x0->a);
+  const uint32_t* b0 = reinterpret_cast<const uint32_t*>(x0->b);
+  const uint32_t* a1 = reinterpret_cast<const uint32_t*>(x1->a);
+  const uint32_t* b1 = reinterpret_cast<const uint32_t*>(x1->b);
+  // acc[quarter][scale half]: quarter k covers elements 32k..32k+31 of the
+  // half (k = 0..3); scale half = l / 16.
+  int A[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+  int B[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int s = i >> 2;
+    const uint32_t wl = ql[i], wl2 = ql[8 + i], wh = qh[i];
+    // Each byte becomes 4*(q-32) as int8: the 6-bit q sits in bits 2..7 and
+    // flipping bit 7 subtracts 128.
+    const uint32_t v0 = (((wl & 0x0F0F0F0Fu) << 2) | ((wh & 0x03030303u) << 6)) ^ 0x80808080u;
+    const uint32_t v1 = (((wl2 & 0x0F0F0F0Fu) << 2) | ((wh & 0x0C0C0C0Cu) << 4)) ^ 0x80808080u;
+    const uint32_t v2 = (((wl >> 2) & 0x3C3C3C3Cu) | ((wh & 0x30303030u) << 2)) ^ 0x80808080u;
+    const uint32_t v3 = (((wl2 >> 2) & 0x3C3C3C3Cu) | (wh & 0xC0C0C0C0u)) ^ 0x80808080u;
+    A[0][s] = sdot4(v0, a0[i], A[0][s]);
+    B[0][s] = sdot4(v0, b0[i], B[0][s]);
+    A[1][s] = sdot4(v1, a0[8 + i], A[1][s]);
+    B[1][s] = sdot4(v1, b0[8 + i], B[1][s]);
+    A[2][s] = sdot4(v2, a1[i], A[2][s]);
+    B[2][s] = sdot4(v2, b1[i], B[2][s]);
+    A[3][s] = sdot4(v3, a1[8 + i], A[3][s]);
+    B[3][s] = sdot4(v3, b1[8 + i], B[3][s]);
+  }
+  const float k254 = 1.0f / 254.0f;
+  const float xs[4] = {x0->s[0], x0->s[1], x1->s[0], x1->s[1]};
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    // scales sc[2k + s]: byte (2k + s) of the 8 scale bytes, as int8
+    const uint32_t word = sc[k >> 1];
+    const int sh = (k & 1) * 16;
+    const int sa = (int)(int8_t)((word >> sh) & 0xFF);
+    const int sb = (int)(int8_t)((word >> (sh + 8)) & 0xFF);
+    const int ia = sa * A[k][0] + sb * A[k][1];
+    const int ib = sa * B[k][0] + sb * B[k][1];
+    acc = fmaf(xs[k], fmaf((float)ib, k254, (float)ia), acc);
+  }
+  return acc * 0.25f;
+}
+
+// Sum over the 16 lanes of a row group (lanes 16r..16r+15); every lane of
+// the group receives the total.
+__device__ __forceinline__ float sum16(float v) {
+  v += __shfl_xor(v, 8);
+  v += __shfl_xor(v, 4);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 1);
+  return v;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+// Digits of the 32 elements of one sub-block.  Called by all 32 lanes of a
+// half-wave (lane index `l` 0..31 within it), each holding one element v.
+// Returns a / b digits for the lane and the sub-block's scale and exact sum.
+__device__ __forceinline__ void make_digits32(float v, int8_t& a_out, int8_t& b_out,
+                                              float& s_out, float& sum_out) {
+  float amax = fabsf(v);
+  float sum = v;
+#pragma unroll
+  for (int m = 16; m >= 1; m >>= 1) {
+    amax = fmaxf(amax, __shfl_xor(amax, m, 32));
+    sum += __shfl_xor(sum, m, 32);
+  }
+  int a = 0, b = 0;
+  float s;
+  if (amax > 0.0f && amax <= 3.4028234e38f) {
+    const float inv = 127.0f / amax;
+    s = amax / 127.0f;
+    const float t = v * inv;
+    float ra = rintf(t);
+    ra = fminf(fmaxf(ra, -127.0f), 127.0f);
+    const float rb = fminf(fmaxf(rintf((t - ra) * 254.0f), -127.0f), 127.0f);
+    a = (int)ra;
+    b = (int)rb;
+  } else {
+    // all zero: s = 0 gives exact zeros; inf/NaN: propagate a NaN scale
+    s = (amax == 0.0f) ? 0.0f : __builtin_nanf("");
+  }
+  a_out = (int8_t)a;
+  b_out = (int8_t)b;
+  s_out = s;
+  sum_out = sum;
+}
+
+}  // namespace fdm

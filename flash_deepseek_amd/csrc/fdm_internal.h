@@ -1,0 +1,69 @@
+// fdm_internal.h -- launchers shared between the kernel translation units
+// and the C ABI (capi.hip).  All launchers are asynchronous on `stream` and
+// return the hipError_t of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "fdm_device.h"
+
+namespace fdm {
+
+// quant_kernels.hip
+hipError_t launch_fp16_to_fp32(const uint16_t* src, float* dst, size_t n, hipStream_t s);
+hipError_t launch_dequant_q4k(const uint8_t* src, float* dst, size_t n_blocks, hipStream_t s);
+hipError_t launch_dequant_q6k(const uint8_t* src, float* dst, size_t n_blocks, hipStream_t s);
+
+// matvec_kernels.hip
+// Digits of `n_groups` consecutive 64-element groups of x.
+hipError_t launch_xdigits(const float* x, size_t n_groups, XGroup* xd, hipStream_t s);
+hipError_t launch_matvec_q4k(const uint8_t* W, const XGroup* xd, float* y, int rows,
+                             int in_dim, hipStream_t s);
+hipError_t launch_matvec_q6k(const uint8_t* W, const XGroup* xd, float* y, int rows,
+                             int in_dim, hipStream_t s);
+
+// router_kernels.hip
+hipError_t launch_router_logits(const float* Wg, const float* x, int n_exp, int dim, int T,
+                                float* logits, hipStream_t s);
+hipError_t launch_route(const float* logits, const float* bias, int T, int K, int* idx,
+                        float* w, hipStream_t s);
+// Batch-1 layer front end: logits of the 256 R1 experts for h_post, the
+// digits of h_post (xd, 112 groups) and, in the last workgroup to finish,
+// route() into idx/w.  `counter` must be zero on entry; it is left zero.
+hipError_t launch_router_layer(const float* Wg, const float* bias, const float* h_post, int K,
+                               float* logits, XGroup* xd, int* idx, float* w, int* counter,
+                               hipStream_t s);
+
+// moe_kernels.hip
+struct SlotTable {
+  const uint8_t* experts;  // n_experts packed blobs
+  size_t expert_size;
+  int n_experts;
+  const uint8_t* shared;   // slot K (may be null)
+  const int* idx;          // K routed expert ids (device)
+  const float* w;          // K routing weights (device)
+  int K;                   // routed slots
+  int n_slots;             // K or K + 1 (shared)
+};
+// gate/up matvecs + SwiGLU for every slot; writes act[slot][2048] and the
+// digits of act (act_xd[slot][32]).
+hipError_t launch_gateup(const SlotTable& t, const XGroup* xd, float* act, XGroup* act_xd,
+                         hipStream_t s);
+// down matvecs for every slot and the combine:
+//   out[i] = (h_in[i] + sum_{k<K} w[k] * E_k[i]) + S[i]
+// moe_out (optional) receives sum_k w[k] * E_k[i].
+hipError_t launch_down_combine(const SlotTable& t, bool down_q6, const XGroup* act_xd,
+                               const float* h_in, float* out, float* moe_out, hipStream_t s);
+
+// synth_kernels.hip
+hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);
+hipError_t launch_synth_q6k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);
+hipError_t launch_synth_normal(float* dst, size_t n, float mean, float std_dev, uint64_t seed,
+                               hipStream_t s);
+
+// grid sizing: number of CUs of the current device (set by fdm_init)
+extern int g_num_cus;
+
+}  // namespace fdm

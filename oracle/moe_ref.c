@@ -1,0 +1,327 @@
+/*
+ * moe_ref.c -- CPU restatement of the reference's MoE expert path: router
+ * logits, route(), the expert FFN and the combine.  TEST INFRASTRUCTURE
+ * ONLY (the checker); the shipped library never calls it.
+ *
+ * Numerics.
+ *  - Expert outputs are computed in double from the bit-exact dequantised
+ *    weights and rounded to float once: that is the truth the kernels are
+ *    held to (1e-3 relative L2).  The single-precision column-order matvec
+ *    the reference runs (cblas_sgemv, infer.m:1081-1090) is provided
+ *    separately (orc_matvec_*_f32) for the CPU baseline.
+ *  - Router logits use one fixed summation order, shared with the HIP
+ *    router kernel, so both sides produce the same bits and routing can be
+ *    compared exactly.  The reference's cblas_sgemv order is unspecified
+ *    (Accelerate is closed), so any fixed order is an equally faithful
+ *    restatement of infer.m:350-353.
+ *  - sigmoidf is the reference's formula 1.0f/(1.0f+expf(-x)) (infer.m:376)
+ *    with expf evaluated by orc_expf: exp in double from fma/mul/add only,
+ *    rounded once to float, i.e. the correctly rounded expf except when the
+ *    exact value lies within ~1e-16 relative of a rounding boundary.  The
+ *    HIP router evaluates the identical sequence of IEEE operations.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------- */
+/* Deterministic exp.  exp(x) = 2^k * e^r, k = floor(x/ln2 + 1/2),
+ * r = x - k ln2 (two-constant Cody-Waite reduction with fma), e^r by its
+ * Taylor series to r^13 (|r| <= 0.347: truncation < 5e-18) in Horner form. */
+static double exp_det(double x) {
+    if (x != x) return x;
+    if (x > 709.0) return INFINITY;
+    if (x < -746.0) return 0.0;
+    const double inv_ln2 = 1.4426950408889634;
+    const double ln2_hi = 0x1.62e42fefa39efp-1;
+    const double ln2_lo = 0x1.abc9e3b39803fp-56;
+    double t = x * inv_ln2;
+    double k = floor(t + 0.5);
+    double r = fma(-k, ln2_hi, x);
+    r = fma(-k, ln2_lo, r);
+    static const double inv_fact[14] = {
+        1.0, 1.0, 1.0 / 2, 1.0 / 6, 1.0 / 24, 1.0 / 120, 1.0 / 720, 1.0 / 5040,
+        1.0 / 40320, 1.0 / 362880, 1.0 / 3628800, 1.0 / 39916800, 1.0 / 479001600,
+        1.0 / 6227020800.0};
+    double p = inv_fact[13];
+    for (int i = 12; i >= 0; --i) p = fma(p, r, inv_fact[i]);
+    return ldexp(p, (int)k);
+}
+
+float orc_expf(float x) { return (float)exp_det((double)x); }
+
+/* infer.m:376 */
+float orc_sigmoidf(float x) { return 1.0f / (1.0f + orc_expf(-x)); }
+
+/* infer.m:378-383 */
+void orc_silu_mul(const float *g, const float *u, float *o, int d) {
+    for (int i = 0; i < d; ++i) {
+        const float v = g[i];
+        o[i] = (v / (1.0f + orc_expf(-v))) * u[i];
+    }
+}
+
+/* infer.m:369-374: inv = 1/sqrt(ss/d + eps); o = x * inv * w. */
+void orc_rms_norm(const float *x, const float *w, float *o, int d) {
+    float ss = 0.0f;
+    for (int i = 0; i < d; ++i) ss += x[i] * x[i];
+    const float inv = 1.0f / sqrtf(ss / (float)d + ORC_RMS_EPS);
+    for (int i = 0; i < d; ++i) o[i] = w ? x[i] * inv * w[i] : x[i] * inv;
+}
+
+/* ---------------------------------------------------------------------- */
+/* Matvec oracles: bit-exact dequant of one row at a time, then a dot. */
+typedef void (*deq_fn)(const void *, float *, size_t);
+
+static void matvec_generic(deq_fn deq, size_t row_bytes, const void *W, const float *x,
+                           float *y, int rows, int cols, int f32_order) {
+    float *row = (float *)malloc(sizeof(float) * (size_t)cols);
+    const uint8_t *w = (const uint8_t *)W;
+    for (int r = 0; r < rows; ++r) {
+        deq(w + (size_t)r * row_bytes, row, (size_t)cols);
+        if (f32_order) {
+            float acc = 0.0f;
+            for (int c = 0; c < cols; ++c) acc += row[c] * x[c];
+            y[r] = acc;
+        } else {
+            double acc = 0.0;
+            for (int c = 0; c < cols; ++c) acc += (double)row[c] * (double)x[c];
+            y[r] = (float)acc;
+        }
+    }
+    free(row);
+}
+
+void orc_matvec_q4k(const void *W, const float *x, float *y, int rows, int cols) {
+    matvec_generic(orc_dequantize_row_q4_K, (size_t)cols / ORC_QK_K * ORC_Q4K_BLOCK, W, x, y,
+                   rows, cols, 0);
+}
+void orc_matvec_q6k(const void *W, const float *x, float *y, int rows, int cols) {
+    matvec_generic(orc_dequantize_row_q6_K, (size_t)cols / ORC_QK_K * ORC_Q6K_BLOCK, W, x, y,
+                   rows, cols, 0);
+}
+void orc_matvec_q4k_f32(const void *W, const float *x, float *y, int rows, int cols) {
+    matvec_generic(orc_dequantize_row_q4_K, (size_t)cols / ORC_QK_K * ORC_Q4K_BLOCK, W, x, y,
+                   rows, cols, 1);
+}
+void orc_matvec_q6k_f32(const void *W, const float *x, float *y, int rows, int cols) {
+    matvec_generic(orc_dequantize_row_q6_K, (size_t)cols / ORC_QK_K * ORC_Q6K_BLOCK, W, x, y,
+                   rows, cols, 1);
+}
+
+/* Double-precision matvec over a dequantised row stream (internal). */
+static void matvec_d(deq_fn deq, size_t row_bytes, const void *W, const double *x, double *y,
+                     int rows, int cols) {
+    float *row = (float *)malloc(sizeof(float) * (size_t)cols);
+    const uint8_t *w = (const uint8_t *)W;
+    for (int r = 0; r < rows; ++r) {
+        deq(w + (size_t)r * row_bytes, row, (size_t)cols);
+        double acc = 0.0;
+        for (int c = 0; c < cols; ++c) acc += (double)row[c] * x[c];
+        y[r] = acc;
+    }
+    free(row);
+}
+
+/* infer.m:1069-1091 (expert_worker): gate = Wg.x, up = Wu.x,
+ * act = silu(gate) * up, out = Wd.act; blob offsets infer.m:71-78. */
+void orc_expert_ffn(const void *blob, int down_is_q6, const float *x, float *out,
+                    float *gate_out, float *up_out, float *act_out) {
+    const int H = ORC_HIDDEN, F = ORC_FFN;
+    const uint8_t *b = (const uint8_t *)blob;
+    const size_t q4_row_h = (size_t)H / ORC_QK_K * ORC_Q4K_BLOCK;
+    double *xd = (double *)malloc(sizeof(double) * H);
+    double *g = (double *)malloc(sizeof(double) * F);
+    double *u = (double *)malloc(sizeof(double) * F);
+    double *a = (double *)malloc(sizeof(double) * F);
+    double *o = (double *)malloc(sizeof(double) * H);
+    for (int i = 0; i < H; ++i) xd[i] = x[i];
+    matvec_d(orc_dequantize_row_q4_K, q4_row_h, b, xd, g, F, H);
+    matvec_d(orc_dequantize_row_q4_K, q4_row_h, b + ORC_GATE_BYTES, xd, u, F, H);
+    for (int i = 0; i < F; ++i) a[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
+    if (down_is_q6)
+        matvec_d(orc_dequantize_row_q6_K, (size_t)F / ORC_QK_K * ORC_Q6K_BLOCK,
+                 b + 2 * ORC_GATE_BYTES, a, o, H, F);
+    else
+        matvec_d(orc_dequantize_row_q4_K, (size_t)F / ORC_QK_K * ORC_Q4K_BLOCK,
+                 b + 2 * ORC_GATE_BYTES, a, o, H, F);
+    for (int i = 0; i < H; ++i) out[i] = (float)o[i];
+    for (int i = 0; i < F; ++i) {
+        if (gate_out) gate_out[i] = (float)g[i];
+        if (up_out) up_out[i] = (float)u[i];
+        if (act_out) act_out[i] = (float)a[i];
+    }
+    free(xd);
+    free(g);
+    free(u);
+    free(a);
+    free(o);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Router logits, canonical order.  For output row e, 256 partial sums are
+ * formed: partial t accumulates, with one fmaf per element, the float4
+ * chunks c = t, t+256, t+512, ... (c indexes groups of 4 consecutive
+ * columns), components in order.  The 256 partials are split into four
+ * runs of 64; each run is reduced by an xor butterfly (v[l] += v[l ^ m] for
+ * m = 32,16,8,4,2,1, all l at once) and the four results are combined as
+ * (s0 + s1) + (s2 + s3).  The HIP router kernel computes exactly this. */
+void orc_router_logits(const float *Wg, const float *x, float *logits, int n_exp, int dim) {
+    const int n4 = dim / 4;
+    for (int e = 0; e < n_exp; ++e) {
+        const float *w = Wg + (size_t)e * dim;
+        float part[256];
+        for (int t = 0; t < 256; ++t) {
+            float acc = 0.0f;
+            for (int c = t; c < n4; c += 256)
+                for (int q = 0; q < 4; ++q) acc = fmaf(w[4 * c + q], x[4 * c + q], acc);
+            part[t] = acc;
+        }
+        float s[4];
+        for (int run = 0; run < 4; ++run) {
+            float v[64], nv[64];
+            memcpy(v, part + 64 * run, sizeof v);
+            for (int m = 32; m >= 1; m >>= 1) {
+                for (int l = 0; l < 64; ++l) nv[l] = v[l] + v[l ^ m];
+                memcpy(v, nv, sizeof v);
+            }
+            s[run] = v[0];
+        }
+        logits[e] = (s[0] + s[1]) + (s[2] + s[3]);
+    }
+}
+
+/* infer.m:920-991, DeepSeek-V3 noaux_tc routing:
+ *   score = sigmoid(logit) (weights), choice = score + bias (selection);
+ *   group score = sum of the top two choices in the group (running top-2
+ *   from -1e30, strict >); the top `topk_group` groups are taken by repeated
+ *   strict-> argmax passes (lowest index wins a tie); other groups are
+ *   masked to -1e30; the top K are picked by one pass over the experts in
+ *   index order that replaces the first minimum slot when strictly greater;
+ *   weights are the unbiased scores of the picks, summed in slot order and
+ *   scaled by scale/sum when the sum is positive.
+ * One deviation: where every remaining group score is <= -1e30 (all
+ * choices NaN or -inf), the reference stores group -1 and then indexes out
+ * of bounds; here such a group is skipped. */
+void orc_route_ex(const float *logits, const float *bias, int n_exp, int n_group,
+                  int topk_group, int K, float scale, int *exp_idx, float *exp_w) {
+    float score[1024], choice[1024], masked[1024];
+    const int per = n_exp / n_group;
+    for (int i = 0; i < n_exp; ++i) {
+        score[i] = orc_sigmoidf(logits[i]);
+        choice[i] = score[i] + (bias ? bias[i] : 0.0f);
+    }
+    float gscore[64];
+    for (int g = 0; g < n_group; ++g) {
+        float t1 = -1e30f, t2 = -1e30f;
+        for (int e = 0; e < per; ++e) {
+            const float s = choice[g * per + e];
+            if (s > t1) {
+                t2 = t1;
+                t1 = s;
+            } else if (s > t2) {
+                t2 = s;
+            }
+        }
+        gscore[g] = t1 + t2;
+    }
+    int chosen[64];
+    for (int k = 0; k < topk_group; ++k) {
+        int best = -1;
+        float bs = -1e30f;
+        for (int g = 0; g < n_group; ++g) {
+            int taken = 0;
+            for (int j = 0; j < k; ++j) taken |= (chosen[j] == g);
+            if (!taken && gscore[g] > bs) {
+                bs = gscore[g];
+                best = g;
+            }
+        }
+        chosen[k] = best;
+    }
+    for (int i = 0; i < n_exp; ++i) masked[i] = -1e30f;
+    for (int k = 0; k < topk_group; ++k) {
+        const int g = chosen[k];
+        if (g < 0) continue;
+        for (int e = 0; e < per; ++e) masked[g * per + e] = choice[g * per + e];
+    }
+    float key[ORC_MAX_K];
+    for (int k = 0; k < K; ++k) {
+        key[k] = -1e30f;
+        exp_idx[k] = 0;
+    }
+    for (int i = 0; i < n_exp; ++i) {
+        int slot = 0;
+        for (int k = 1; k < K; ++k)
+            if (key[k] < key[slot]) slot = k;
+        if (masked[i] > key[slot]) {
+            key[slot] = masked[i];
+            exp_idx[slot] = i;
+        }
+    }
+    for (int k = 0; k < K; ++k) exp_w[k] = score[exp_idx[k]];
+    float sum = 0.0f;
+    for (int k = 0; k < K; ++k) sum += exp_w[k];
+    if (sum > 0.0f) {
+        const float f = scale / sum;
+        for (int k = 0; k < K; ++k) exp_w[k] *= f;
+    }
+}
+
+void orc_route(const float *logits, const float *bias, int K, int *exp_idx, float *exp_w) {
+    orc_route_ex(logits, bias, ORC_N_EXPERTS, ORC_N_GROUP, ORC_TOPK_GROUP, K, ORC_ROUTED_SCALE,
+                 exp_idx, exp_w);
+}
+
+/* ---------------------------------------------------------------------- */
+static int down_is_q6_for(size_t expert_size) {
+    return expert_size == 2 * ORC_GATE_BYTES + ORC_DOWN_Q6K_BYTES;
+}
+
+/* metal_moe_forward, infer.m:1604-1700: moe_out = 0, then moe_out +=
+ * w[k] * E_k for k = 0..K-1 (the saxpy loop at infer.m:1690-1695). */
+void orc_moe_forward(const void *experts, size_t expert_size, const float *h_post,
+                     const int *exp_idx, const float *exp_w, int K, float *moe_out) {
+    const int q6 = down_is_q6_for(expert_size);
+    float *eo = (float *)malloc(sizeof(float) * ORC_HIDDEN);
+    for (int i = 0; i < ORC_HIDDEN; ++i) moe_out[i] = 0.0f;
+    for (int k = 0; k < K; ++k) {
+        const uint8_t *blob = (const uint8_t *)experts + (size_t)exp_idx[k] * expert_size;
+        orc_expert_ffn(blob, q6, h_post, eo, NULL, NULL, NULL);
+        for (int i = 0; i < ORC_HIDDEN; ++i) moe_out[i] = fmaf(exp_w[k], eo[i], moe_out[i]);
+    }
+    free(eo);
+}
+
+/* The MoE branch of layer_forward, infer.m:1878-1922. */
+void orc_moe_layer(const void *experts, size_t expert_size, const float *Wg, const float *bias,
+                   const void *shared_blob, const float *h_post, const float *h_in, int K,
+                   float *hidden_out, int *idx_out, float *w_out, float *moe_out,
+                   float *shared_out) {
+    float logits[ORC_N_EXPERTS];
+    int idx[ORC_MAX_K];
+    float w[ORC_MAX_K];
+    orc_router_logits(Wg, h_post, logits, ORC_N_EXPERTS, ORC_HIDDEN);
+    orc_route(logits, bias, K, idx, w);
+    float *moe = (float *)malloc(sizeof(float) * ORC_HIDDEN);
+    float *sd = (float *)malloc(sizeof(float) * ORC_HIDDEN);
+    orc_moe_forward(experts, expert_size, h_post, idx, w, K, moe);
+    if (shared_blob)
+        orc_expert_ffn(shared_blob, down_is_q6_for(expert_size), h_post, sd, NULL, NULL, NULL);
+    else
+        memset(sd, 0, sizeof(float) * ORC_HIDDEN);
+    for (int i = 0; i < ORC_HIDDEN; ++i) {
+        const float hin = h_in ? h_in[i] : 0.0f;
+        if (hidden_out) hidden_out[i] = hin + moe[i] + sd[i];
+        if (moe_out) moe_out[i] = moe[i];
+        if (shared_out) shared_out[i] = sd[i];
+    }
+    for (int k = 0; k < K; ++k) {
+        if (idx_out) idx_out[k] = idx[k];
+        if (w_out) w_out[k] = w[k];
+    }
+    free(moe);
+    free(sd);
+}
