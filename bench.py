@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Batch-1 decode through a full DeepSeek-R1-shape MoE layer on one MI355X.
+
+One step = one token through the MoE branch of a layer (router logits ->
+route -> 8 routed experts + 1 shared expert -> combine -> residual), via
+the library's C ABI (fdm_moe_layer).  Every step uses a different seeded
+token and the next of `--layers` resident layers (round robin), so the
+256 MB Infinity Cache cannot serve the weights: each step streams its
+experts from HBM.  All inputs are already resident when timing starts.
+
+Prints one JSON line (rank 0):
+  value        microseconds per token (lower is better)
+  layer_gbps   algorithmic bytes per token / time per token
+  roofline     the dominant kernel (gate/up + SwiGLU over the 9 experts),
+               timed live with HIP events on the launch stream
+  cpu_baseline the reference's CPU expert path (C restatement) on this
+               host's cores, on a bounded sample of the same workload
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "Q4_K MoE layer µs/token (batch 1) + achieved HBM GB/s as % of ~8 TB/s peak"
+HBM_PEAK_GBPS = 8000.0
+
+# Algorithmic bytes (weights actually required + fp32 activations in/out).
+GATE_BYTES = 57344 * 144                     # one Q4_K 2048 x 7168 matrix
+DOWN_BYTES = {"q4k": 57344 * 144, "q6k": 57344 * 210}
+ROUTER_BYTES = 256 * 7168 * 4 + 256 * 4      # W_g + bias
+HIDDEN, FFN = 7168, 2048
+
+
+def layer_bytes(down, K=8):
+    slots = K + 1
+    weights = slots * (2 * GATE_BYTES + DOWN_BYTES[down]) + ROUTER_BYTES
+    acts = HIDDEN * 4 * 3  # h_post, h_in in; hidden out
+    return weights + acts
+
+
+def gateup_bytes(K=8):
+    slots = K + 1
+    return slots * 2 * GATE_BYTES + HIDDEN * 4 + slots * FFN * 4  # W + x in + act out
+
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch measured by rocprofv3 counters (profiles/)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel, {}).get(workload)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(down, seconds, K=8):
+    """Median us/token of the reference-shaped CPU path on a bounded sample."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+    q6 = down == "q6k"
+    blobs = [O.synth_expert(900 + i, down_is_q6=q6) for i in range(K + 1)]
+    Wg = O.synth_normal(256 * HIDDEN, 0.0, 0.01, 901).reshape(256, HIDDEN)
+    bias = O.synth_normal(256, 0.0, 0.1, 902)
+    x = O.synth_normal(HIDDEN, 0.0, 1.0, 903)
+    h_in = O.synth_normal(HIDDEN, 0.0, 1.0, 904)
+    t0 = time.perf_counter()
+    first, _ = O.cpu_layer_baseline(blobs, q6, Wg, bias, x, h_in, 2)
+    per = max(time.perf_counter() - t0, 1e-3) / 2
+    reps = int(max(3, min(200, seconds / per)))
+    us, _ = O.cpu_layer_baseline(blobs, q6, Wg, bias, x, h_in, reps)
+    return {
+        "value": round(us, 1),
+        "unit": "us/token",
+        "cores": K + 1,
+        "kind": "port",
+        "sample": (f"{reps} tokens through one R1 MoE layer on the host: router sgemv + "
+                   f"route() + {K} routed and 1 shared expert, each dequantised to fp32 and "
+                   f"run as 3 sgemv + SiLU*mul on its own thread (infer.m:1878-1922, "
+                   f"USE_CPU_EXPERTS), {down.upper()} down; median per token; "
+                   f"{os.cpu_count()} host CPUs visible"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--layers", type=int, default=12, help="resident layers rotated per step")
+    ap.add_argument("--down", choices=["q4k", "q6k"], default="q4k")
+    ap.add_argument("--prof-steps", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on exactly one GPU (asked for {max(args.gpus, world)}): this "
+              "build measures the hot path on one MI355X; multi-GPU sharding is a design "
+              "note, not a measured configuration.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, ROOT)
+    import flash_deepseek_amd as F
+    from flash_deepseek_amd.synthetic import make_layer, make_tokens
+
+    K = 8
+    F.init(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    layers = []
+    for l in range(args.layers):
+        lay = make_layer(1 + l, down_q6=(args.down == "q6k"))
+        F.attach_layer(3 + l, lay.experts, lay.expert_size, lay.Wg, lay.bias, lay.shared)
+        layers.append(lay)
+    n_tok = args.warmup + max(args.steps, args.prof_steps)
+    h_post = make_tokens(n_tok, 7001)
+    h_in = make_tokens(n_tok, 7002)
+    out = torch.empty((n_tok, HIDDEN), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i):
+        F.moe_layer(3 + i % args.layers, h_post[i], h_in[i], K, out[i], stream=stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, args.warmup + args.steps):
+        step(i)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    us_per_token = elapsed / args.steps * 1e6
+
+    # per-kernel durations from HIP events on the launch stream
+    F.prof_enable(True)
+    F.prof_reset()
+    for i in range(args.warmup, args.warmup + args.prof_steps):
+        step(i)
+    torch.cuda.synchronize()
+    phases = {}
+    for name in ("router", "gateup", "down"):
+        n, tot, mn, mx = F.prof_read(name)
+        phases[name] = {"launches": n, "avg_us": round(tot / max(n, 1) * 1e3, 2),
+                        "min_us": round(mn * 1e3, 2), "max_us": round(mx * 1e3, 2)}
+    F.prof_enable(False)
+
+    gu_bytes = gateup_bytes(K)
+    gu_us = phases["gateup"]["avg_us"]
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    lb = layer_bytes(args.down, K)
+    layer_gbps = lb / (us_per_token * 1e-6) / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(us_per_token, 2),
+        "unit": "us/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us_per_token / 1e3, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4k x int8-digit dot4 -> fp32",
+        "data": "synthetic (seeded, device-generated; no real weights)",
+        "config": {
+            "workload": ("DeepSeek-R1 MoE layer, batch-1 decode: fp32 router 256x7168 + "
+                         "group-limited top-8 + 8 routed and 1 shared SwiGLU expert "
+                         f"(Q4_K gate/up 2048x7168, {args.down.upper()} down 7168x2048), "
+                         "combine + residual; 256 experts resident per layer"),
+            "hidden": HIDDEN, "expert_ffn": FFN, "experts": 256, "top_k": K, "shared": 1,
+            "batch": 1, "down": args.down, "layers_rotated": args.layers,
+            "resident_gb": round(args.layers * (256 + 1) * layers[0].expert_size / 1e9, 1),
+        },
+        "layer_bytes": lb,
+        "layer_gbps": round(layer_gbps, 1),
+        "layer_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
+        "phases_us": phases,
+        "roofline": {
+            "kernel": "k_gateup (gate+up matvecs + SwiGLU, 9 experts)",
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": load_traffic("k_gateup", "r1_batch1_q4k"),
+            "bytes_per_launch": gu_bytes,
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args.down, args.cpu_seconds, K)
+        cb = result["cpu_baseline"]["value"]
+        result["speedup_vs_cpu"] = round(cb / us_per_token, 1)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -29,7 +29,7 @@ __all__ = [
     "init", "shutdown", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
     "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
-    "moe_forward_host", "moe_layer", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "moe_forward_host", "moe_layer", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -152,6 +152,27 @@ def moe_layer(L, h_post, h_in, K, hidden, idx=None, w=None, stream=None):
     """MoE branch of layer_forward: hidden = h_in + routed + shared."""
     call("fdm_moe_layer", L, _p(h_post), _p(h_in), K, _p(hidden), _p(idx), _p(w),
          _stream(stream))
+
+
+# ---- per-kernel GPU timing (HIP events; the moe_prof_t counterpart) --------------------
+PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
+          "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC}
+
+
+def prof_enable(on=True):
+    call("fdm_prof_enable", 1 if on else 0)
+
+
+def prof_reset():
+    call("fdm_prof_reset")
+
+
+def prof_read(phase):
+    """(count, total_ms, min_ms, max_ms) of one phase since the last reset."""
+    n, tot, mn, mx = ctypes.c_int(), ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+    call("fdm_prof_read", PHASES.get(phase, phase), ctypes.byref(n), ctypes.byref(tot),
+         ctypes.byref(mn), ctypes.byref(mx))
+    return n.value, tot.value, mn.value, mx.value
 
 
 # ---- synthetic data ------------------------------------------------------------------

@@ -18,6 +18,8 @@ FDM_E_NOMEM = -5
 FDM_E_SIZE = -6
 FDM_E_IO = -7
 
+PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC = range(5)
+
 QK_K = 256
 Q4K_BLOCK_SIZE = 144
 Q6K_BLOCK_SIZE = 210
@@ -65,6 +67,10 @@ SIGNATURES = {
     "fdm_moe_forward": [_i, _vp, _vp, _vp, _i, _vp, _vp],
     "fdm_moe_forward_host": [_i, _vp, _vp, _vp, _i, _vp],
     "fdm_moe_layer": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
+    "fdm_prof_enable": [_i],
+    "fdm_prof_reset": [],
+    "fdm_prof_read": [_i, ctypes.POINTER(_i), ctypes.POINTER(ctypes.c_double),
+                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
     "fdm_synth_q4k": [_vp, _sz, _u64, _vp],
     "fdm_synth_q6k": [_vp, _sz, _u64, _vp],
     "fdm_synth_normal": [_vp, _sz, _f, _f, _u64, _vp],
@@ -85,13 +91,29 @@ def _load():
             "(hipcc, gfx950). There is no CPU fallback.")
     lib = ctypes.CDLL(LIB_PATH)
     for name, args in SIGNATURES.items():
-        fn = getattr(lib, name)
+        try:
+            fn = getattr(lib, name)
+        except AttributeError as e:
+            raise ImportError(f"{LIB_PATH} lacks {name}: it is stale, rebuild it with "
+                              "`python -m flash_deepseek_amd.build`") from e
         fn.argtypes = args
         fn.restype = _RESTYPES.get(name, _i)
     return lib
 
 
-lib = _load()
+class _LazyLib:
+    """Loads libfdm.so on first use, so the package (and its build module)
+    can be imported before the library exists."""
+
+    _handle = None
+
+    def __getattr__(self, name):
+        if _LazyLib._handle is None:
+            _LazyLib._handle = _load()
+        return getattr(_LazyLib._handle, name)
+
+
+lib = _LazyLib()
 
 
 def check(rc, fn="fdm call"):

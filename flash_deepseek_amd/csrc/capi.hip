@@ -60,8 +60,21 @@ struct Layer {
   const uint8_t* shared = nullptr;
 };
 
+// Event pairs recorded around kernel launches when profiling is on.
+struct Prof {
+  static constexpr int kPool = 8192;
+  bool on = false;
+  hipEvent_t start[kPool], stop[kPool];
+  int phase[kPool];
+  int created = 0;
+  int pending = 0;  // pairs recorded and not yet read
+  int count[FDM_PROF_PHASES];
+  double total[FDM_PROF_PHASES], mn[FDM_PROF_PHASES], mx[FDM_PROF_PHASES];
+};
+
 struct State {
   bool ready = false;
+  Prof prof;
   int device = -1;
   Workspace ws;
   Layer layers[FDM_MAX_LAYERS];
@@ -143,6 +156,51 @@ int check_K(int K) {
 
 hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+void prof_clear_stats() {
+  Prof& p = g.prof;
+  for (int i = 0; i < FDM_PROF_PHASES; ++i) {
+    p.count[i] = 0;
+    p.total[i] = 0.0;
+    p.mn[i] = 1e300;
+    p.mx[i] = 0.0;
+  }
+}
+
+// Fold every recorded pair into the statistics (synchronises on them).
+int prof_drain() {
+  Prof& p = g.prof;
+  for (int i = 0; i < p.pending; ++i) {
+    FDM_HIP(hipEventSynchronize(p.stop[i]));
+    float ms = 0.0f;
+    FDM_HIP(hipEventElapsedTime(&ms, p.start[i], p.stop[i]));
+    const int ph = p.phase[i];
+    p.count[ph] += 1;
+    p.total[ph] += ms;
+    if (ms < p.mn[ph]) p.mn[ph] = ms;
+    if (ms > p.mx[ph]) p.mx[ph] = ms;
+  }
+  p.pending = 0;
+  return FDM_OK;
+}
+
+// Brackets one launch with events when profiling is on.
+struct ProfScope {
+  int slot = -1;
+  hipStream_t s;
+  ProfScope(int phase, hipStream_t st) : s(st) {
+    Prof& p = g.prof;
+    if (!p.on) return;
+    if (p.pending == Prof::kPool && prof_drain() != FDM_OK) return;
+    slot = p.pending;
+    p.phase[slot] = phase;
+    if (hipEventRecord(p.start[slot], s) != hipSuccess) slot = -1;
+  }
+  ~ProfScope() {
+    if (slot < 0) return;
+    if (hipEventRecord(g.prof.stop[slot], s) == hipSuccess) g.prof.pending = slot + 1;
+  }
+};
+
 SlotTable slots_for(const Layer& L, const int* idx, const float* w, int K, bool with_shared) {
   SlotTable t;
   t.experts = L.experts;
@@ -193,6 +251,13 @@ int fdm_shutdown(void) {
   (void)hipDeviceSynchronize();
   for (auto& L : g.layers) release_layer(L);
   free_workspace();
+  for (int i = 0; i < g.prof.created; ++i) {
+    (void)hipEventDestroy(g.prof.start[i]);
+    (void)hipEventDestroy(g.prof.stop[i]);
+  }
+  g.prof.created = 0;
+  g.prof.pending = 0;
+  g.prof.on = false;
   g.ready = false;
   g.device = -1;
   return FDM_OK;
@@ -300,9 +365,15 @@ int fdm_matvec_q4k(const void* d_W, const float* d_x, float* d_y, uint32_t out_d
                    uint32_t in_dim, void* stream) {
   if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 4)) return rc;
   hipStream_t s = as_stream(stream);
-  FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
-  FDM_HIP(launch_matvec_q4k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
-                            (int)in_dim, s));
+  {
+    ProfScope p(FDM_PROF_XDIGITS, s);
+    FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_MATVEC, s);
+    FDM_HIP(launch_matvec_q4k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
+                              (int)in_dim, s));
+  }
   return FDM_OK;
 }
 
@@ -310,9 +381,15 @@ int fdm_matvec_q6k(const void* d_W, const float* d_x, float* d_y, uint32_t out_d
                    uint32_t in_dim, void* stream) {
   if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 2)) return rc;
   hipStream_t s = as_stream(stream);
-  FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
-  FDM_HIP(launch_matvec_q6k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
-                            (int)in_dim, s));
+  {
+    ProfScope p(FDM_PROF_XDIGITS, s);
+    FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_MATVEC, s);
+    FDM_HIP(launch_matvec_q6k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
+                              (int)in_dim, s));
+  }
   return FDM_OK;
 }
 
@@ -336,9 +413,18 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   t.w = nullptr;
   t.K = 0;
   t.n_slots = 1;
-  FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, g.ws.xd, s));
-  FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
-  FDM_HIP(launch_down_combine(t, q6, g.ws.act_xd, nullptr, d_out, nullptr, s));
+  {
+    ProfScope p(FDM_PROF_XDIGITS, s);
+    FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, g.ws.xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_GATEUP, s);
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_DOWN, s);
+    FDM_HIP(launch_down_combine(t, q6, g.ws.act_xd, nullptr, d_out, nullptr, s));
+  }
   if (d_act)
     FDM_HIP(hipMemcpyAsync(d_act, g.ws.act, FDM_MOE_FFN * sizeof(float),
                            hipMemcpyDeviceToDevice, s));
@@ -467,9 +553,18 @@ int fdm_moe_forward(int L, const float* d_h_post, const int* d_idx, const float*
   if (!d_h_post || !d_idx || !d_w || !d_moe_out) return fail(FDM_E_INVAL, "null pointer");
   hipStream_t s = as_stream(stream);
   const SlotTable t = slots_for(*y, d_idx, d_w, K, false);
-  FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, g.ws.xd, s));
-  FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
-  FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, nullptr, d_moe_out, nullptr, s));
+  {
+    ProfScope p(FDM_PROF_XDIGITS, s);
+    FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, g.ws.xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_GATEUP, s);
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_DOWN, s);
+    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, nullptr, d_moe_out, nullptr, s));
+  }
   return FDM_OK;
 }
 
@@ -499,11 +594,66 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   hipStream_t s = as_stream(stream);
   int* idx = d_idx ? d_idx : g.ws.idx;
   float* w = d_w ? d_w : g.ws.w;
-  FDM_HIP(launch_router_layer(y->Wg, y->bias, d_h_post, K, g.ws.logits, g.ws.xd, idx, w,
-                              g.ws.counter, s));
+  {
+    ProfScope p(FDM_PROF_ROUTER, s);
+    FDM_HIP(launch_router_layer(y->Wg, y->bias, d_h_post, K, g.ws.logits, g.ws.xd, idx, w,
+                                g.ws.counter, s));
+  }
   const SlotTable t = slots_for(*y, idx, w, K, true);
-  FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
-  FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, d_h_in, d_hidden, nullptr, s));
+  {
+    ProfScope p(FDM_PROF_GATEUP, s);
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+  }
+  {
+    ProfScope p(FDM_PROF_DOWN, s);
+    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, d_h_in, d_hidden, nullptr, s));
+  }
+  return FDM_OK;
+}
+
+// ---- per-kernel timing ----------------------------------------------------------------
+int fdm_prof_enable(int on) {
+  if (int rc = check_ready()) return rc;
+  Prof& p = g.prof;
+  if (on && p.created == 0) {
+    for (int i = 0; i < Prof::kPool; ++i) {
+      FDM_HIP(hipEventCreate(&p.start[i]));
+      FDM_HIP(hipEventCreate(&p.stop[i]));
+      p.created = i + 1;
+    }
+    prof_clear_stats();
+  }
+  if (!on && p.on) {
+    if (int rc = prof_drain()) return rc;
+  }
+  p.on = on != 0;
+  return FDM_OK;
+}
+
+int fdm_prof_reset(void) {
+  if (int rc = check_ready()) return rc;
+  if (g.prof.created == 0) return FDM_OK;
+  if (int rc = prof_drain()) return rc;
+  prof_clear_stats();
+  return FDM_OK;
+}
+
+int fdm_prof_read(int phase, int* count, double* total_ms, double* min_ms, double* max_ms) {
+  if (int rc = check_ready()) return rc;
+  if (phase < 0 || phase >= FDM_PROF_PHASES) return fail(FDM_E_INVAL, "phase %d", phase);
+  Prof& p = g.prof;
+  if (p.created == 0) {
+    if (count) *count = 0;
+    if (total_ms) *total_ms = 0.0;
+    if (min_ms) *min_ms = 0.0;
+    if (max_ms) *max_ms = 0.0;
+    return FDM_OK;
+  }
+  if (int rc = prof_drain()) return rc;
+  if (count) *count = p.count[phase];
+  if (total_ms) *total_ms = p.total[phase];
+  if (min_ms) *min_ms = p.count[phase] ? p.mn[phase] : 0.0;
+  if (max_ms) *max_ms = p.mx[phase];
   return FDM_OK;
 }
 

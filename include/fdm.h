@@ -146,6 +146,21 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
 
+/* ---- per-kernel GPU timing: replaces the host-clock moe_prof_t ring
+ * (infer.m:177-261) with HIP events recorded on the launch stream around
+ * every kernel of the entry points above.  fdm_prof_read synchronises on
+ * the recorded events and returns the count, total, min and max duration
+ * (milliseconds) of one phase since the last reset. */
+#define FDM_PROF_ROUTER 0   /* router logits + digits of h_post + route */
+#define FDM_PROF_GATEUP 1   /* gate/up matvecs + SwiGLU, all slots      */
+#define FDM_PROF_DOWN 2     /* down matvecs + combine (+ residual)      */
+#define FDM_PROF_XDIGITS 3  /* activation digits (routing given)        */
+#define FDM_PROF_MATVEC 4   /* fdm_matvec_q4k / _q6k kernel             */
+#define FDM_PROF_PHASES 5
+int fdm_prof_enable(int on);
+int fdm_prof_reset(void);
+int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);
+
 /* ---- seeded synthetic tensors (benchmark inputs; same generator as the
  * C restatement's synth.c) ---------------------------------------------- */
 int fdm_synth_q4k(void *d_dst, size_t n_blocks, uint64_t seed, void *stream);

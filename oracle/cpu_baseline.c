@@ -108,3 +108,55 @@ double orc_cpu_expert_baseline(const void *const *blobs, int n_experts, int down
     free(th);
     return med;
 }
+
+/* The whole MoE branch of layer_forward on the CPU, as the reference runs it
+ * with USE_CPU_EXPERTS (infer.m:1878-1922): router sgemv on the calling
+ * thread, route(), then one thread per routed expert plus one for the
+ * shared expert (infer.m:1886-1914), slot-order combine and the residual.
+ * blobs[0..K-1] are the routed experts to run (a bounded sample: the same K
+ * blobs whatever route() picks), blobs[K] the shared expert.  Returns the
+ * median microseconds per token over `reps`; out receives the last result. */
+double orc_cpu_layer_baseline(const void *const *blobs, int K, int down_is_q6, const float *Wg,
+                              const float *bias, const float *x, const float *h_in,
+                              float *out, int reps) {
+    if (K <= 0 || K > ORC_MAX_K || reps <= 0) return -1.0;
+    const int n = K + 1;
+    const size_t nel = (size_t)ORC_FFN * ORC_HIDDEN;
+    job_t *jobs = (job_t *)calloc((size_t)n, sizeof(job_t));
+    for (int k = 0; k < n; ++k) {
+        jobs[k].blob = blobs[k];
+        jobs[k].down_is_q6 = down_is_q6;
+        jobs[k].x = x;
+        jobs[k].gate_mat = (float *)malloc(nel * sizeof(float));
+        jobs[k].up_mat = (float *)malloc(nel * sizeof(float));
+        jobs[k].down_mat = (float *)malloc(nel * sizeof(float));
+    }
+    double *t = (double *)malloc(sizeof(double) * (size_t)reps);
+    pthread_t th[ORC_MAX_K + 1];
+    float logits[ORC_N_EXPERTS];
+    int idx[ORC_MAX_K];
+    float w[ORC_MAX_K];
+    for (int r = 0; r < reps; ++r) {
+        const double t0 = now_us();
+        sgemv_rows(Wg, x, logits, ORC_N_EXPERTS, ORC_HIDDEN);
+        orc_route(logits, bias, K, idx, w);
+        for (int k = 0; k < n; ++k) pthread_create(&th[k], NULL, expert_job, &jobs[k]);
+        for (int k = 0; k < n; ++k) pthread_join(th[k], NULL);
+        for (int i = 0; i < ORC_HIDDEN; ++i) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; ++k) acc += w[k] * jobs[k].out[i];
+            out[i] = h_in[i] + acc + jobs[K].out[i];
+        }
+        t[r] = now_us() - t0;
+    }
+    qsort(t, (size_t)reps, sizeof(double), cmp_double);
+    const double med = t[reps / 2];
+    for (int k = 0; k < n; ++k) {
+        free(jobs[k].gate_mat);
+        free(jobs[k].up_mat);
+        free(jobs[k].down_mat);
+    }
+    free(jobs);
+    free(t);
+    return med;
+}

@@ -111,6 +111,11 @@ void orc_synth_q6k(uint8_t *dst, size_t n_blocks, uint64_t seed);
 double orc_cpu_expert_baseline(const void *const *blobs, int n_experts, int down_is_q6,
                                const float *x, const float *w, float *out, int reps,
                                int n_threads);
+/* Router + route + K routed experts + shared expert + combine + residual,
+ * K+1 threads (infer.m:1878-1922 with USE_CPU_EXPERTS). */
+double orc_cpu_layer_baseline(const void *const *blobs, int K, int down_is_q6, const float *Wg,
+                              const float *bias, const float *x, const float *h_in,
+                              float *out, int reps);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,9 @@ def _load():
         "orc_cpu_expert_baseline": (ctypes.c_double, [ctypes.POINTER(_vp), ctypes.c_int,
                                                       ctypes.c_int, _f32p, _f32p, _f32p,
                                                       ctypes.c_int, ctypes.c_int]),
+        "orc_cpu_layer_baseline": (ctypes.c_double, [ctypes.POINTER(_vp), ctypes.c_int,
+                                                     ctypes.c_int, _f32p, _f32p, _f32p, _f32p,
+                                                     _f32p, ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -243,6 +246,19 @@ def cpu_expert_baseline(blobs, down_is_q6, x, w, reps, n_threads=0):
     w = np.ascontiguousarray(w, dtype=np.float32)
     us = L.orc_cpu_expert_baseline(arr, len(blobs), int(down_is_q6), x, w, out, reps,
                                    n_threads)
+    return us, out
+
+
+def cpu_layer_baseline(blobs, down_is_q6, Wg, bias, x, h_in, reps):
+    """Median microseconds per token of the reference-shaped CPU MoE layer
+    (blobs: K routed experts then the shared one)."""
+    arr = (ctypes.c_void_p * len(blobs))(*[b.ctypes.data for b in blobs])
+    out = np.empty(HIDDEN, dtype=np.float32)
+    us = L.orc_cpu_layer_baseline(arr, len(blobs) - 1, int(down_is_q6),
+                                  np.ascontiguousarray(Wg, np.float32),
+                                  np.ascontiguousarray(bias, np.float32),
+                                  np.ascontiguousarray(x, np.float32),
+                                  np.ascontiguousarray(h_in, np.float32), out, reps)
     return us, out
 
 
