@@ -43,8 +43,9 @@ def layer_bytes(down, K=8):
 
 
 def gateup_bytes(K=8):
-    slots = K + 1
-    return slots * 2 * GATE_BYTES + HIDDEN * 4 + slots * FFN * 4  # W + x in + act out
+    """Routed gate/up launch: the K selected experts' gate and up matrices
+    (the shared expert's run inside the router launch)."""
+    return K * 2 * GATE_BYTES + HIDDEN * 4 + K * FFN * 4  # W + x in + act out
 
 
 def load_traffic(kernel, workload):
@@ -181,7 +182,7 @@ def main():
         "layer_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "phases_us": phases,
         "roofline": {
-            "kernel": "k_gateup (gate+up matvecs + SwiGLU, 9 experts)",
+            "kernel": "k_gateup (gate+up matvecs + SwiGLU, 8 routed experts)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,

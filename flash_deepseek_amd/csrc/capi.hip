@@ -36,12 +36,17 @@ int hip_fail(hipError_t e, const char* what) {
 
 struct Workspace {
   XGroup* xd = nullptr;       // digits of activations (up to FDM_MAX_TOKENS x 112)
-  float* logits = nullptr;    // FDM_MAX_TOKENS x 256
+  float* logits = nullptr;    // FDM_MAX_TOKENS x 256 (the layer path: sigmoid scores)
   int* idx = nullptr;         // FDM_MAX_TOKENS x 16
+  int* pidx = nullptr;        // the expert set the layer's slots run (FDM_MAX_K)
+  int* perm = nullptr;        // combine order over those slots (FDM_MAX_K)
   float* w = nullptr;         // FDM_MAX_TOKENS x 16
   float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
   XGroup* act_xd = nullptr;   // (FDM_MAX_K + 1) x 32
-  int* counter = nullptr;     // last-workgroup counter of the router
+  int* counter = nullptr;     // arrival counters of the router (two levels)
+  int* gu_count = nullptr;    // arrival counters: (FDM_MAX_K + 1) x 64 act sub-blocks
+  int* dn_count = nullptr;    // arrival counters: 448 down row tiles
+  float* eo = nullptr;        // per-slot expert outputs (FDM_MAX_K + 1) x 7168
   float* stage_x = nullptr;   // host-API staging: h_post
   float* stage_y = nullptr;   //                   moe_out
   int* stage_idx = nullptr;   //                   exp_idx
@@ -107,8 +112,9 @@ int down_type(size_t expert_size, bool* q6) {
 
 void free_workspace() {
   Workspace& w = g.ws;
-  void* ptrs[] = {w.xd,      w.logits,  w.idx,     w.w,         w.act,     w.act_xd,
-                  w.counter, w.stage_x, w.stage_y, w.stage_idx, w.stage_w};
+  void* ptrs[] = {w.xd,       w.logits,   w.idx,     w.w,       w.act,
+                  w.act_xd,   w.counter,  w.gu_count, w.dn_count, w.eo,
+                  w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w, w.pidx, w.perm};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -122,8 +128,15 @@ int alloc_workspace() {
   FDM_HIP(hipMalloc(&w.w, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(float)));
   FDM_HIP(hipMalloc(&w.act, (size_t)(FDM_MAX_K + 1) * FDM_MOE_FFN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.act_xd, (size_t)(FDM_MAX_K + 1) * (FDM_MOE_FFN / 64) * sizeof(XGroup)));
-  FDM_HIP(hipMalloc(&w.counter, 256));
-  FDM_HIP(hipMemset(w.counter, 0, 256));
+  FDM_HIP(hipMalloc(&w.counter, kRouterCounterInts * sizeof(int)));
+  FDM_HIP(hipMemset(w.counter, 0, kRouterCounterInts * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.gu_count, (FDM_MAX_K + 1) * 64 * sizeof(int)));
+  FDM_HIP(hipMemset(w.gu_count, 0, (FDM_MAX_K + 1) * 64 * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.dn_count, 448 * sizeof(int)));
+  FDM_HIP(hipMemset(w.dn_count, 0, 448 * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.eo, (size_t)(FDM_MAX_K + 1) * FDM_HIDDEN * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.pidx, FDM_MAX_K * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.perm, FDM_MAX_K * sizeof(int)));
   FDM_HIP(hipMalloc(&w.stage_x, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_y, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_idx, FDM_MAX_K * sizeof(int)));
@@ -209,6 +222,7 @@ SlotTable slots_for(const Layer& L, const int* idx, const float* w, int K, bool 
   t.shared = with_shared ? L.shared : nullptr;
   t.idx = idx;
   t.w = w;
+  t.perm = nullptr;
   t.K = K;
   t.n_slots = K + ((with_shared && L.shared) ? 1 : 0);
   return t;
@@ -419,11 +433,12 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   }
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, ExactRoute{}, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, q6, g.ws.act_xd, nullptr, d_out, nullptr, s));
+    FDM_HIP(launch_down_combine(t, q6, g.ws.act_xd, nullptr, d_out, nullptr, g.ws.eo,
+                                g.ws.dn_count, s));
   }
   if (d_act)
     FDM_HIP(hipMemcpyAsync(d_act, g.ws.act, FDM_MOE_FFN * sizeof(float),
@@ -559,11 +574,12 @@ int fdm_moe_forward(int L, const float* d_h_post, const int* d_idx, const float*
   }
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, ExactRoute{}, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, nullptr, d_moe_out, nullptr, s));
+    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, nullptr, d_moe_out, nullptr,
+                                g.ws.eo, g.ws.dn_count, s));
   }
   return FDM_OK;
 }
@@ -596,17 +612,28 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   float* w = d_w ? d_w : g.ws.w;
   {
     ProfScope p(FDM_PROF_ROUTER, s);
-    FDM_HIP(launch_router_layer(y->Wg, y->bias, d_h_post, K, g.ws.logits, g.ws.xd, idx, w,
-                                g.ws.counter, s));
+    // The router selects the expert set (pidx); the shared expert's gate/up
+    // runs inside the same launch (slot K).
+    FDM_HIP(launch_router_layer(y->Wg, y->bias, d_h_post, K, g.ws.logits, g.ws.xd, g.ws.pidx,
+                                g.ws.counter, y->shared, g.ws.act + (size_t)K * FDM_MOE_FFN,
+                                g.ws.act_xd + (size_t)K * (FDM_MOE_FFN / 64),
+                                g.ws.gu_count + K * 64, s));
   }
-  const SlotTable t = slots_for(*y, idx, w, K, true);
+  // Slots run the experts of pidx; the combine takes the reference's slot
+  // order (idx/w) through perm, both written by the gate/up launch.
+  SlotTable t = slots_for(*y, g.ws.pidx, w, K, true);
+  t.perm = g.ws.perm;
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, s));
+    SlotTable routed = t;
+    routed.n_slots = K;  // routed experts only
+    const ExactRoute r{g.ws.logits, y->bias, g.ws.pidx, idx, w, g.ws.perm};
+    FDM_HIP(launch_gateup(routed, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, r, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, d_h_in, d_hidden, nullptr, s));
+    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, d_h_in, d_hidden, nullptr, g.ws.eo,
+                                g.ws.dn_count, s));
   }
   return FDM_OK;
 }

@@ -168,6 +168,42 @@ __device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, 
   return fmaf(d, qx, -dmin * mx);
 }
 
+// Broadcast lane `src` of each group of four lanes to the whole quad (DPP
+// quad_perm [src,src,src,src]; no LDS traffic).
+template <int SRC>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  constexpr int ctrl = SRC | (SRC << 2) | (SRC << 4) | (SRC << 6);
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, 0xF, 0xF, false);
+}
+
+// The weight bytes one lane needs for one Q4_K group.  The four lanes that
+// share a block (groups g = 0..3 of it, consecutive lanes) each load one
+// dword of the 16-byte block header and exchange them by DPP, instead of
+// all four loading the whole header.
+struct Q4KGroupLoad {
+  uint32_t hdr_part;  // header dword g of the block
+  u32x4 q0, q1;       // the group's 32 qs bytes
+};
+
+__device__ __forceinline__ Q4KGroupLoad q4k_load_group(const uint8_t* blk, int g) {
+  Q4KGroupLoad r;
+  r.hdr_part = *reinterpret_cast<const uint32_t*>(blk + 4 * g);
+  r.q0 = *reinterpret_cast<const u32x4_a4*>(blk + 16 + 32 * g);
+  r.q1 = *reinterpret_cast<const u32x4_a4*>(blk + 32 + 32 * g);
+  return r;
+}
+
+// Every lane of the quad must call this (it exchanges header dwords).
+__device__ __forceinline__ float q4k_group_dot_ld(const Q4KGroupLoad& r, const Q4KScaleSel& sel,
+                                                  const XGroup* __restrict__ xg) {
+  u32x4 h;
+  h.x = quad_bcast<0>(r.hdr_part);
+  h.y = quad_bcast<1>(r.hdr_part);
+  h.z = quad_bcast<2>(r.hdr_part);
+  h.w = quad_bcast<3>(r.hdr_part);
+  return q4k_group_dot(h, r.q0, r.q1, sel, xg);
+}
+
 // funnel: the 4 bytes starting `byte_shift` (0..3) bytes into the 8-byte
 // little-endian pair (lo, hi).
 __device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t byte_shift) {
@@ -234,6 +270,26 @@ __device__ __forceinline__ float sum16(float v) {
   v += __shfl_xor(v, 2);
   v += __shfl_xor(v, 1);
   return v;
+}
+
+// Cross-workgroup hand-off inside one kernel (arrival counters).  The few
+// values handed over are written with agent-scope stores (written through
+// past the per-XCD L2) and read with agent-scope loads, so the writer only
+// has to wait for its stores to be acknowledged before bumping the counter.
+// A __threadfence() would do the same but write back and invalidate the
+// whole L2 of the XCD, once per workgroup.
+__device__ __forceinline__ void store_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ int arrive_agent(int* counter) {
+  return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_agent(int* counter) {
+  __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }

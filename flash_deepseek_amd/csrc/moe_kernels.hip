@@ -2,17 +2,27 @@
 // experts at once (infer.m:1559-1575 encode_expert, run for every slot, and
 // the combine of infer.m:1689-1695 / 1922).
 //
-// k_gateup:  one workgroup per (slot, 32-row tile).  Each wave computes a
-//   pair of rows of gate AND the same pair of rows of up (lanes 0-31 gate,
-//   32-63 up, 16 lanes per row), so SwiGLU is applied in registers
-//   (swiglu_fused, shaders.metal:210-220, needs no launch of its own).  The
-//   tile's 32 activations form one sub-block of the down matvec's input:
-//   the workgroup writes their digits directly.
-// k_down_combine:  one workgroup per 16 output rows, looping over the
-//   slots: down row of each slot, weighted by the routing weight in slot
-//   order, then the shared expert and the residual are added
-//   (hidden = h_in + moe_out + shared, infer.m:1922).
+// Both kernels are shaped for memory-level parallelism: many small
+// workgroups, each issuing every weight load it needs before any math, so
+// that the HBM queue stays full (one 16-byte load per lane per step; the
+// four lanes of a Q4_K block share its header through DPP).
+//
+// k_gateup  one workgroup per (slot, 8-row tile), plus (workgroup 0, first
+//   to be dispatched) the exact route() of the token when the router only
+//   selected the expert set: the slot order and weights are needed by the
+//   combine alone, so they are computed here beside the weight stream.  Wave w owns rows 2w and
+//   2w+1 of the tile in BOTH gate and up (lanes 0-31 gate, 32-63 up, 16
+//   lanes per row), so SwiGLU (swiglu_fused, shaders.metal:210-220) is
+//   applied in registers.  The last of the four tiles of a 32-row sub-block
+//   to finish turns the sub-block's activations into the digits the down
+//   matvec reads (a per-sub-block arrival counter).
+// k_down    one workgroup per (slot, 16-row tile): the slot's down rows.
+//   The last of the slots of a row tile to finish combines them in slot
+//   order, then adds the shared expert and the residual
+//   (moe_out += w_k * E_k, infer.m:1690-1695; hidden = h_in + moe_out + sd,
+//   infer.m:1922).
 #include "fdm_internal.h"
+#include "route_device.h"
 
 namespace fdm {
 
@@ -25,172 +35,226 @@ __device__ __forceinline__ const uint8_t* slot_blob(const SlotTable& t, int slot
   return t.shared;
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k_gateup(SlotTable t, const XGroup* __restrict__ xd,
-                                                float* __restrict__ act,
-                                                XGroup* __restrict__ act_xd) {
-  __shared__ XGroup xs[kHidden / 64];
-  __shared__ float act_tile[32];
-  const int slot = blockIdx.y, tile = blockIdx.x;
-  const uint8_t* blob = slot_blob(t, slot);
-  {
-    const u32x4* s = reinterpret_cast<const u32x4*>(xd);
-    u32x4* d = reinterpret_cast<u32x4*>(xs);
-    for (int i = threadIdx.x; i < (kHidden / 64) * 9; i += 256) d[i] = s[i];
+__device__ __forceinline__ void stage_groups(XGroup* __restrict__ dst,
+                                             const XGroup* __restrict__ src, int n) {
+  const u32x4* s = reinterpret_cast<const u32x4*>(src);
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  for (int i = threadIdx.x; i < n * 9; i += blockDim.x) d[i] = s[i];
+}
+
+constexpr int kGuRows = 8;                 // rows of gate (and up) per workgroup
+constexpr int kGuTiles = kFfn / kGuRows;   // 256 tiles per slot
+
+// Workgroup body of the exact route(): wave 0 runs it; lane k < K finds
+// the provisional slot holding its expert.
+__device__ void exact_route_wg(const ExactRoute& r, int K) {
+  if (threadIdx.x >= 64) return;
+  const int lane = threadIdx.x;
+  float sc[4], bj[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = r.scores[64 * j + lane];
+    bj[j] = r.bias ? r.bias[64 * j + lane] : 0.0f;
   }
-  __syncthreads();
+  route_scores_wave(sc, bj, K, 2.5f, r.idx, r.w);
+  if (lane < K) {
+    const int id = r.idx[lane];
+    int p = 0;
+    for (int s = K - 1; s >= 0; --s) p = r.prov_idx[s] == id ? s : p;
+    r.perm[lane] = p;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __restrict__ xd,
+                                                float* __restrict__ act,
+                                                XGroup* __restrict__ act_xd,
+                                                int* __restrict__ counters, ExactRoute r) {
+  __shared__ XGroup xs[kHidden / 64];
+  __shared__ int last;
+  int b = blockIdx.x;
+  if (r.scores) {
+    if (b == 0) {
+      exact_route_wg(r, t.K);
+      return;
+    }
+    --b;
+  }
+  const int slot = b / kGuTiles, tile = b % kGuTiles;
+  const uint8_t* blob = slot_blob(t, slot);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
-  const Q4KScaleSel sel = q4k_scale_sel(g);
-#pragma unroll 1
-  for (int it = 0; it < 4; ++it) {
-    const int rp = 8 * it + 2 * wave + (q & 1);  // row within the tile
-    const int row = tile * 32 + rp;
-    float acc = 0.0f;
-    if (blob) {
-      const uint8_t* rowp = blob + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
-      // issue every weight load of the row first (7 groups x 48 bytes per
-      // lane), then consume the groups one by one against the LDS digits
-      u32x4 hdr[7], q0[7], q1[7];
+  const int row = tile * kGuRows + 2 * wave + (q & 1);
+  Q4KGroupLoad ld[7];
+  if (blob) {
+    const uint8_t* rowp = blob + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
 #pragma unroll
-      for (int i = 0; i < 7; ++i) {
-        const uint8_t* bp = rowp + (4 * i + (l16 >> 2)) * kQ4KBlock;
-        hdr[i] = *reinterpret_cast<const u32x4_a4*>(bp);
-        q0[i] = *reinterpret_cast<const u32x4_a4*>(bp + 16 + 32 * g);
-        q1[i] = *reinterpret_cast<const u32x4_a4*>(bp + 32 + 32 * g);
-      }
+    for (int i = 0; i < 7; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
+  }
+  stage_groups(xs, xd, kHidden / 64);
+  __syncthreads();
+  float acc = 0.0f;
+  if (blob) {
+    const Q4KScaleSel sel = q4k_scale_sel(g);
 #pragma unroll
-      for (int i = 0; i < 7; ++i) {
-        acc += q4k_group_dot(hdr[i], q0[i], q1[i], sel, &xs[16 * i + l16]);
-        // keep each group's LDS reads next to its math (bounds live registers)
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int i = 0; i < 7; ++i) {
+      acc += q4k_group_dot_ld(ld[i], sel, &xs[16 * i + l16]);
+      __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
     }
-    acc = sum16(acc);
-    const float up = __shfl(acc, (lane + 32) & 63);
-    if (lane == 0 || lane == 16) act_tile[rp] = silu_mul(acc, up);
+  }
+  acc = sum16(acc);
+  const float up = __shfl(acc, (lane + 32) & 63);
+  if (lane == 0 || lane == 16) {
+    store_agent(act + (size_t)slot * kFfn + row, silu_mul(acc, up));
+    wait_stores_done();
   }
   __syncthreads();
-  if (threadIdx.x < 32) {
-    const float v = act_tile[threadIdx.x];
-    act[(size_t)slot * kFfn + tile * 32 + threadIdx.x] = v;
-    int8_t a, b;
-    float s, sum;
-    make_digits32(v, a, b, s, sum);
-    XGroup* xg = act_xd + (size_t)slot * (kFfn / 64) + (tile >> 1);
-    const int half = tile & 1;
-    xg->a[32 * half + threadIdx.x] = a;
-    xg->b[32 * half + threadIdx.x] = b;
-    if (threadIdx.x == 0) {
-      xg->s[half] = s;
-      xg->xsum[half] = sum;
+  int* cnt = counters + slot * (kFfn / 32) + (tile >> 2);
+  if (threadIdx.x == 0) last = (arrive_agent(cnt) == 3);
+  __syncthreads();
+  if (last) {
+    if (threadIdx.x < 32) {
+      const int base = (tile >> 2) * 32;
+      const float v = load_agent(act + (size_t)slot * kFfn + base + threadIdx.x);
+      int8_t a, b;
+      float s, sum;
+      make_digits32(v, a, b, s, sum);
+      XGroup* xg = act_xd + (size_t)slot * (kFfn / 64) + (tile >> 3);
+      const int half = (tile >> 2) & 1;
+      xg->a[32 * half + threadIdx.x] = a;
+      xg->b[32 * half + threadIdx.x] = b;
+      if (threadIdx.x == 0) {
+        xg->s[half] = s;
+        xg->xsum[half] = sum;
+        reset_agent(cnt);
+      }
     }
   }
 }
 
+// Raw words of one 128-element half of a Q6_K block, loaded from
+// dword-aligned addresses (a block starts at any even byte offset).
+struct Q6KHalfLoad {
+  uint32_t ql[17], qh[9];
+  uint32_t sc[2];
+  uint32_t d;
+  uint32_t shift;
+};
+
+__device__ __forceinline__ Q6KHalfLoad q6k_load_half(const uint8_t* blk, int h) {
+  Q6KHalfLoad r;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(blk + 64 * h);
+  r.shift = a0 & 3u;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(a0 - r.shift);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r.ql[i] = p[i];
+  r.ql[16] = r.shift ? p[16] : 0u;
+  const uint32_t* ph =
+      reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk + 128 + 32 * h) - r.shift);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r.qh[i] = ph[i];
+  r.qh[8] = r.shift ? ph[8] : 0u;
+  const uint16_t* s16 = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h);
+  r.sc[0] = (uint32_t)s16[0] | ((uint32_t)s16[1] << 16);
+  r.sc[1] = (uint32_t)s16[2] | ((uint32_t)s16[3] << 16);
+  r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+  return r;
+}
+
+__device__ __forceinline__ float q6k_half_dot_ld(const Q6KHalfLoad& r,
+                                                 const XGroup* __restrict__ xg) {
+  uint32_t ql[16], qh[8];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) ql[i] = funnel(r.ql[i], r.ql[i + 1], r.shift);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) qh[i] = funnel(r.qh[i], r.qh[i + 1], r.shift);
+  return half_to_float(r.d) * q6k_half_dot(ql, qh, r.sc, xg, xg + 1);
+}
+
+constexpr int kDnRows = 16;                   // down rows per workgroup
+constexpr int kDnTiles = kHidden / kDnRows;   // 448
+
 template <bool Q6>
-__global__ __launch_bounds__(256) void k_down_combine(SlotTable t,
-                                                      const XGroup* __restrict__ act_xd,
-                                                      const float* __restrict__ h_in,
-                                                      float* __restrict__ out,
-                                                      float* __restrict__ moe_out) {
-  extern __shared__ XGroup xs[];  // n_slots * 32 records
-  {
-    const u32x4* s = reinterpret_cast<const u32x4*>(act_xd);
-    u32x4* d = reinterpret_cast<u32x4*>(xs);
-    const int n = t.n_slots * (kFfn / 64) * 9;
-    for (int i = threadIdx.x; i < n; i += 256) d[i] = s[i];
-  }
-  __syncthreads();
+__global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restrict__ act_xd,
+                                              const float* __restrict__ h_in,
+                                              float* __restrict__ out,
+                                              float* __restrict__ moe_out,
+                                              float* __restrict__ eo,
+                                              int* __restrict__ counters) {
+  __shared__ XGroup xs[kFfn / 64];
+  __shared__ int last;
+  const int slot = blockIdx.y, tile = blockIdx.x;
+  const uint8_t* blob = slot_blob(t, slot);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
-  const int row = blockIdx.x * 16 + wave * 4 + (lane >> 4);
-  float moe = 0.0f, sd = 0.0f;
-#pragma unroll 1
-  for (int k = 0; k < t.n_slots; ++k) {
-    const uint8_t* blob = slot_blob(t, k);
-    float acc = 0.0f;
+  const int row = tile * kDnRows + wave * 4 + (lane >> 4);
+  float acc = 0.0f;
+  if (!Q6) {
+    Q4KGroupLoad ld[2];
     if (blob) {
-      const uint8_t* dp = blob + 2 * (size_t)kGateBytes;
-      const XGroup* xk = xs + k * (kFfn / 64);
-      if (!Q6) {
-        const uint8_t* rowp = dp + (size_t)row * kQ4KRowFfn;
+      const uint8_t* rowp = blob + 2 * (size_t)kGateBytes + (size_t)row * kQ4KRowFfn;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int G = 16 * i + l16;
-          const int g = G & 3;
-          const Q4KScaleSel sel = q4k_scale_sel(g);
-          const uint8_t* bp = rowp + (G >> 2) * kQ4KBlock;
-          const u32x4 hdr = *reinterpret_cast<const u32x4_a4*>(bp);
-          const u32x4 q0 = *reinterpret_cast<const u32x4_a4*>(bp + 16 + 32 * g);
-          const u32x4 q1 = *reinterpret_cast<const u32x4_a4*>(bp + 32 + 32 * g);
-          acc += q4k_group_dot(hdr, q0, q1, sel, &xk[G]);
-        }
-      } else {
-        // 16 halves of 128 elements per 2048-column row: one per lane
-        const uint8_t* blk = dp + (size_t)row * kQ6KRowFfn + (l16 >> 1) * kQ6KBlock;
-        const int h = l16 & 1;
-        uint32_t ql[16], qh[8], sc[2];
-        {
-          const uintptr_t a0 = reinterpret_cast<uintptr_t>(blk + 64 * h);
-          const uint32_t sh = a0 & 3u;
-          const uint32_t* p = reinterpret_cast<const uint32_t*>(a0 - sh);
-          uint32_t wv[17];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) wv[i] = p[i];
-          wv[16] = sh ? p[16] : 0u;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) ql[i] = funnel(wv[i], wv[i + 1], sh);
-          const uint32_t* ph = reinterpret_cast<const uint32_t*>(
-              reinterpret_cast<uintptr_t>(blk + 128 + 32 * h) - sh);
-          uint32_t wh[9];
-#pragma unroll
-          for (int i = 0; i < 8; ++i) wh[i] = ph[i];
-          wh[8] = sh ? ph[8] : 0u;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) qh[i] = funnel(wh[i], wh[i + 1], sh);
-        }
-        const uint16_t* s16 = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h);
-        sc[0] = (uint32_t)s16[0] | ((uint32_t)s16[1] << 16);
-        sc[1] = (uint32_t)s16[2] | ((uint32_t)s16[3] << 16);
-        const float d = half_to_float(*reinterpret_cast<const uint16_t*>(blk + 208));
-        acc = d * q6k_half_dot(ql, qh, sc, &xk[2 * l16], &xk[2 * l16 + 1]);
-      }
+      for (int i = 0; i < 2; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
     }
-    acc = sum16(acc);
-    if (k < t.K)
-      moe = fmaf(t.w[k], acc, moe);
-    else
-      sd = acc;
+    stage_groups(xs, act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
+    __syncthreads();
+    if (blob) {
+      const Q4KScaleSel sel = q4k_scale_sel(l16 & 3);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) acc += q4k_group_dot_ld(ld[i], sel, &xs[16 * i + l16]);
+    }
+  } else {
+    // 16 halves of 128 elements per 2048-column row: one per lane
+    Q6KHalfLoad ld;
+    if (blob)
+      ld = q6k_load_half(blob + 2 * (size_t)kGateBytes + (size_t)row * kQ6KRowFfn +
+                             (l16 >> 1) * kQ6KBlock,
+                         l16 & 1);
+    stage_groups(xs, act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
+    __syncthreads();
+    if (blob) acc = q6k_half_dot_ld(ld, &xs[2 * l16]);
   }
+  acc = sum16(acc);
   if (l16 == 0) {
-    const float hin = h_in ? h_in[row] : 0.0f;
-    out[row] = (hin + moe) + sd;
-    if (moe_out) moe_out[row] = moe;
+    store_agent(eo + (size_t)slot * kHidden + row, acc);
+    wait_stores_done();
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) last = (arrive_agent(counters + tile) == t.n_slots - 1);
+  __syncthreads();
+  if (last) {
+    if (threadIdx.x < kDnRows) {
+      const int r = tile * kDnRows + threadIdx.x;
+      float moe = 0.0f;
+      for (int k = 0; k < t.K; ++k) {
+        const int sl = t.perm ? t.perm[k] : k;
+        moe = fmaf(t.w[k], load_agent(eo + (size_t)sl * kHidden + r), moe);
+      }
+      const float sd = t.n_slots > t.K ? load_agent(eo + (size_t)t.K * kHidden + r) : 0.0f;
+      const float hin = h_in ? h_in[r] : 0.0f;
+      out[r] = (hin + moe) + sd;
+      if (moe_out) moe_out[r] = moe;
+    }
+    if (threadIdx.x == 0) reset_agent(counters + tile);
   }
 }
 
 hipError_t launch_gateup(const SlotTable& t, const XGroup* xd, float* act, XGroup* act_xd,
-                         hipStream_t s) {
-  hipLaunchKernelGGL(k_gateup, dim3(kFfn / 32, t.n_slots), dim3(256), 0, s, t, xd, act, act_xd);
+                         int* counters, const ExactRoute& r, hipStream_t s) {
+  const int grid = kGuTiles * t.n_slots + (r.scores ? 1 : 0);
+  hipLaunchKernelGGL(k_gateup, dim3(grid), dim3(256), 0, s, t, xd, act, act_xd, counters, r);
   return hipGetLastError();
 }
 
 hipError_t launch_down_combine(const SlotTable& t, bool down_q6, const XGroup* act_xd,
-                               const float* h_in, float* out, float* moe_out, hipStream_t s) {
-  const size_t lds = (size_t)t.n_slots * (kFfn / 64) * sizeof(XGroup);
-  const dim3 grid(kHidden / 16), block(256);
-  if (lds > 65536) {
-    // more than 13 slots: ask for the LDS beyond the 64 KiB default
-    const void* fn = down_q6 ? reinterpret_cast<const void*>(&k_down_combine<true>)
-                             : reinterpret_cast<const void*>(&k_down_combine<false>);
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-  }
+                               const float* h_in, float* out, float* moe_out, float* eo,
+                               int* counters, hipStream_t s) {
+  const dim3 grid(kDnTiles, t.n_slots), block(256);
   if (down_q6)
-    hipLaunchKernelGGL(k_down_combine<true>, grid, block, lds, s, t, act_xd, h_in, out, moe_out);
+    hipLaunchKernelGGL(k_down<true>, grid, block, 0, s, t, act_xd, h_in, out, moe_out, eo,
+                       counters);
   else
-    hipLaunchKernelGGL(k_down_combine<false>, grid, block, lds, s, t, act_xd, h_in, out,
-                       moe_out);
+    hipLaunchKernelGGL(k_down<false>, grid, block, 0, s, t, act_xd, h_in, out, moe_out, eo,
+                       counters);
   return hipGetLastError();
 }
 

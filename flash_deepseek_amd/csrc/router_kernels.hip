@@ -1,147 +1,16 @@
 // router_kernels.hip -- router logits and route() for DeepSeek-V3 noaux_tc
 // routing (infer.m:350-353, 376, 920-991).
 //
-// Exactness.  Indices must match the reference bit for bit, so both halves
-// of the router are defined operation by operation:
-//  - logits: partial t of 256 accumulates float4 chunks t, t+256, ... with
-//    one fma per element; the partials are reduced by an xor butterfly per
-//    wave and the four wave sums combined as (s0 + s1) + (s2 + s3).  The C
-//    restatement (oracle) sums in this same order.
-//  - sigmoid: 1/(1 + expf(-x)) with expf evaluated as a double-precision
-//    exp built from fma/mul/add (exp_det) and rounded once; float division
-//    and addition are IEEE, so the CPU and GPU agree bit for bit.
-//  - route: the reference's sequential semantics (running top-2 per group,
-//    strict-> group passes with lowest index winning ties, replace-the-
-//    first-minimum slot scan over experts in index order, weights summed in
-//    slot order) are reproduced by one wave: top-2 by a multiset butterfly,
-//    group choice by uniform passes, and the slot scan by ballots that jump
-//    straight to the next expert able to displace the current minimum.
+// Exactness.  Indices must match the reference bit for bit, so the logits
+// are defined operation by operation: partial t of 256 accumulates float4
+// chunks t, t+256, ... with one fma per element; the partials are reduced
+// by an xor butterfly per wave and the four wave sums combined as
+// (s0 + s1) + (s2 + s3).  The C restatement (oracle) sums in this same
+// order.  route() itself is in route_device.h.
 #include "fdm_internal.h"
+#include "route_device.h"
 
 namespace fdm {
-
-__device__ __noinline__ double exp_det(double x) {
-#pragma clang fp contract(off)
-  if (x != x) return x;
-  if (x > 709.0) return __builtin_inf();
-  if (x < -746.0) return 0.0;
-  const double inv_ln2 = 1.4426950408889634;
-  const double ln2_hi = 0x1.62e42fefa39efp-1;
-  const double ln2_lo = 0x1.abc9e3b39803fp-56;
-  const double t = x * inv_ln2;
-  const double k = floor(t + 0.5);
-  double r = fma(-k, ln2_hi, x);
-  r = fma(-k, ln2_lo, r);
-  const double inv_fact[14] = {1.0,         1.0,          1.0 / 2,       1.0 / 6,
-                               1.0 / 24,    1.0 / 120,    1.0 / 720,     1.0 / 5040,
-                               1.0 / 40320, 1.0 / 362880, 1.0 / 3628800, 1.0 / 39916800,
-                               1.0 / 479001600, 1.0 / 6227020800.0};
-  double p = inv_fact[13];
-#pragma unroll
-  for (int i = 12; i >= 0; --i) p = fma(p, r, inv_fact[i]);
-  return ldexp(p, (int)k);
-}
-
-__device__ __forceinline__ float sigmoid_det(float x) {
-#pragma clang fp contract(off)
-  const float e = (float)exp_det((double)(-x));
-  return __fdiv_rn(1.0f, 1.0f + e);
-}
-
-__device__ __forceinline__ float load_relaxed(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// route() for one token, executed by one full wave.  Expert i lives in
-// lane i % 64 of "chunk" i / 64; group of expert i = i / 32.
-// R1 geometry: 256 experts, 8 groups of 32, 4 groups kept.
-__device__ void route_wave(const float* logits, const float* bias, int K, float scale,
-                          int* __restrict__ idx_out, float* __restrict__ w_out) {
-#pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  float score[4], choice[4], gs_lane[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = 64 * j + lane;
-    score[j] = sigmoid_det(load_relaxed(logits + i));
-    choice[j] = score[j] + (bias ? bias[i] : 0.0f);
-    // running top-2 of the group = top-2 of the multiset of choices that
-    // exceed -1e30 (NaN never enters), padded with -1e30
-    float t1 = choice[j] > -1e30f ? choice[j] : -1e30f;
-    float t2 = -1e30f;
-#pragma unroll
-    for (int m = 16; m >= 1; m >>= 1) {
-      const float o1 = __shfl_xor(t1, m, 32);
-      const float o2 = __shfl_xor(t2, m, 32);
-      const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-      t1 = fmaxf(t1, o1);
-      t2 = n2;
-    }
-    gs_lane[j] = t1 + t2;
-  }
-  float gs[8];
-#pragma unroll
-  for (int G = 0; G < 8; ++G) gs[G] = __shfl(gs_lane[G >> 1], (G & 1) * 32);
-  unsigned selmask = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    int best = -1;
-    float bs = -1e30f;
-#pragma unroll
-    for (int G = 0; G < 8; ++G) {
-      if (!((selmask >> G) & 1u) && gs[G] > bs) {
-        bs = gs[G];
-        best = G;
-      }
-    }
-    if (best >= 0) selmask |= 1u << best;
-  }
-  // Slot scan.  Slot k lives in lane k (k < K <= 16).  mu / minslot are the
-  // current first minimum; candidates are re-balloted after each insertion.
-  float key = -1e30f;
-  int id = 0;
-  float mu = -1e30f;
-  int minslot = 0;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool in_sel = (selmask >> (2 * j + (lane >> 5))) & 1u;
-    const float v = in_sel ? choice[j] : -1e30f;
-    unsigned long long cand = __ballot(v > mu);
-    while (cand) {
-      const int l = __ffsll((unsigned long long)cand) - 1;
-      const float vl = __shfl(v, l);
-      if (lane == minslot) {
-        key = vl;
-        id = 64 * j + l;
-      }
-      float kk = lane < K ? key : __builtin_inff();
-      kk = fminf(kk, __shfl_xor(kk, 8));
-      kk = fminf(kk, __shfl_xor(kk, 4));
-      kk = fminf(kk, __shfl_xor(kk, 2));
-      kk = fminf(kk, __shfl_xor(kk, 1));
-      mu = __shfl(kk, 0);
-      const unsigned long long eq = __ballot(lane < K && key == mu);
-      minslot = __ffsll((unsigned long long)eq) - 1;
-      const unsigned long long later = (l == 63) ? 0ull : (~0ull << (l + 1));
-      cand = __ballot(v > mu) & later;
-    }
-  }
-  // Weights: unbiased scores of the picks, normalised in slot order.
-  const int jj = id >> 6, ll = id & 63;
-  const float s0 = __shfl(score[0], ll), s1 = __shfl(score[1], ll);
-  const float s2 = __shfl(score[2], ll), s3 = __shfl(score[3], ll);
-  float wv = jj == 0 ? s0 : (jj == 1 ? s1 : (jj == 2 ? s2 : s3));
-  float sum = 0.0f;
-  for (int k = 0; k < K; ++k) sum += __shfl(wv, k);
-  if (sum > 0.0f) {
-    const float f = __fdiv_rn(scale, sum);
-    wv *= f;
-  }
-  if (lane < K) {
-    idx_out[lane] = id;
-    w_out[lane] = wv;
-  }
-}
 
 // One router logit per (expert, token) in the canonical order; TPW tokens
 // share each load of the weight row.
@@ -196,61 +65,187 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
   route_wave(logits + (size_t)t * 256, bias, K, 2.5f, idx + (size_t)t * K, w + (size_t)t * K);
 }
 
-// Batch-1 front end of the MoE layer; 256 workgroups, one per expert.
+// Dot of one Q4_K group with fp32 activations x64 (the group's 64 values)
+// and their two sub-block sums: sum over the group of (d*sc*q - dmin*m)*x.
+__device__ __forceinline__ float q4k_group_dot_f32(const u32x4 hdr, const u32x4 q0, const u32x4 q1,
+                                                   const Q4KScaleSel& sel,
+                                                   const float* __restrict__ x64, float xs0,
+                                                   float xs1) {
+  const uint32_t wq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+  const f32x4* xv = reinterpret_cast<const f32x4*>(x64);
+  float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t lo = wq[i] & 0x0F0F0F0Fu, hi = (wq[i] >> 4) & 0x0F0F0F0Fu;
+    const f32x4 xl = xv[i], xh = xv[8 + i];
+    a0 = fmaf((float)(lo & 0xFF), xl.x, a0);
+    b0 = fmaf((float)((lo >> 8) & 0xFF), xl.y, b0);
+    a0 = fmaf((float)((lo >> 16) & 0xFF), xl.z, a0);
+    b0 = fmaf((float)(lo >> 24), xl.w, b0);
+    a1 = fmaf((float)(hi & 0xFF), xh.x, a1);
+    b1 = fmaf((float)((hi >> 8) & 0xFF), xh.y, b1);
+    a1 = fmaf((float)((hi >> 16) & 0xFF), xh.z, a1);
+    b1 = fmaf((float)(hi >> 24), xh.w, b1);
+  }
+  int sc0, m0, sc1, m1;
+  q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, sel, sc0, m0, sc1, m1);
+  const float d = half_to_float(hdr.x), dmin = half_to_float(hdr.x >> 16);
+  const float qx = fmaf((float)sc0, a0 + b0, (float)sc1 * (a1 + b1));
+  const float mx = fmaf((float)m0, xs0, (float)m1 * xs1);
+  return fmaf(d, qx, -dmin * mx);
+}
+
+// Batch-1 front end of the MoE layer, one launch of 512 workgroups:
+//  0..255    router row e (4 waves = the 4 canonical runs of 64 partials),
+//            stored as its sigmoid score; workgroups 0..27 also produce the
+//            digits of h_post (one 64-element group per wave).  Arrival is
+//            counted in two levels (16 groups of 16 workgroups, then the 16
+//            group finishers), so no counter sees more than 16 atomics; the
+//            last workgroup reads the 256 scores and selects the expert SET
+//            (route_set_wave) into prov_idx.  The exact reference slot order
+//            and weights are produced later, off the critical path, by the
+//            gate/up launch.
+//  256..511  gate/up + SwiGLU of the shared expert (which needs no routing)
+//            for 8 rows each, against fp32 h_post staged in LDS, while the
+//            router runs; the activation digits are finished as in k_gateup.
+constexpr int kRouterWGs = 256;
+constexpr int kArriveGroup = 16;
+constexpr int kCounterStride = 64;  // ints between counters (256 bytes)
+
 __global__ __launch_bounds__(256) void k_router_layer(const float* __restrict__ Wg,
                                                       const float* __restrict__ bias,
                                                       const float* __restrict__ h, int K,
-                                                      float* __restrict__ logits,
+                                                      float* __restrict__ scores,
                                                       XGroup* __restrict__ xd,
-                                                      int* __restrict__ idx,
-                                                      float* __restrict__ w,
-                                                      int* __restrict__ counter) {
+                                                      int* __restrict__ prov_idx,
+                                                      int* __restrict__ counters,
+                                                      const uint8_t* __restrict__ shared,
+                                                      float* __restrict__ act_s,
+                                                      XGroup* __restrict__ act_xd_s,
+                                                      int* __restrict__ gu_counters_s) {
 #pragma clang fp contract(off)
+  __shared__ float xf[kHidden];
+  __shared__ float xsum[kHidden / 32];
   __shared__ float red[4];
-  __shared__ int is_last;
-  const int e = blockIdx.x;
+  __shared__ int flag;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // digits of h_post: group e (112 groups of 64 elements)
-  if (e < kHidden / 64 && wave == 1) {
-    const float v = h[e * 64 + lane];
-    int8_t a, b;
-    float s, sum;
-    make_digits32(v, a, b, s, sum);
-    XGroup* g = xd + e;
-    g->a[lane] = a;
-    g->b[lane] = b;
-    if ((lane & 31) == 0) {
-      g->s[lane >> 5] = s;
-      g->xsum[lane >> 5] = sum;
+  if (blockIdx.x >= kRouterWGs) {
+    // ---- shared expert gate/up tile ----
+    const int tile = blockIdx.x - kRouterWGs;
+    const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
+    const int row = tile * 8 + 2 * wave + (q & 1);
+    const uint8_t* rowp = shared + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
+    Q4KGroupLoad ld[7];
+#pragma unroll
+    for (int i = 0; i < 7; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
+    const float4* h4 = reinterpret_cast<const float4*>(h);
+    for (int i = threadIdx.x; i < kHidden / 4; i += 256) reinterpret_cast<float4*>(xf)[i] = h4[i];
+    __syncthreads();
+    if (threadIdx.x < kHidden / 32) {
+      float sacc = 0.0f;
+      for (int k = 0; k < 32; ++k) sacc += xf[32 * threadIdx.x + k];
+      xsum[threadIdx.x] = sacc;
     }
+    __syncthreads();
+    const Q4KScaleSel sel = q4k_scale_sel(g);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) {
+      const int G = 16 * i + l16;
+      u32x4 hd;
+      hd.x = quad_bcast<0>(ld[i].hdr_part);
+      hd.y = quad_bcast<1>(ld[i].hdr_part);
+      hd.z = quad_bcast<2>(ld[i].hdr_part);
+      hd.w = quad_bcast<3>(ld[i].hdr_part);
+      acc += q4k_group_dot_f32(hd, ld[i].q0, ld[i].q1, sel, xf + 64 * G, xsum[2 * G],
+                               xsum[2 * G + 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    acc = sum16(acc);
+    const float up = __shfl(acc, (lane + 32) & 63);
+    if (lane == 0 || lane == 16) {
+      store_agent(act_s + row, silu_mul(acc, up));
+      wait_stores_done();
+    }
+    __syncthreads();
+    int* cnt = gu_counters_s + (tile >> 2);
+    if (threadIdx.x == 0) flag = (arrive_agent(cnt) == 3);
+    __syncthreads();
+    if (flag && threadIdx.x < 32) {
+      const float v = load_agent(act_s + (tile >> 2) * 32 + threadIdx.x);
+      int8_t a, b;
+      float sc, sum;
+      make_digits32(v, a, b, sc, sum);
+      XGroup* xg = act_xd_s + (tile >> 3);
+      const int half = (tile >> 2) & 1;
+      xg->a[32 * half + threadIdx.x] = a;
+      xg->b[32 * half + threadIdx.x] = b;
+      if (threadIdx.x == 0) {
+        xg->s[half] = sc;
+        xg->xsum[half] = sum;
+        reset_agent(cnt);
+      }
+    }
+    return;
   }
+  // ---- router row e ----
+  const int e = blockIdx.x;
+  const int t = 64 * wave + lane;  // canonical partial index
   const float4* w4 = reinterpret_cast<const float4*>(Wg + (size_t)e * kHidden);
   const float4* x4 = reinterpret_cast<const float4*>(h);
+  float4 wv[kHidden / 1024], xv[kHidden / 1024];
+#pragma unroll
+  for (int i = 0; i < kHidden / 1024; ++i) {
+    wv[i] = w4[t + 256 * i];
+    xv[i] = x4[t + 256 * i];
+  }
+  if (e < kHidden / 256) {
+    const int G = 4 * e + wave;
+    const float v = h[G * 64 + lane];
+    int8_t a, b;
+    float sc, sum;
+    make_digits32(v, a, b, sc, sum);
+    XGroup* gx = xd + G;
+    gx->a[lane] = a;
+    gx->b[lane] = b;
+    if ((lane & 31) == 0) {
+      gx->s[lane >> 5] = sc;
+      gx->xsum[lane >> 5] = sum;
+    }
+  }
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < kHidden / 1024; ++i) {
-    const int c = threadIdx.x + 256 * i;
-    const float4 wv = w4[c], xv = x4[c];
-    acc = fmaf(wv.x, xv.x, acc);
-    acc = fmaf(wv.y, xv.y, acc);
-    acc = fmaf(wv.z, xv.z, acc);
-    acc = fmaf(wv.w, xv.w, acc);
+    acc = fmaf(wv[i].x, xv[i].x, acc);
+    acc = fmaf(wv[i].y, xv[i].y, acc);
+    acc = fmaf(wv[i].z, xv[i].z, acc);
+    acc = fmaf(wv[i].w, xv[i].w, acc);
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
   if (lane == 0) red[wave] = acc;
   __syncthreads();
   if (threadIdx.x == 0) {
-    logits[e] = (red[0] + red[1]) + (red[2] + red[3]);
-    __threadfence();
-    const int done = atomicAdd(counter, 1);
-    is_last = (done == (int)gridDim.x - 1);
+    store_agent(scores + e, sigmoid_det((red[0] + red[1]) + (red[2] + red[3])));
+    wait_stores_done();
+    int* grp = counters + kCounterStride * (1 + e / kArriveGroup);
+    int last = 0;
+    if (arrive_agent(grp) == kArriveGroup - 1) {
+      reset_agent(grp);
+      last = arrive_agent(counters) == kRouterWGs / kArriveGroup - 1;
+    }
+    flag = last;
   }
   __syncthreads();
-  if (is_last) {
-    __threadfence();
-    if (wave == 0) route_wave(logits, bias, K, 2.5f, idx, w);
-    if (threadIdx.x == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (flag && wave == 0) {
+    float sc[4], bj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sc[j] = load_agent(scores + 64 * j + lane);
+      bj[j] = bias ? bias[64 * j + lane] : 0.0f;
+    }
+    route_set_wave(sc, bj, K, prov_idx);
+    if (lane == 0) reset_agent(counters);
   }
 }
 
@@ -273,10 +268,12 @@ hipError_t launch_route(const float* logits, const float* bias, int T, int K, in
 }
 
 hipError_t launch_router_layer(const float* Wg, const float* bias, const float* h_post, int K,
-                               float* logits, XGroup* xd, int* idx, float* w, int* counter,
-                               hipStream_t s) {
-  hipLaunchKernelGGL(k_router_layer, dim3(256), dim3(256), 0, s, Wg, bias, h_post, K, logits,
-                     xd, idx, w, counter);
+                               float* scores, XGroup* xd, int* prov_idx, int* counters,
+                               const uint8_t* shared, float* act_s, XGroup* act_xd_s,
+                               int* gu_counters_s, hipStream_t s) {
+  const int grid = kRouterWGs + (shared ? kFfn / 8 : 0);
+  hipLaunchKernelGGL(k_router_layer, dim3(grid), dim3(256), 0, s, Wg, bias, h_post, K, scores,
+                     xd, prov_idx, counters, shared, act_s, act_xd_s, gu_counters_s);
   return hipGetLastError();
 }
 

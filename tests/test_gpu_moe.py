@@ -27,9 +27,9 @@ def layer(request, fdm):
     fdm.release_layer(L)
 
 
-def oracle_layer(oracle, lay, h, h_in, K):
-    Wg = to_host(lay.Wg)
-    bias = to_host(lay.bias)
+def oracle_layer(oracle, lay, h, h_in, K, Wg=None, bias=None):
+    Wg = to_host(lay.Wg if Wg is None else Wg)
+    bias = to_host(lay.bias if bias is None else bias)
     ri, rw = oracle.route(oracle.router_logits(Wg, h), bias, K=K)
     moe = np.zeros(7168)
     for k in range(K):
@@ -38,26 +38,51 @@ def oracle_layer(oracle, lay, h, h_in, K):
     return ri, rw, moe, sd, h_in.astype(np.float64) + moe + sd
 
 
-@pytest.mark.parametrize("tok", [0, 1])
-def test_moe_layer(fdm, oracle, layer, tok):
+def run_layer(fdm, oracle, L, lay, K, tok, Wg=None, bias=None):
     import torch
-    L, lay = layer
-    K = 8
     h = oracle.synth_normal(7168, 0.0, 1.0, 500 + tok)
     h_in = oracle.synth_normal(7168, 0.0, 1.0, 600 + tok)
     hid = empty_f32(7168)
     idx = torch.empty(K, dtype=torch.int32, device="cuda")
     w = empty_f32(K)
-    say(f"moe_layer L={L} tok={tok}")
+    say(f"moe_layer L={L} K={K} tok={tok}")
     fdm.moe_layer(L, to_dev(h), to_dev(h_in), K, hid, idx, w)
     got, gi, gw = to_host(hid), to_host(idx), to_host(w)
-    ri, rw, moe, sd, want = oracle_layer(oracle, lay, h, h_in, K)
+    ri, rw, moe, sd, want = oracle_layer(oracle, lay, h, h_in, K, Wg, bias)
+    return h_in, got, gi, gw, ri, rw, moe, sd, want
+
+
+@pytest.mark.parametrize("K,tok", [(8, 0), (8, 1), (1, 2), (4, 3), (16, 4)])
+def test_moe_layer(fdm, oracle, layer, K, tok):
+    L, lay = layer
+    h_in, got, gi, gw, ri, rw, moe, sd, want = run_layer(fdm, oracle, L, lay, K, tok)
     assert np.array_equal(gi, ri)
     assert np.array_equal(gw.view(np.uint32), rw.view(np.uint32))
     err = rel_l2(got, want)
     err_moe = rel_l2(got.astype(np.float64) - h_in, moe + sd)
     print(f"idx={gi.tolist()} rel_l2={err:.3e} (moe part {err_moe:.3e})")
     assert err <= TOL and err_moe <= TOL
+
+
+@pytest.mark.parametrize("K", [5, 7])
+def test_moe_layer_tied_set(fdm, oracle, layer, K):
+    """Every router row and bias duplicated in adjacent experts (same group):
+    each choice occurs twice, so with K odd the K-th largest is tied with an
+    expert left out and the set itself depends on route()'s scan order."""
+    L, lay = layer
+    Wg = lay.Wg.clone()
+    Wg[1::2] = Wg[0::2]
+    bias = lay.bias.clone()
+    bias[1::2] = bias[0::2]
+    L2 = L + 20
+    fdm.attach_layer(L2, lay.experts, lay.expert_size, Wg, bias, lay.shared)
+    try:
+        h_in, got, gi, gw, ri, rw, moe, sd, want = run_layer(fdm, oracle, L2, lay, K, 9, Wg, bias)
+    finally:
+        fdm.release_layer(L2)
+    assert np.array_equal(gi, ri)
+    assert np.array_equal(gw.view(np.uint32), rw.view(np.uint32))
+    assert rel_l2(got, want) <= TOL
 
 
 def test_moe_forward_given_routing(fdm, oracle, layer):
