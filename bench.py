@@ -11,8 +11,8 @@ experts from HBM.  All inputs are already resident when timing starts.
 Prints one JSON line (rank 0):
   value        microseconds per token (lower is better)
   layer_gbps   algorithmic bytes per token / time per token
-  roofline     the dominant kernel (gate/up + SwiGLU over the 9 experts),
-               timed live with HIP events on the launch stream
+  roofline     the layer kernel (router, route, 9 experts, combine in one
+               launch), timed live with HIP events on the launch stream
   cpu_baseline the reference's CPU expert path (C restatement) on this
                host's cores, on a bounded sample of the same workload
 """
@@ -40,12 +40,6 @@ def layer_bytes(down, K=8):
     weights = slots * (2 * GATE_BYTES + DOWN_BYTES[down]) + ROUTER_BYTES
     acts = HIDDEN * 4 * 3  # h_post, h_in in; hidden out
     return weights + acts
-
-
-def gateup_bytes(K=8):
-    """Routed gate/up launch: the K selected experts' gate and up matrices
-    (the shared expert's run inside the router launch)."""
-    return K * 2 * GATE_BYTES + HIDDEN * 4 + K * FFN * 4  # W + x in + act out
 
 
 def load_traffic(kernel, workload):
@@ -144,16 +138,15 @@ def main():
         step(i)
     torch.cuda.synchronize()
     phases = {}
-    for name in ("router", "gateup", "down"):
+    for name in ("layer",):
         n, tot, mn, mx = F.prof_read(name)
         phases[name] = {"launches": n, "avg_us": round(tot / max(n, 1) * 1e3, 2),
                         "min_us": round(mn * 1e3, 2), "max_us": round(mx * 1e3, 2)}
     F.prof_enable(False)
 
-    gu_bytes = gateup_bytes(K)
-    gu_us = phases["gateup"]["avg_us"]
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
     lb = layer_bytes(args.down, K)
+    k_us = phases["layer"]["avg_us"]
+    achieved = lb / (k_us * 1e-6) / 1e9
     layer_gbps = lb / (us_per_token * 1e-6) / 1e9
     result = {
         "metric": METRIC,
@@ -182,14 +175,14 @@ def main():
         "layer_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
         "phases_us": phases,
         "roofline": {
-            "kernel": "k_gateup (gate+up matvecs + SwiGLU, 8 routed experts)",
+            "kernel": "k_layer (router + route + 8 routed and 1 shared expert + combine)",
             "bound": "hbm",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": load_traffic("k_gateup", "r1_batch1_q4k"),
-            "bytes_per_launch": gu_bytes,
+            "traffic": load_traffic("k_layer", f"r1_batch1_{args.down}"),
+            "bytes_per_launch": lb,
         },
         "cpu_baseline": None,
     }

@@ -156,7 +156,7 @@ def moe_layer(L, h_post, h_in, K, hidden, idx=None, w=None, stream=None):
 
 # ---- per-kernel GPU timing (HIP events; the moe_prof_t counterpart) --------------------
 PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
-          "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC}
+          "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER}
 
 
 def prof_enable(on=True):

@@ -18,7 +18,7 @@ FDM_E_NOMEM = -5
 FDM_E_SIZE = -6
 FDM_E_IO = -7
 
-PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC = range(5)
+PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER = range(6)
 
 QK_K = 256
 Q4K_BLOCK_SIZE = 144

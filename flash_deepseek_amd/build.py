@@ -23,6 +23,7 @@ SOURCES = [
     "matvec_kernels.hip",
     "router_kernels.hip",
     "moe_kernels.hip",
+    "layer_kernel.hip",
     "synth_kernels.hip",
     "capi.hip",
 ]

@@ -39,6 +39,10 @@ struct Workspace {
   float* logits = nullptr;    // FDM_MAX_TOKENS x 256 (the layer path: sigmoid scores)
   int* idx = nullptr;         // FDM_MAX_TOKENS x 16
   int* pidx = nullptr;        // the expert set the layer's slots run (FDM_MAX_K)
+  int* layer_cnt = nullptr;   // layer kernel arrival counters (kLayerCounters x stride)
+  unsigned* layer_flags = nullptr;  // layer kernel epoch flags (kLayerFlags x stride)
+  unsigned epoch = 0;         // last epoch handed to the layer kernel
+  unsigned err_reported = 0;  // last error epoch reported by fdm_stream_sync
   int* perm = nullptr;        // combine order over those slots (FDM_MAX_K)
   float* w = nullptr;         // FDM_MAX_TOKENS x 16
   float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
@@ -114,7 +118,8 @@ void free_workspace() {
   Workspace& w = g.ws;
   void* ptrs[] = {w.xd,       w.logits,   w.idx,     w.w,       w.act,
                   w.act_xd,   w.counter,  w.gu_count, w.dn_count, w.eo,
-                  w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w, w.pidx, w.perm};
+                  w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w, w.pidx, w.perm,
+                  w.layer_cnt, w.layer_flags};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -137,6 +142,10 @@ int alloc_workspace() {
   FDM_HIP(hipMalloc(&w.eo, (size_t)(FDM_MAX_K + 1) * FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.pidx, FDM_MAX_K * sizeof(int)));
   FDM_HIP(hipMalloc(&w.perm, FDM_MAX_K * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.layer_cnt, (size_t)kLayerCounters * kLayerStride * sizeof(int)));
+  FDM_HIP(hipMemset(w.layer_cnt, 0, (size_t)kLayerCounters * kLayerStride * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.layer_flags, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
+  FDM_HIP(hipMemset(w.layer_flags, 0, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
   FDM_HIP(hipMalloc(&w.stage_x, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_y, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_idx, FDM_MAX_K * sizeof(int)));
@@ -326,6 +335,16 @@ int fdm_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stream) {
 int fdm_stream_sync(void* stream) {
   if (int rc = check_ready()) return rc;
   FDM_HIP(hipStreamSynchronize(as_stream(stream)));
+  if (g.ws.epoch != 0) {
+    // the layer kernel records the epoch of a call whose waits timed out
+    unsigned err = 0;
+    FDM_HIP(hipMemcpy(&err, g.ws.layer_flags + kLayerFlagErr * kLayerStride, sizeof(err),
+                      hipMemcpyDeviceToHost));
+    if (err != 0 && err != g.ws.err_reported) {
+      g.ws.err_reported = err;
+      return fail(FDM_E_STATE, "fdm_moe_layer call %u timed out inside the kernel", err);
+    }
+  }
   return FDM_OK;
 }
 
@@ -608,32 +627,36 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   if (!d_h_post || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
   if (!aligned(d_h_post, 16)) return fail(FDM_E_INVAL, "h_post must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
-  int* idx = d_idx ? d_idx : g.ws.idx;
-  float* w = d_w ? d_w : g.ws.w;
+  LayerArgs a;
+  a.Wg = y->Wg;
+  a.bias = y->bias;
+  a.h = d_h_post;
+  a.h_in = d_h_in;
+  a.out = d_hidden;
+  a.moe_out = nullptr;
+  a.experts = y->experts;
+  a.expert_size = y->expert_size;
+  a.n_experts = y->n_experts;
+  a.shared = y->shared;
+  a.down_q6 = y->down_q6 ? 1 : 0;
+  a.K = K;
+  a.n_slots = K + (y->shared ? 1 : 0);
+  a.idx = d_idx ? d_idx : g.ws.idx;
+  a.w = d_w ? d_w : g.ws.w;
+  a.xd = g.ws.xd;
+  a.scores = g.ws.logits;
+  a.prov = g.ws.pidx;
+  a.perm = g.ws.perm;
+  a.act = g.ws.act;
+  a.act_xd = g.ws.act_xd;
+  a.eo = g.ws.eo;
+  a.counters = g.ws.layer_cnt;
+  a.flags = g.ws.layer_flags;
+  if (++g.ws.epoch == 0) ++g.ws.epoch;  // flags start at 0: skip epoch 0 on wrap
+  a.epoch = g.ws.epoch;
   {
-    ProfScope p(FDM_PROF_ROUTER, s);
-    // The router selects the expert set (pidx); the shared expert's gate/up
-    // runs inside the same launch (slot K).
-    FDM_HIP(launch_router_layer(y->Wg, y->bias, d_h_post, K, g.ws.logits, g.ws.xd, g.ws.pidx,
-                                g.ws.counter, y->shared, g.ws.act + (size_t)K * FDM_MOE_FFN,
-                                g.ws.act_xd + (size_t)K * (FDM_MOE_FFN / 64),
-                                g.ws.gu_count + K * 64, s));
-  }
-  // Slots run the experts of pidx; the combine takes the reference's slot
-  // order (idx/w) through perm, both written by the gate/up launch.
-  SlotTable t = slots_for(*y, g.ws.pidx, w, K, true);
-  t.perm = g.ws.perm;
-  {
-    ProfScope p(FDM_PROF_GATEUP, s);
-    SlotTable routed = t;
-    routed.n_slots = K;  // routed experts only
-    const ExactRoute r{g.ws.logits, y->bias, g.ws.pidx, idx, w, g.ws.perm};
-    FDM_HIP(launch_gateup(routed, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, r, s));
-  }
-  {
-    ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, d_h_in, d_hidden, nullptr, g.ws.eo,
-                                g.ws.dn_count, s));
+    ProfScope p(FDM_PROF_LAYER, s);
+    FDM_HIP(launch_layer(a, s));
   }
   return FDM_OK;
 }

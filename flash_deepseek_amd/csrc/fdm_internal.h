@@ -80,6 +80,45 @@ hipError_t launch_down_combine(const SlotTable& t, bool down_q6, const XGroup* a
                                const float* h_in, float* out, float* moe_out, float* eo,
                                int* counters, hipStream_t s);
 
+// layer_kernel.hip
+// The batch-1 MoE layer of one token in one launch: digits, router, route,
+// shared + routed experts, combine, residual.
+constexpr int kLayerStride = 64;                 // ints between counters / flags
+constexpr int kLayerMaxSlots = 17;               // FDM_MAX_K routed + 1 shared
+// counters: router (17), digits (1), act sub-blocks (17 x 64), slots (17),
+// down row tiles (224)
+constexpr int kLayerCounters = 17 + 1 + kLayerMaxSlots * 64 + kLayerMaxSlots + 224;
+constexpr int kLayerFlags = 24;                  // route, exact, error, digits, act[17]
+constexpr int kLayerFlagErr = 2;                 // flag slot of the timed-out epoch
+struct LayerArgs {
+  const float* Wg;         // router weights [256][7168] fp32
+  const float* bias;       // [256] or null
+  const float* h;          // h_post [7168]
+  const float* h_in;       // residual [7168] or null
+  float* out;              // hidden = h_in + moe + shared [7168]
+  float* moe_out;          // sum_k w_k E_k [7168] or null
+  const uint8_t* experts;  // n_experts packed blobs
+  size_t expert_size;
+  int n_experts;
+  const uint8_t* shared;   // shared expert blob or null
+  int down_q6;
+  int K;                   // routed experts
+  int n_slots;             // K (+1 with a shared expert)
+  int* idx;                // out: route() slot order [K]
+  float* w;                // out: route() weights [K]
+  XGroup* xd;              // workspace: digits of h [112]
+  float* scores;           // workspace: 256 sigmoid scores
+  int* prov;               // workspace: the expert set, one per slot [K]
+  int* perm;               // workspace: combine order over the slots [K]
+  float* act;              // workspace: [kLayerMaxSlots][2048]
+  XGroup* act_xd;          // workspace: [kLayerMaxSlots][32]
+  float* eo;               // workspace: [kLayerMaxSlots][7168]
+  int* counters;           // kLayerCounters x kLayerStride ints, zero at first use
+  unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
+  unsigned epoch;          // non-zero, different from the previous call's
+};
+hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
+
 // synth_kernels.hip
 hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);
 hipError_t launch_synth_q6k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);

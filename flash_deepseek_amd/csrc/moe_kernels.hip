@@ -131,45 +131,6 @@ __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __res
   }
 }
 
-// Raw words of one 128-element half of a Q6_K block, loaded from
-// dword-aligned addresses (a block starts at any even byte offset).
-struct Q6KHalfLoad {
-  uint32_t ql[17], qh[9];
-  uint32_t sc[2];
-  uint32_t d;
-  uint32_t shift;
-};
-
-__device__ __forceinline__ Q6KHalfLoad q6k_load_half(const uint8_t* blk, int h) {
-  Q6KHalfLoad r;
-  const uintptr_t a0 = reinterpret_cast<uintptr_t>(blk + 64 * h);
-  r.shift = a0 & 3u;
-  const uint32_t* p = reinterpret_cast<const uint32_t*>(a0 - r.shift);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) r.ql[i] = p[i];
-  r.ql[16] = r.shift ? p[16] : 0u;
-  const uint32_t* ph =
-      reinterpret_cast<const uint32_t*>(reinterpret_cast<uintptr_t>(blk + 128 + 32 * h) - r.shift);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r.qh[i] = ph[i];
-  r.qh[8] = r.shift ? ph[8] : 0u;
-  const uint16_t* s16 = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * h);
-  r.sc[0] = (uint32_t)s16[0] | ((uint32_t)s16[1] << 16);
-  r.sc[1] = (uint32_t)s16[2] | ((uint32_t)s16[3] << 16);
-  r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
-  return r;
-}
-
-__device__ __forceinline__ float q6k_half_dot_ld(const Q6KHalfLoad& r,
-                                                 const XGroup* __restrict__ xg) {
-  uint32_t ql[16], qh[8];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) ql[i] = funnel(r.ql[i], r.ql[i + 1], r.shift);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) qh[i] = funnel(r.qh[i], r.qh[i + 1], r.shift);
-  return half_to_float(r.d) * q6k_half_dot(ql, qh, r.sc, xg, xg + 1);
-}
-
 constexpr int kDnRows = 16;                   // down rows per workgroup
 constexpr int kDnTiles = kHidden / kDnRows;   // 448
 

@@ -78,28 +78,45 @@ __device__ __forceinline__ int sort_key(float f) {
   return b >= 0 ? b : b ^ 0x7FFFFFFF;
 }
 
-// The replace-the-first-minimum slot scan of route() (infer.m:970-990) on
-// wave-uniform state.  vk: order-preserving keys of the masked choices,
-// expert 64j + lane in vk[j]; score: the unbiased sigmoid scores.  Keys,
-// ids and scores of the K slots live in scalar registers; the next
+// Maximum of an int over the whole wave (DPP within rows of 16, then the
+// four row results).
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x111, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x112, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x114, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x118, 0xF, 0xF, false));
+  const int a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
+  const int c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
+  return max(max(a, b), max(c, d));
+}
+
+// Minimum of an int over the whole wave.
+__device__ __forceinline__ int wave_min_i32(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x111, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x112, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x114, 0xF, 0xF, false));
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x118, 0xF, 0xF, false));
+  const int a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
+  const int c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
+  return min(min(a, b), min(c, d));
+}
+
+// The replace-the-first-minimum slot scan of route() (infer.m:970-990).
+// vk: order-preserving keys of the masked choices, expert 64j + lane in
+// vk[j]; score: the unbiased sigmoid scores.  Slot k lives in lane k (key,
+// id, score; lanes >= K hold a key no slot minimum can be).  The next
 // candidate is the first later expert whose key beats the current first
-// minimum (a ballot), re-evaluated after every insertion.  On return lane k
-// (k < K) holds slot k's expert id and normalised weight.
-template <int K>
-__device__ __forceinline__ void slot_scan(const int vk[4], const float score[4], float scale,
-                                          int& id_out, float& w_out) {
+// minimum (a ballot), re-evaluated after every insertion.  On return lane
+// k (k < K) holds slot k's expert id and normalised weight.
+__device__ __forceinline__ void slot_scan(const int vk[4], const float score[4], int K,
+                                          float scale, int& id_out, float& w_out) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int init = sort_key(-1e30f);
   // a slot never filled keeps expert 0, as exp_idx starts zeroed
-  const int score0 = __builtin_amdgcn_readlane(__float_as_int(score[0]), 0);
-  int skey[K], sid[K], ssc[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    skey[k] = init;
-    sid[k] = 0;
-    ssc[k] = score0;
-  }
+  int skey = lane < K ? init : INT_MAX;
+  int sid = 0;
+  float ssc = readlane_f(score[0], 0);
   int mu = init, ms = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -107,37 +124,24 @@ __device__ __forceinline__ void slot_scan(const int vk[4], const float score[4],
     while (cand) {
       const int l = __ffsll((unsigned long long)cand) - 1;
       const int vl = __builtin_amdgcn_readlane(vk[j], l);
-      const int sl = __builtin_amdgcn_readlane(__float_as_int(score[j]), l);
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        const bool hit = k == ms;
-        skey[k] = hit ? vl : skey[k];
-        sid[k] = hit ? 64 * j + l : sid[k];
-        ssc[k] = hit ? sl : ssc[k];
+      const float sl = readlane_f(score[j], l);
+      if (lane == ms) {
+        skey = vl;
+        sid = 64 * j + l;
+        ssc = sl;
       }
-      mu = skey[0];
-#pragma unroll
-      for (int k = 1; k < K; ++k) mu = min(mu, skey[k]);
-      ms = K - 1;
-#pragma unroll
-      for (int k = K - 2; k >= 0; --k) ms = skey[k] == mu ? k : ms;
+      mu = wave_min_i32(skey);
+      ms = __ffsll((unsigned long long)__ballot(skey == mu)) - 1;
       const unsigned long long later = (l == 63) ? 0ull : (~0ull << (l + 1));
       cand = __ballot(vk[j] > mu) & later;
     }
   }
   // Weights: unbiased scores of the picks, summed and scaled in slot order.
   float sum = 0.0f;
-#pragma unroll
-  for (int k = 0; k < K; ++k) sum += __int_as_float(ssc[k]);
+  for (int k = 0; k < K; ++k) sum += readlane_f(ssc, k);
   const float f = sum > 0.0f ? __fdiv_rn(scale, sum) : 1.0f;
-  int id = 0, sc = 0;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    id = lane == k ? sid[k] : id;
-    sc = lane == k ? ssc[k] : sc;
-  }
-  id_out = id;
-  w_out = sum > 0.0f ? __int_as_float(sc) * f : __int_as_float(sc);
+  id_out = sid;
+  w_out = sum > 0.0f ? ssc * f : ssc;
 }
 
 // The first half of route() for one token held in registers (lane l holds
@@ -192,33 +196,24 @@ __device__ __forceinline__ void route_keys(const float score[4], const float bj[
   }
 }
 
-__device__ __forceinline__ void slot_scan_dispatch(int K, const int vk[4], const float score[4],
-                                                   float scale, int& id, float& wv) {
-  switch (K) {
-#define FDM_SCAN_CASE(N) \
-  case N:                \
-    slot_scan<N>(vk, score, scale, id, wv); \
-    break;
-    FDM_SCAN_CASE(1) FDM_SCAN_CASE(2) FDM_SCAN_CASE(3) FDM_SCAN_CASE(4)
-    FDM_SCAN_CASE(5) FDM_SCAN_CASE(6) FDM_SCAN_CASE(7) FDM_SCAN_CASE(8)
-    FDM_SCAN_CASE(9) FDM_SCAN_CASE(10) FDM_SCAN_CASE(11) FDM_SCAN_CASE(12)
-    FDM_SCAN_CASE(13) FDM_SCAN_CASE(14) FDM_SCAN_CASE(15) FDM_SCAN_CASE(16)
-#undef FDM_SCAN_CASE
-    default:
-      break;
-  }
-}
-
 // route() for one token, executed by one full wave with the sigmoid scores
-// in registers: exact reference selection, tie rules and slot order.
-__device__ inline void route_scores_wave(const float score[4], const float bj[4], int K, float scale,
-                                  int* __restrict__ idx_out, float* __restrict__ w_out) {
-  const int lane = threadIdx.x & 63;
+// in registers: exact reference selection, tie rules and slot order.  Lane
+// k (k < K) receives slot k's expert id and weight.
+__device__ __forceinline__ void route_exact_lane(const float score[4], const float bj[4], int K,
+                                        float scale, int& id, float& wv) {
   int vk[4];
   route_keys(score, bj, vk);
-  int id = 0;
-  float wv = 0.0f;
-  slot_scan_dispatch(K, vk, score, scale, id, wv);
+  id = 0;
+  wv = 0.0f;
+  slot_scan(vk, score, K, scale, id, wv);
+}
+
+__device__ __forceinline__ void route_scores_wave(const float score[4], const float bj[4], int K, float scale,
+                                  int* __restrict__ idx_out, float* __restrict__ w_out) {
+  const int lane = threadIdx.x & 63;
+  int id;
+  float wv;
+  route_exact_lane(score, bj, K, scale, id, wv);
   if (lane < K) {
     idx_out[lane] = id;
     w_out[lane] = wv;
@@ -226,7 +221,7 @@ __device__ inline void route_scores_wave(const float score[4], const float bj[4]
 }
 
 // route() reading the token's logits (and bias) from memory.
-__device__ inline void route_wave(const float* logits, const float* bias, int K, float scale,
+__device__ __forceinline__ void route_wave(const float* logits, const float* bias, int K, float scale,
                           int* __restrict__ idx_out, float* __restrict__ w_out) {
   const int lane = threadIdx.x & 63;
   float score[4], bj[4];
@@ -238,18 +233,6 @@ __device__ inline void route_wave(const float* logits, const float* bias, int K,
   route_scores_wave(score, bj, K, scale, idx_out, w_out);
 }
 
-// Maximum of an int over the whole wave (DPP within rows of 16, then the
-// four row results).
-__device__ __forceinline__ int wave_max_i32(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x111, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x112, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x114, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x118, 0xF, 0xF, false));
-  const int a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
-  const int c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
-  return max(max(a, b), max(c, d));
-}
-
 // The SET of experts route() selects, found in parallel: K extractions of
 // the wave maximum of the masked keys.  The sequential slot scan always
 // ends holding K elements that are >= everything it does not hold, so when
@@ -258,13 +241,11 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 // scan) when the K-th key is tied with a candidate left out, or when fewer
 // than K candidates exceed -1e30.  On success lane k (k < K) receives the
 // k-th extracted expert id; the order (descending key) is provisional.
-template <int K>
-__device__ __forceinline__ bool topk_set(const int vk_in[4], int& id_out) {
+__device__ __forceinline__ bool topk_set(const int vk_in[4], int K, int& id_out) {
   const int lane = threadIdx.x & 63;
   const int floor_key = sort_key(-1e30f);
   int v[4] = {vk_in[0], vk_in[1], vk_in[2], vk_in[3]};
   int id = 0, m = INT_MIN;
-#pragma unroll
   for (int k = 0; k < K; ++k) {
     m = wave_max_i32(max(max(v[0], v[1]), max(v[2], v[3])));
     if (m <= floor_key) return false;
@@ -274,7 +255,9 @@ __device__ __forceinline__ bool topk_set(const int vk_in[4], int& id_out) {
       const unsigned long long b = __ballot(v[j] == m);
       if (b) pick = 64 * j + __ffsll(b) - 1;  // lowest expert index holding m
     }
-    if (lane == (pick & 63)) v[pick >> 6] = INT_MIN;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)  // constant indices only: v stays in registers
+      if (j == (pick >> 6) && lane == (pick & 63)) v[j] = INT_MIN;
     if (lane == k) id = pick;
   }
   const bool tie = __ballot(v[0] == m || v[1] == m || v[2] == m || v[3] == m) != 0ull;
@@ -283,35 +266,27 @@ __device__ __forceinline__ bool topk_set(const int vk_in[4], int& id_out) {
 }
 
 // Critical-path routing for the batch-1 layer: group limit and the expert
-// set (topk_set) from the sigmoid scores, written to prov_idx[0..K).  When
-// the set is ambiguous (a tie at the K-th key, or fewer than K candidates),
-// the exact reference scan runs here instead and prov_idx is the reference
-// slot order.
-__device__ inline void route_set_wave(const float score[4], const float bj[4], int K,
-                               int* __restrict__ prov_idx) {
+// set (topk_set) from the sigmoid scores; lane k (k < K) receives the k-th
+// expert of the set.  When the set is ambiguous (a tie at the K-th key, or
+// fewer than K candidates), the exact reference scan runs instead and the
+// lanes hold the reference slot order.
+__device__ __forceinline__ int route_set_lane(const float score[4], const float bj[4], int K) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
   int vk[4];
   route_keys(score, bj, vk);
   int id = 0;
-  bool ok = false;
-  switch (K) {
-#define FDM_SET_CASE(N) \
-  case N:               \
-    ok = topk_set<N>(vk, id); \
-    break;
-    FDM_SET_CASE(1) FDM_SET_CASE(2) FDM_SET_CASE(3) FDM_SET_CASE(4)
-    FDM_SET_CASE(5) FDM_SET_CASE(6) FDM_SET_CASE(7) FDM_SET_CASE(8)
-    FDM_SET_CASE(9) FDM_SET_CASE(10) FDM_SET_CASE(11) FDM_SET_CASE(12)
-    FDM_SET_CASE(13) FDM_SET_CASE(14) FDM_SET_CASE(15) FDM_SET_CASE(16)
-#undef FDM_SET_CASE
-    default:
-      break;
-  }
+  const bool ok = topk_set(vk, K, id);
   if (!ok) {
     float wv;
-    slot_scan_dispatch(K, vk, score, 2.5f, id, wv);
+    slot_scan(vk, score, K, 2.5f, id, wv);
   }
+  return id;
+}
+
+__device__ __forceinline__ void route_set_wave(const float score[4], const float bj[4], int K,
+                                      int* __restrict__ prov_idx) {
+  const int lane = threadIdx.x & 63;
+  const int id = route_set_lane(score, bj, K);
   if (lane < K) prov_idx[lane] = id;
 }
 

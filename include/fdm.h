@@ -142,7 +142,11 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
  * shared expert, combine, and the residual:
  *   hidden = h_in + sum_k w[k] E_k(h_post) + S(h_post).
  * d_h_in may be NULL (no residual).  d_idx / d_w (optional) receive the
- * routing. */
+ * routing.  One cooperative launch; calls on one device must not overlap
+ * (they share the library's workspace).  A launch whose internal waits
+ * time out (never expected; it would mean a broken device) completes with
+ * an unspecified result and makes the next fdm_stream_sync return
+ * FDM_E_STATE. */
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
 
@@ -151,12 +155,13 @@ int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, floa
  * every kernel of the entry points above.  fdm_prof_read synchronises on
  * the recorded events and returns the count, total, min and max duration
  * (milliseconds) of one phase since the last reset. */
-#define FDM_PROF_ROUTER 0   /* router logits + digits of h_post + route */
-#define FDM_PROF_GATEUP 1   /* gate/up matvecs + SwiGLU, all slots      */
-#define FDM_PROF_DOWN 2     /* down matvecs + combine (+ residual)      */
+#define FDM_PROF_ROUTER 0   /* fdm_router_logits / fdm_route kernels    */
+#define FDM_PROF_GATEUP 1   /* gate/up matvecs + SwiGLU (routing given) */
+#define FDM_PROF_DOWN 2     /* down matvecs + combine (routing given)   */
 #define FDM_PROF_XDIGITS 3  /* activation digits (routing given)        */
 #define FDM_PROF_MATVEC 4   /* fdm_matvec_q4k / _q6k kernel             */
-#define FDM_PROF_PHASES 5
+#define FDM_PROF_LAYER 5    /* fdm_moe_layer: the whole layer, 1 launch */
+#define FDM_PROF_PHASES 6
 int fdm_prof_enable(int on);
 int fdm_prof_reset(void);
 int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);
