@@ -40,6 +40,7 @@ struct Workspace {
   int* idx = nullptr;         // FDM_MAX_TOKENS x 16
   int* pidx = nullptr;        // the expert set the layer's slots run (FDM_MAX_K)
   int* layer_cnt = nullptr;   // layer kernel arrival counters (kLayerCounters x stride)
+  uint64_t* layer_tagged = nullptr;  // layer kernel tagged words (kLayerTagged)
   unsigned* layer_flags = nullptr;  // layer kernel epoch flags (kLayerFlags x stride)
   unsigned epoch = 0;         // last epoch handed to the layer kernel
   unsigned err_reported = 0;  // last error epoch reported by fdm_stream_sync
@@ -119,7 +120,7 @@ void free_workspace() {
   void* ptrs[] = {w.xd,       w.logits,   w.idx,     w.w,       w.act,
                   w.act_xd,   w.counter,  w.gu_count, w.dn_count, w.eo,
                   w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w, w.pidx, w.perm,
-                  w.layer_cnt, w.layer_flags};
+                  w.layer_cnt, w.layer_flags, w.layer_tagged};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -146,6 +147,8 @@ int alloc_workspace() {
   FDM_HIP(hipMemset(w.layer_cnt, 0, (size_t)kLayerCounters * kLayerStride * sizeof(int)));
   FDM_HIP(hipMalloc(&w.layer_flags, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
   FDM_HIP(hipMemset(w.layer_flags, 0, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
+  FDM_HIP(hipMalloc(&w.layer_tagged, kLayerTagged * sizeof(uint64_t)));
+  FDM_HIP(hipMemset(w.layer_tagged, 0, kLayerTagged * sizeof(uint64_t)));
   FDM_HIP(hipMalloc(&w.stage_x, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_y, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_idx, FDM_MAX_K * sizeof(int)));
@@ -644,12 +647,13 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   a.idx = d_idx ? d_idx : g.ws.idx;
   a.w = d_w ? d_w : g.ws.w;
   a.xd = g.ws.xd;
-  a.scores = g.ws.logits;
-  a.prov = g.ws.pidx;
-  a.perm = g.ws.perm;
-  a.act = g.ws.act;
-  a.act_xd = g.ws.act_xd;
-  a.eo = g.ws.eo;
+  uint64_t* tg = g.ws.layer_tagged;
+  a.scores = tg;
+  a.prov = tg + 256;
+  a.route_w = tg + 256 + 16;
+  a.route_perm = tg + 256 + 32;
+  a.act = tg + 256 + 48;
+  a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
   a.counters = g.ws.layer_cnt;
   a.flags = g.ws.layer_flags;
   if (++g.ws.epoch == 0) ++g.ws.epoch;  // flags start at 0: skip epoch 0 on wrap

@@ -333,18 +333,32 @@ __device__ __forceinline__ void reset_agent(int* counter) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
-// Digits of the 32 elements of one sub-block.  Called by all 32 lanes of a
-// half-wave (lane index `l` 0..31 within it), each holding one element v.
-// Returns a / b digits for the lane and the sub-block's scale and exact sum.
+// Reduction of v over each half-wave (lanes 0-31 and 32-63) by DPP: row
+// shifts within rows of 16, then row_bcast:15 folds rows 0/2 into rows 1/3;
+// every lane receives its half's result (readlane of lane 31 / 63).
+template <bool MAX>
+__device__ __forceinline__ float half_reduce(float v) {
+  const auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
+  const int fill = MAX ? __float_as_int(-__builtin_inff()) : 0;
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(v), 0x111, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(v), 0x112, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(v), 0x114, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(v), 0x118, 0xF, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+  const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+  return (threadIdx.x & 32) ? hi : lo;
+}
+
+// Digits of the 32 elements of one sub-block.  Called by all 64 lanes of a
+// wave; each half-wave (lanes 0-31, 32-63) is one sub-block and each lane
+// holds one element v.  Returns the a / b digits for the lane and the
+// sub-block's scale and fp32 sum (summed in one fixed order, so every
+// caller gets the same bits for the same elements).
 __device__ __forceinline__ void make_digits32(float v, int8_t& a_out, int8_t& b_out,
                                               float& s_out, float& sum_out) {
-  float amax = fabsf(v);
-  float sum = v;
-#pragma unroll
-  for (int m = 16; m >= 1; m >>= 1) {
-    amax = fmaxf(amax, __shfl_xor(amax, m, 32));
-    sum += __shfl_xor(sum, m, 32);
-  }
+  const float amax = half_reduce<true>(fabsf(v));
+  const float sum = half_reduce<false>(v);
   int a = 0, b = 0;
   float s;
   if (amax > 0.0f && amax <= 3.4028234e38f) {

@@ -82,14 +82,16 @@ hipError_t launch_down_combine(const SlotTable& t, bool down_q6, const XGroup* a
 
 // layer_kernel.hip
 // The batch-1 MoE layer of one token in one launch: digits, router, route,
-// shared + routed experts, combine, residual.
+// shared + routed experts, combine, residual.  Values handed between
+// workgroups are tagged 64-bit words {epoch, payload}.
 constexpr int kLayerStride = 64;                 // ints between counters / flags
 constexpr int kLayerMaxSlots = 17;               // FDM_MAX_K routed + 1 shared
-// counters: router (17), digits (1), act sub-blocks (17 x 64), slots (17),
-// down row tiles (224)
-constexpr int kLayerCounters = 17 + 1 + kLayerMaxSlots * 64 + kLayerMaxSlots + 224;
-constexpr int kLayerFlags = 24;                  // route, exact, error, digits, act[17]
+constexpr int kLayerCounters = 1;                // arrivals of the digit items
+constexpr int kLayerFlags = 4;                   // digits ready, -, error, -
 constexpr int kLayerFlagErr = 2;                 // flag slot of the timed-out epoch
+// tagged words: scores 256, prov 16, route_w 16, route_perm 16,
+// act 17 x 2048, eo 17 x 7168
+constexpr size_t kLayerTagged = 256 + 3 * 16 + (size_t)kLayerMaxSlots * (2048 + 7168);
 struct LayerArgs {
   const float* Wg;         // router weights [256][7168] fp32
   const float* bias;       // [256] or null
@@ -107,15 +109,15 @@ struct LayerArgs {
   int* idx;                // out: route() slot order [K]
   float* w;                // out: route() weights [K]
   XGroup* xd;              // workspace: digits of h [112]
-  float* scores;           // workspace: 256 sigmoid scores
-  int* prov;               // workspace: the expert set, one per slot [K]
-  int* perm;               // workspace: combine order over the slots [K]
-  float* act;              // workspace: [kLayerMaxSlots][2048]
-  XGroup* act_xd;          // workspace: [kLayerMaxSlots][32]
-  float* eo;               // workspace: [kLayerMaxSlots][7168]
+  uint64_t* scores;        // tagged: 256 sigmoid scores
+  uint64_t* prov;          // tagged: the expert set, one per slot [K]
+  uint64_t* route_w;       // tagged: weights in the reference's slot order [K]
+  uint64_t* route_perm;    // tagged: slot running the k-th expert of that order [K]
+  uint64_t* act;           // tagged: [kLayerMaxSlots][2048]
+  uint64_t* eo;            // tagged: [kLayerMaxSlots][7168]
   int* counters;           // kLayerCounters x kLayerStride ints, zero at first use
   unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
-  unsigned epoch;          // non-zero, different from the previous call's
+  unsigned epoch;          // non-zero, different from every earlier call's
 };
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
 
