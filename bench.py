@@ -33,6 +33,7 @@ GATE_BYTES = 57344 * 144                     # one Q4_K 2048 x 7168 matrix
 DOWN_BYTES = {"q4k": 57344 * 144, "q6k": 57344 * 210}
 ROUTER_BYTES = 256 * 7168 * 4 + 256 * 4      # W_g + bias
 HIDDEN, FFN = 7168, 2048
+COPY_BYTES = 256 << 20   # calibration copy of the counter passes
 
 
 def layer_bytes(down, K=8):
@@ -90,6 +91,9 @@ def main():
     ap.add_argument("--prof-steps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="counter-collection run: a few layer steps, then plain 256 MiB "
+                         "copies (read + write of known size) that calibrate the counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -120,6 +124,19 @@ def main():
 
     def step(i):
         F.moe_layer(3 + i % args.layers, h_post[i], h_in[i], K, out[i], stream=stream)
+
+    if args.pmc_workload:
+        for i in range(min(n_tok, 40)):
+            step(i)
+        n = COPY_BYTES // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes 256 MiB
+        torch.cuda.synchronize()
+        print(json.dumps({"pmc_workload": True, "layer_steps": min(n_tok, 40),
+                          "copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
+        return
 
     for i in range(args.warmup):
         step(i)
@@ -181,7 +198,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": load_traffic("k_layer", f"r1_batch1_{args.down}"),
+            "traffic": load_traffic("k_layer", f"deepseek_r1_batch1_{args.down}"),
             "bytes_per_launch": lb,
         },
         "cpu_baseline": None,

@@ -38,17 +38,14 @@ struct Workspace {
   XGroup* xd = nullptr;       // digits of activations (up to FDM_MAX_TOKENS x 112)
   float* logits = nullptr;    // FDM_MAX_TOKENS x 256 (the layer path: sigmoid scores)
   int* idx = nullptr;         // FDM_MAX_TOKENS x 16
-  int* pidx = nullptr;        // the expert set the layer's slots run (FDM_MAX_K)
   int* layer_cnt = nullptr;   // layer kernel arrival counters (kLayerCounters x stride)
   uint64_t* layer_tagged = nullptr;  // layer kernel tagged words (kLayerTagged)
   unsigned* layer_flags = nullptr;  // layer kernel epoch flags (kLayerFlags x stride)
   unsigned epoch = 0;         // last epoch handed to the layer kernel
   unsigned err_reported = 0;  // last error epoch reported by fdm_stream_sync
-  int* perm = nullptr;        // combine order over those slots (FDM_MAX_K)
   float* w = nullptr;         // FDM_MAX_TOKENS x 16
   float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
   XGroup* act_xd = nullptr;   // (FDM_MAX_K + 1) x 32
-  int* counter = nullptr;     // arrival counters of the router (two levels)
   int* gu_count = nullptr;    // arrival counters: (FDM_MAX_K + 1) x 64 act sub-blocks
   int* dn_count = nullptr;    // arrival counters: 448 down row tiles
   float* eo = nullptr;        // per-slot expert outputs (FDM_MAX_K + 1) x 7168
@@ -118,8 +115,8 @@ int down_type(size_t expert_size, bool* q6) {
 void free_workspace() {
   Workspace& w = g.ws;
   void* ptrs[] = {w.xd,       w.logits,   w.idx,     w.w,       w.act,
-                  w.act_xd,   w.counter,  w.gu_count, w.dn_count, w.eo,
-                  w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w, w.pidx, w.perm,
+                  w.act_xd,   w.gu_count, w.dn_count, w.eo,
+                  w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w,
                   w.layer_cnt, w.layer_flags, w.layer_tagged};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
@@ -134,15 +131,11 @@ int alloc_workspace() {
   FDM_HIP(hipMalloc(&w.w, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(float)));
   FDM_HIP(hipMalloc(&w.act, (size_t)(FDM_MAX_K + 1) * FDM_MOE_FFN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.act_xd, (size_t)(FDM_MAX_K + 1) * (FDM_MOE_FFN / 64) * sizeof(XGroup)));
-  FDM_HIP(hipMalloc(&w.counter, kRouterCounterInts * sizeof(int)));
-  FDM_HIP(hipMemset(w.counter, 0, kRouterCounterInts * sizeof(int)));
   FDM_HIP(hipMalloc(&w.gu_count, (FDM_MAX_K + 1) * 64 * sizeof(int)));
   FDM_HIP(hipMemset(w.gu_count, 0, (FDM_MAX_K + 1) * 64 * sizeof(int)));
   FDM_HIP(hipMalloc(&w.dn_count, 448 * sizeof(int)));
   FDM_HIP(hipMemset(w.dn_count, 0, 448 * sizeof(int)));
   FDM_HIP(hipMalloc(&w.eo, (size_t)(FDM_MAX_K + 1) * FDM_HIDDEN * sizeof(float)));
-  FDM_HIP(hipMalloc(&w.pidx, FDM_MAX_K * sizeof(int)));
-  FDM_HIP(hipMalloc(&w.perm, FDM_MAX_K * sizeof(int)));
   FDM_HIP(hipMalloc(&w.layer_cnt, (size_t)kLayerCounters * kLayerStride * sizeof(int)));
   FDM_HIP(hipMemset(w.layer_cnt, 0, (size_t)kLayerCounters * kLayerStride * sizeof(int)));
   FDM_HIP(hipMalloc(&w.layer_flags, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
@@ -234,7 +227,6 @@ SlotTable slots_for(const Layer& L, const int* idx, const float* w, int K, bool 
   t.shared = with_shared ? L.shared : nullptr;
   t.idx = idx;
   t.w = w;
-  t.perm = nullptr;
   t.K = K;
   t.n_slots = K + ((with_shared && L.shared) ? 1 : 0);
   return t;
@@ -455,7 +447,7 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   }
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, ExactRoute{}, s));
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);
@@ -596,7 +588,7 @@ int fdm_moe_forward(int L, const float* d_h_post, const int* d_idx, const float*
   }
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, ExactRoute{}, s));
+    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);

@@ -29,19 +29,6 @@ hipError_t launch_router_logits(const float* Wg, const float* x, int n_exp, int 
                                 float* logits, hipStream_t s);
 hipError_t launch_route(const float* logits, const float* bias, int T, int K, int* idx,
                         float* w, hipStream_t s);
-// Batch-1 layer front end, one launch: the sigmoid scores of the 256 R1
-// experts for h_post (scores[256]), the digits of h_post (xd, 112 groups),
-// the SET of K experts route() selects into prov_idx[K] (in the last router
-// workgroup to finish; the order is provisional unless the set was tied),
-// and, when `shared` is not null, the shared expert's gate/up + SwiGLU into
-// act_s[2048] with its digits in act_xd_s[32] (gu_counters_s: 64 of the
-// gate/up arrival counters).  `counters`: kRouterCounterInts ints, zero on
-// entry and left zero.
-constexpr int kRouterCounterInts = 17 * 64;
-hipError_t launch_router_layer(const float* Wg, const float* bias, const float* h_post, int K,
-                               float* scores, XGroup* xd, int* prov_idx, int* counters,
-                               const uint8_t* shared, float* act_s, XGroup* act_xd_s,
-                               int* gu_counters_s, hipStream_t s);
 
 // moe_kernels.hip
 struct SlotTable {
@@ -50,28 +37,15 @@ struct SlotTable {
   int n_experts;
   const uint8_t* shared;   // slot K (may be null)
   const int* idx;          // K routed expert ids (device), one per slot
-  const float* w;          // K routing weights (device), in combine order
-  const int* perm;         // combine order: k-th term is slot perm[k] (null: k)
+  const float* w;          // K routing weights (device)
   int K;                   // routed slots
   int n_slots;             // K or K + 1 (shared)
-};
-// The exact route() of one token, run by one extra workgroup of the gate/up
-// launch from the router's sigmoid scores: the reference's slot order and
-// weights into idx[K], w[K], and perm[K] = the slot of prov_idx holding the
-// k-th expert (so the combine sums in the reference's order).
-struct ExactRoute {
-  const float* scores;     // 256 sigmoid scores (null: no route workgroup)
-  const float* bias;       // 256 or null
-  const int* prov_idx;     // the K experts the gate/up slots run
-  int* idx;
-  float* w;
-  int* perm;
 };
 // gate/up matvecs + SwiGLU for every slot; writes act[slot][2048] and the
 // digits of act (act_xd[slot][32]).  counters: (FDM_MAX_K + 1) x 64 ints,
 // zero on entry and left zero.
 hipError_t launch_gateup(const SlotTable& t, const XGroup* xd, float* act, XGroup* act_xd,
-                         int* counters, const ExactRoute& r, hipStream_t s);
+                         int* counters, hipStream_t s);
 // down matvecs for every slot (into eo[slot][7168]) and the combine:
 //   out[i] = (h_in[i] + sum_{k<K} w[k] * E_k[i]) + S[i]
 // moe_out (optional) receives sum_k w[k] * E_k[i].  counters: 448 ints,

@@ -7,10 +7,7 @@
 // that the HBM queue stays full (one 16-byte load per lane per step; the
 // four lanes of a Q4_K block share its header through DPP).
 //
-// k_gateup  one workgroup per (slot, 8-row tile), plus (workgroup 0, first
-//   to be dispatched) the exact route() of the token when the router only
-//   selected the expert set: the slot order and weights are needed by the
-//   combine alone, so they are computed here beside the weight stream.  Wave w owns rows 2w and
+// k_gateup  one workgroup per (slot, 8-row tile).  Wave w owns rows 2w and
 //   2w+1 of the tile in BOTH gate and up (lanes 0-31 gate, 32-63 up, 16
 //   lanes per row), so SwiGLU (swiglu_fused, shaders.metal:210-220) is
 //   applied in registers.  The last of the four tiles of a 32-row sub-block
@@ -22,7 +19,6 @@
 //   (moe_out += w_k * E_k, infer.m:1690-1695; hidden = h_in + moe_out + sd,
 //   infer.m:1922).
 #include "fdm_internal.h"
-#include "route_device.h"
 
 namespace fdm {
 
@@ -45,41 +41,13 @@ __device__ __forceinline__ void stage_groups(XGroup* __restrict__ dst,
 constexpr int kGuRows = 8;                 // rows of gate (and up) per workgroup
 constexpr int kGuTiles = kFfn / kGuRows;   // 256 tiles per slot
 
-// Workgroup body of the exact route(): wave 0 runs it; lane k < K finds
-// the provisional slot holding its expert.
-__device__ void exact_route_wg(const ExactRoute& r, int K) {
-  if (threadIdx.x >= 64) return;
-  const int lane = threadIdx.x;
-  float sc[4], bj[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sc[j] = r.scores[64 * j + lane];
-    bj[j] = r.bias ? r.bias[64 * j + lane] : 0.0f;
-  }
-  route_scores_wave(sc, bj, K, 2.5f, r.idx, r.w);
-  if (lane < K) {
-    const int id = r.idx[lane];
-    int p = 0;
-    for (int s = K - 1; s >= 0; --s) p = r.prov_idx[s] == id ? s : p;
-    r.perm[lane] = p;
-  }
-}
-
 __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __restrict__ xd,
                                                 float* __restrict__ act,
                                                 XGroup* __restrict__ act_xd,
-                                                int* __restrict__ counters, ExactRoute r) {
+                                                int* __restrict__ counters) {
   __shared__ XGroup xs[kHidden / 64];
   __shared__ int last;
-  int b = blockIdx.x;
-  if (r.scores) {
-    if (b == 0) {
-      exact_route_wg(r, t.K);
-      return;
-    }
-    --b;
-  }
-  const int slot = b / kGuTiles, tile = b % kGuTiles;
+  const int slot = blockIdx.x / kGuTiles, tile = blockIdx.x % kGuTiles;
   const uint8_t* blob = slot_blob(t, slot);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
@@ -186,10 +154,7 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
     if (threadIdx.x < kDnRows) {
       const int r = tile * kDnRows + threadIdx.x;
       float moe = 0.0f;
-      for (int k = 0; k < t.K; ++k) {
-        const int sl = t.perm ? t.perm[k] : k;
-        moe = fmaf(t.w[k], load_agent(eo + (size_t)sl * kHidden + r), moe);
-      }
+      for (int k = 0; k < t.K; ++k) moe = fmaf(t.w[k], load_agent(eo + (size_t)k * kHidden + r), moe);
       const float sd = t.n_slots > t.K ? load_agent(eo + (size_t)t.K * kHidden + r) : 0.0f;
       const float hin = h_in ? h_in[r] : 0.0f;
       out[r] = (hin + moe) + sd;
@@ -200,9 +165,9 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
 }
 
 hipError_t launch_gateup(const SlotTable& t, const XGroup* xd, float* act, XGroup* act_xd,
-                         int* counters, const ExactRoute& r, hipStream_t s) {
-  const int grid = kGuTiles * t.n_slots + (r.scores ? 1 : 0);
-  hipLaunchKernelGGL(k_gateup, dim3(grid), dim3(256), 0, s, t, xd, act, act_xd, counters, r);
+                         int* counters, hipStream_t s) {
+  hipLaunchKernelGGL(k_gateup, dim3(kGuTiles * t.n_slots), dim3(256), 0, s, t, xd, act, act_xd,
+                     counters);
   return hipGetLastError();
 }
 

@@ -63,6 +63,13 @@ __device__ __forceinline__ float row_shr(float v, float fill) {
       __builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), 0x110 | N, 0xF, 0xF, false));
 }
 
+// DPP row_bcast:15 of a float into rows 1 and 3: their lanes receive lane
+// 15 of the row before (rows 0 and 2 keep v).
+__device__ __forceinline__ float row_bcast15(float v, float fill) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(v), 0x142, 0xA, 0xF, false));
+}
+
 // Merge two top-2 multisets (a1 >= a2, b1 >= b2).
 __device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float o2) {
   const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
@@ -76,18 +83,6 @@ __device__ __forceinline__ int sort_key(float f) {
   if (f != f) return INT_MIN;
   const int b = __float_as_int(f + 0.0f);
   return b >= 0 ? b : b ^ 0x7FFFFFFF;
-}
-
-// Maximum of an int over the whole wave (DPP within rows of 16, then the
-// four row results).
-__device__ __forceinline__ int wave_max_i32(int v) {
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x111, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x112, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x114, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x118, 0xF, 0xF, false));
-  const int a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
-  const int c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
-  return max(max(a, b), max(c, d));
 }
 
 // Minimum of an int over the whole wave.
@@ -149,46 +144,53 @@ __device__ __forceinline__ void slot_scan(const int vk[4], const float score[4],
 // bj[j]): the order-preserving keys of the choices (score + bias) masked to
 // the top-4 groups; experts outside them get the key of -1e30.  R1
 // geometry: 256 experts, 8 groups of 32; group of expert i = i / 32 =
-// 2j + l / 32.
+// 2j + l / 32 (rows 0-1 of register j are group 2j, rows 2-3 group 2j+1).
+//  - group top-2 (infer.m:933-941): the running top-2 of a group is the
+//    top-2 of the multiset of its choices above -1e30 (NaN never enters),
+//    padded with -1e30.  Each row of 16 lanes is reduced by DPP row shifts,
+//    then row_bcast:15 folds row 0 into row 1 and row 2 into row 3, leaving
+//    the group's pair in lanes 31 and 63.
+//  - group choice (infer.m:944-954): four strict-> passes that start from
+//    -1e30 select the top 4 of the groups whose sum exceeds -1e30, by value
+//    and then lowest index: a group is chosen iff it is eligible and fewer
+//    than 4 eligible groups rank above it (computed for all 8 at once).
 __device__ __forceinline__ void route_keys(const float score[4], const float bj[4], int vk[4]) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  float choice[4];
-  float gs[8];
+  float choice[4], t1[4], t2[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     choice[j] = score[j] + bj[j];
-    // running top-2 of a group = top-2 of the multiset of its choices that
-    // exceed -1e30 (NaN never enters), padded with -1e30: reduce each row of
-    // 16 lanes by DPP, then merge the two rows of the group
-    float t1 = choice[j] > -1e30f ? choice[j] : -1e30f;
-    float t2 = -1e30f;
-    top2_merge(t1, t2, row_shr<1>(t1, -1e30f), row_shr<1>(t2, -1e30f));
-    top2_merge(t1, t2, row_shr<2>(t1, -1e30f), row_shr<2>(t2, -1e30f));
-    top2_merge(t1, t2, row_shr<4>(t1, -1e30f), row_shr<4>(t2, -1e30f));
-    top2_merge(t1, t2, row_shr<8>(t1, -1e30f), row_shr<8>(t2, -1e30f));
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      float a1 = readlane_f(t1, 32 * half + 15), a2 = readlane_f(t2, 32 * half + 15);
-      const float b1 = readlane_f(t1, 32 * half + 31), b2 = readlane_f(t2, 32 * half + 31);
-      top2_merge(a1, a2, b1, b2);
-      gs[2 * j + half] = a1 + a2;
-    }
+    t1[j] = choice[j] > -1e30f ? choice[j] : -1e30f;
+    t2[j] = -1e30f;
   }
-  unsigned selmask = 0;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    int best = -1;
-    float bs = -1e30f;
+  for (int j = 0; j < 4; ++j) top2_merge(t1[j], t2[j], row_shr<1>(t1[j], -1e30f), row_shr<1>(t2[j], -1e30f));
 #pragma unroll
-    for (int G = 0; G < 8; ++G) {
-      if (!((selmask >> G) & 1u) && gs[G] > bs) {
-        bs = gs[G];
-        best = G;
-      }
-    }
-    if (best >= 0) selmask |= 1u << best;
+  for (int j = 0; j < 4; ++j) top2_merge(t1[j], t2[j], row_shr<2>(t1[j], -1e30f), row_shr<2>(t2[j], -1e30f));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) top2_merge(t1[j], t2[j], row_shr<4>(t1[j], -1e30f), row_shr<4>(t2[j], -1e30f));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) top2_merge(t1[j], t2[j], row_shr<8>(t1[j], -1e30f), row_shr<8>(t2[j], -1e30f));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    top2_merge(t1[j], t2[j], row_bcast15(t1[j], -1e30f), row_bcast15(t2[j], -1e30f));
+  float gs[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    gs[2 * j] = readlane_f(t1[j], 31) + readlane_f(t2[j], 31);
+    gs[2 * j + 1] = readlane_f(t1[j], 63) + readlane_f(t2[j], 63);
   }
+  float mine = -1e30f;
+#pragma unroll
+  for (int G = 0; G < 8; ++G) mine = lane == G ? gs[G] : mine;
+  int rank = 0;
+#pragma unroll
+  for (int h = 0; h < 8; ++h) {
+    const bool oe = gs[h] > -1e30f;
+    rank += (oe && (gs[h] > mine || (gs[h] == mine && h < lane))) ? 1 : 0;
+  }
+  const unsigned selmask = (unsigned)__ballot(lane < 8 && mine > -1e30f && rank < 4);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool in_sel = (selmask >> (2 * j + (lane >> 5))) & 1u;
@@ -233,36 +235,51 @@ __device__ __forceinline__ void route_wave(const float* logits, const float* bia
   route_scores_wave(score, bj, K, scale, idx_out, w_out);
 }
 
-// The SET of experts route() selects, found in parallel: K extractions of
-// the wave maximum of the masked keys.  The sequential slot scan always
+// The SET of experts route() selects.  The sequential slot scan always
 // ends holding K elements that are >= everything it does not hold, so when
-// the K-th largest key is unique among the candidates the set is exactly
-// the K extracted experts.  Returns false (the caller then runs the exact
-// scan) when the K-th key is tied with a candidate left out, or when fewer
-// than K candidates exceed -1e30.  On success lane k (k < K) receives the
-// k-th extracted expert id; the order (descending key) is provisional.
-__device__ __forceinline__ bool topk_set(const int vk_in[4], int K, int& id_out) {
+// the K-th largest key T is unique among the candidates the set is exactly
+// {key >= T}.  T is found by a radix search over the order-preserving keys
+// (as unsigned, MSB first: keep bit b when at least K keys are >= the
+// prefix with it), counting with ballots; the search stops as soon as
+// exactly K keys are >= the prefix, which already fixes the set.  Returns
+// false (the caller then runs the exact scan) when the K-th key is tied
+// with a candidate left out, or when fewer than K candidates exceed -1e30.
+// On success lane k (k < K) receives the k-th expert of the set, in
+// (register j, lane) order -- a provisional order.
+__device__ __forceinline__ bool topk_set(const int vk[4], int K, int& id_out) {
   const int lane = threadIdx.x & 63;
-  const int floor_key = sort_key(-1e30f);
-  int v[4] = {vk_in[0], vk_in[1], vk_in[2], vk_in[3]};
-  int id = 0, m = INT_MIN;
-  for (int k = 0; k < K; ++k) {
-    m = wave_max_i32(max(max(v[0], v[1]), max(v[2], v[3])));
-    if (m <= floor_key) return false;
-    int pick = -1;
+  unsigned u[4];
 #pragma unroll
-    for (int j = 3; j >= 0; --j) {
-      const unsigned long long b = __ballot(v[j] == m);
-      if (b) pick = 64 * j + __ffsll(b) - 1;  // lowest expert index holding m
+  for (int j = 0; j < 4; ++j) u[j] = (unsigned)vk[j] ^ 0x80000000u;
+  unsigned T = 0;
+  int nT = 256;
+  for (int b = 31; b >= 0 && nT != K; --b) {
+    const unsigned c = T | (1u << b);
+    const unsigned long long m0 = __ballot(u[0] >= c), m1 = __ballot(u[1] >= c);
+    const unsigned long long m2 = __ballot(u[2] >= c), m3 = __ballot(u[3] >= c);
+    const int n = (__popcll(m0) + __popcll(m1)) + (__popcll(m2) + __popcll(m3));
+    if (n >= K) {
+      T = c;
+      nT = n;
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j)  // constant indices only: v stays in registers
-      if (j == (pick >> 6) && lane == (pick & 63)) v[j] = INT_MIN;
-    if (lane == k) id = pick;
   }
-  const bool tie = __ballot(v[0] == m || v[1] == m || v[2] == m || v[3] == m) != 0ull;
+  const unsigned floor_u = (unsigned)sort_key(-1e30f) ^ 0x80000000u;
+  if (nT != K || T <= floor_u) return false;
+  // compaction: the selected lane at position p pushes its id to lane p
+  int id = 0, base = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned long long sel = __ballot(u[j] >= T);
+    const int cnt = __popcll(sel);
+    const bool mine = (sel >> lane) & 1ull;
+    const int pos = base + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(sel >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((unsigned)sel, 0u));
+    const int got = __builtin_amdgcn_ds_permute((mine ? pos : 63) * 4, 64 * j + lane);
+    id = (lane >= base && lane < base + cnt) ? got : id;
+    base += cnt;
+  }
   id_out = id;
-  return !tie;
+  return true;
 }
 
 // Critical-path routing for the batch-1 layer: group limit and the expert
