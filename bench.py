@@ -81,6 +81,34 @@ def cpu_baseline(down, seconds, K=8):
     }
 
 
+def bench_batched(F, torch, layers, args, stream, K, steps=20, warmup=3):
+    """Batched decode through the resident layers: per token count T, the
+    mean over `steps` steps (new seeded tokens each, next layer each)."""
+    from flash_deepseek_amd.synthetic import make_tokens
+    out = {}
+    es = layers[0].expert_size
+    for T in [int(t) for t in args.batched.split(",") if t]:
+        X = make_tokens((steps + warmup) * T, 8100 + T).reshape(steps + warmup, T, HIDDEN)
+        Hin = make_tokens((steps + warmup) * T, 8200 + T).reshape(steps + warmup, T, HIDDEN)
+        Y = torch.empty((T, HIDDEN), dtype=torch.float32, device="cuda")
+        nd = torch.zeros(steps + warmup, dtype=torch.int32, device="cuda")
+        for i in range(steps + warmup):
+            if i == warmup:
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+            F.moe_forward_batched(3 + i % args.layers, X[i], Hin[i], T, K, Y,
+                                  n_distinct=nd[i:i + 1], stream=stream)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        d_mean = float(nd[warmup:].float().mean().item())
+        step_bytes = (d_mean + 1) * es + ROUTER_BYTES + T * HIDDEN * 4 * 3
+        out[str(T)] = {"us_per_token": round(dt / T * 1e6, 2), "ms_per_step": round(dt * 1e3, 4),
+                       "distinct_experts": round(d_mean, 1),
+                       "gbps": round(step_bytes / dt / 1e9, 1),
+                       "frac": round(step_bytes / dt / 1e9 / HBM_PEAK_GBPS, 4)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,6 +119,8 @@ def main():
     ap.add_argument("--prof-steps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--batched", default="",
+                    help="also time batched decode (config 3) at these token counts, e.g. 16,64,256")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter-collection run: a few layer steps, then plain 256 MiB "
                          "copies (read + write of known size) that calibrate the counters")
@@ -203,6 +233,8 @@ def main():
         },
         "cpu_baseline": None,
     }
+    if args.batched:
+        result["batched"] = bench_batched(F, torch, layers, args, stream, K)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.down, args.cpu_seconds, K)
         cb = result["cpu_baseline"]["value"]

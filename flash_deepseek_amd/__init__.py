@@ -154,9 +154,18 @@ def moe_layer(L, h_post, h_in, K, hidden, idx=None, w=None, stream=None):
          _stream(stream))
 
 
+def moe_forward_batched(L, X, H_in, T, K, hidden, idx=None, w=None, n_distinct=None,
+                        stream=None):
+    """T tokens through the MoE branch of layer L in one step, each selected
+    expert's weights read once: hidden[t] = H_in[t] + routed + shared."""
+    call("fdm_moe_forward_batched", L, _p(X), _p(H_in), T, K, _p(hidden), _p(idx), _p(w),
+         _p(n_distinct), _stream(stream))
+
+
 # ---- per-kernel GPU timing (HIP events; the moe_prof_t counterpart) --------------------
 PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
-          "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER}
+          "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER,
+          "batch": _lib.PROF_BATCH}
 
 
 def prof_enable(on=True):

@@ -1,0 +1,240 @@
+// batched_kernels.hip -- batched decode through one MoE layer: T tokens per
+// step with token -> expert dispatch, so each selected expert's weights are
+// read from HBM once per step however many tokens chose it.
+//
+// The reference decodes one token at a time (infer.m:2219-2229); per token
+// the result is the MoE branch of layer_forward (infer.m:1878-1922), and
+// routing (route(), infer.m:920-991) is exactly the per-token one.
+//
+//   k_router_logits / k_route   per token (router_kernels.hip)
+//   k_dispatch                  group the T*K (token, slot) pairs by expert
+//   k_xdigits                   digits of the T tokens
+//   k_bgateup                   per (distinct expert or shared, 8-row tile): the
+//                               weight tile stays in registers while the
+//                               expert's tokens stream through LDS
+//   k_xdigits                   digits of every pair's activations
+//   k_bdown                     per (expert, 16-row tile), as k_bgateup
+//   k_bcombine                  per token: h_in + sum_k w_k E_k + shared
+#include "fdm_internal.h"
+
+namespace fdm {
+
+namespace {
+
+constexpr int kExperts = 256;                 // R1 routed experts
+constexpr int kBGuRows = 8;                   // gate (and up) rows per tile
+constexpr int kBGuTiles = kFfn / kBGuRows;    // 256
+constexpr int kBDnRows = 16;                  // down rows per tile
+constexpr int kBDnTiles = kHidden / kBDnRows; // 448
+
+// Token t's row list of one work item: a distinct routed expert (its
+// (token, slot) pairs, rows = pair positions) or the shared expert (every
+// token, rows = P + t).
+struct ItemRows {
+  int first, count;  // pair positions [first, first + count) or tokens [0, count)
+  bool shared;
+};
+
+__device__ __forceinline__ ItemRows item_rows(const BatchArgs& b, int d, int D, int* expert) {
+  ItemRows r;
+  if (d < D) {
+    const int e = b.distinct[d];
+    *expert = e;
+    r.first = b.seg_start[e];
+    r.count = b.seg_start[e + 1] - r.first;
+    r.shared = false;
+  } else {
+    *expert = -1;
+    r.first = 0;
+    r.count = b.T;
+    r.shared = true;
+  }
+  return r;
+}
+
+__device__ __forceinline__ void stage_records(XGroup* __restrict__ dst,
+                                              const XGroup* __restrict__ src, int n) {
+  const u32x4* s = reinterpret_cast<const u32x4*>(src);
+  u32x4* d = reinterpret_cast<u32x4*>(dst);
+  for (int i = threadIdx.x; i < n * 9; i += 256) d[i] = s[i];
+}
+
+}  // namespace
+
+// ---- dispatch -------------------------------------------------------------------------
+// One workgroup.  Counts pairs per expert (LDS atomics), the segment starts
+// (exclusive scan), the ascending list of distinct experts, and each pair's
+// position in its expert's segment.  The order of pairs inside a segment
+// does not affect any result: every pair's activations and output are
+// computed from its own token only.
+__global__ __launch_bounds__(256) void k_dispatch(BatchArgs b) {
+  __shared__ int cnt[kExperts];
+  __shared__ int fill[kExperts];
+  __shared__ int start[kExperts + 1];
+  const int P = b.T * b.K;
+  cnt[threadIdx.x] = 0;
+  fill[threadIdx.x] = 0;
+  __syncthreads();
+  for (int p = threadIdx.x; p < P; p += 256) {
+    const int e = b.idx[p];
+    if (e >= 0 && e < kExperts) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int s = 0, d = 0;
+    for (int e = 0; e < kExperts; ++e) {
+      start[e] = s;
+      s += cnt[e];
+      if (cnt[e]) b.distinct[d++] = e;
+    }
+    start[kExperts] = s;
+    *b.n_distinct = d;
+  }
+  __syncthreads();
+  b.seg_start[threadIdx.x] = start[threadIdx.x];
+  if (threadIdx.x == 0) b.seg_start[kExperts] = start[kExperts];
+  for (int p = threadIdx.x; p < P; p += 256) {
+    const int e = b.idx[p];
+    int pos = -1;
+    if (e >= 0 && e < kExperts) {
+      pos = start[e] + atomicAdd(&fill[e], 1);
+      b.pair_tok[pos] = p / b.K;
+    }
+    b.pair_of[p] = pos;  // -1: invalid expert id, contributes 0
+  }
+}
+
+// ---- grouped gate/up ----------------------------------------------------------------------
+// Work item (tile, d): d < D is the d-th distinct expert, d == D the shared
+// expert; workgroups stride over d.  Wave w owns rows 2w, 2w+1 of the tile
+// in gate (lanes 0-31) and up (lanes 32-63), 16 lanes per row; the tile's
+// weights are loaded once and every token of the item is applied to them.
+__global__ __launch_bounds__(256) void k_bgateup(BatchArgs b) {
+  __shared__ XGroup xs[kHidden / 64];
+  const int tile = blockIdx.x;
+  const int D = *b.n_distinct;
+  const int n_items = D + (b.shared ? 1 : 0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
+  const int row = tile * kBGuRows + 2 * wave + (q & 1);
+  const Q4KScaleSel sel = q4k_scale_sel(g);
+  const int P = b.T * b.K;
+  for (int d = blockIdx.y; d < n_items; d += gridDim.y) {
+    int e;
+    const ItemRows r = item_rows(b, d, D, &e);
+    const uint8_t* blob = r.shared ? b.shared : b.experts + (size_t)e * b.expert_size;
+    Q4KGroupLoad ld[7];
+    const uint8_t* rowp = blob + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
+    for (int i = 0; i < r.count; ++i) {
+      const int tok = r.shared ? i : b.pair_tok[r.first + i];
+      const int out_row = r.shared ? P + i : r.first + i;
+      __syncthreads();  // the previous token's records are no longer read
+      stage_records(xs, b.xd + (size_t)tok * (kHidden / 64), kHidden / 64);
+      __syncthreads();
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 7; ++k) {
+        // the weights look changed to the compiler on every token, so their
+        // unpacking stays inside this loop instead of being hoisted out of
+        // it (seven unpacked groups would take 112 more registers)
+        __asm__ volatile("" : "+v"(ld[k].q0), "+v"(ld[k].q1), "+v"(ld[k].hdr_part));
+        acc += q4k_group_dot_ld(ld[k], sel, &xs[16 * k + l16]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      acc = sum16(acc);
+      const float up = __shfl(acc, (lane + 32) & 63);
+      if (lane == 0 || lane == 16) b.act[(size_t)out_row * kFfn + row] = silu_mul(acc, up);
+    }
+  }
+}
+
+// ---- grouped down -------------------------------------------------------------------------
+// Work item (tile, d) as k_bgateup: 16 down rows (wave w: rows 4w..4w+3, 16
+// lanes per row) of one expert, applied to the activation digits of every
+// row of the item.
+template <bool Q6>
+__global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
+  __shared__ XGroup xs[kFfn / 64];
+  const int tile = blockIdx.x;
+  const int D = *b.n_distinct;
+  const int n_items = D + (b.shared ? 1 : 0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15;
+  const int row = tile * kBDnRows + wave * 4 + (lane >> 4);
+  const int P = b.T * b.K;
+  for (int d = blockIdx.y; d < n_items; d += gridDim.y) {
+    int e;
+    const ItemRows r = item_rows(b, d, D, &e);
+    const uint8_t* blob = r.shared ? b.shared : b.experts + (size_t)e * b.expert_size;
+    const uint8_t* dbase = blob + 2 * (size_t)kGateBytes;
+    Q4KGroupLoad ld[2];
+    Q6KHalfLoad l6;
+    if (!Q6) {
+      const uint8_t* rowp = dbase + (size_t)row * kQ4KRowFfn;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
+    } else {
+      l6 = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (l16 >> 1) * kQ6KBlock, l16 & 1);
+    }
+    for (int i = 0; i < r.count; ++i) {
+      const int arow = r.shared ? P + i : r.first + i;
+      __syncthreads();
+      stage_records(xs, b.act_xd + (size_t)arow * (kFfn / 64), kFfn / 64);
+      __syncthreads();
+      float acc = 0.0f;
+      if (!Q6) {
+        const Q4KScaleSel sel = q4k_scale_sel(l16 & 3);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) acc += q4k_group_dot_ld(ld[k], sel, &xs[16 * k + l16]);
+      } else {
+        acc = q6k_half_dot_ld(l6, &xs[2 * l16]);
+      }
+      acc = sum16(acc);
+      if (l16 == 0) b.eo[(size_t)arow * kHidden + row] = acc;
+    }
+  }
+}
+
+// ---- combine ------------------------------------------------------------------------------
+// hidden[t] = (h_in[t] + sum_k w[t][k] E_{idx[t][k]}) + S[t], slots in route()
+// order (infer.m:1689-1695, 1922).
+__global__ __launch_bounds__(256) void k_bcombine(BatchArgs b) {
+  const int t = blockIdx.y;
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= kHidden) return;
+  const int P = b.T * b.K;
+  float moe = 0.0f;
+  for (int k = 0; k < b.K; ++k) {
+    const int pos = b.pair_of[t * b.K + k];
+    const float ev = pos >= 0 ? b.eo[(size_t)pos * kHidden + r] : 0.0f;
+    moe = fmaf(b.w[t * b.K + k], ev, moe);
+  }
+  const float sd = b.shared ? b.eo[(size_t)(P + t) * kHidden + r] : 0.0f;
+  const float hin = b.h_in ? b.h_in[(size_t)t * kHidden + r] : 0.0f;
+  b.out[(size_t)t * kHidden + r] = (hin + moe) + sd;
+}
+
+hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s) {
+  const int P = b.T * b.K;
+  const int rows = P + (b.shared ? b.T : 0);
+  const int max_items = (P < kExperts ? P : kExperts) + (b.shared ? 1 : 0);
+  // workgroups per tile: enough items in flight to fill the chip
+  const int gy = max_items < 16 ? max_items : 16;
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), 0, s, b);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (hipError_t e = launch_xdigits(b.x, (size_t)b.T * (kHidden / 64), b.xd, s)) return e;
+  hipLaunchKernelGGL(k_bgateup, dim3(kBGuTiles, gy), dim3(256), 0, s, b);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (hipError_t e = launch_xdigits(b.act, (size_t)rows * (kFfn / 64), b.act_xd, s)) return e;
+  if (down_q6)
+    hipLaunchKernelGGL(k_bdown<true>, dim3(kBDnTiles, gy), dim3(256), 0, s, b);
+  else
+    hipLaunchKernelGGL(k_bdown<false>, dim3(kBDnTiles, gy), dim3(256), 0, s, b);
+  if (hipError_t e = hipGetLastError()) return e;
+  hipLaunchKernelGGL(k_bcombine, dim3(kHidden / 256, b.T), dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
+}  // namespace fdm

@@ -43,6 +43,16 @@ struct Workspace {
   unsigned* layer_flags = nullptr;  // layer kernel epoch flags (kLayerFlags x stride)
   unsigned epoch = 0;         // last epoch handed to the layer kernel
   unsigned err_reported = 0;  // last error epoch reported by fdm_stream_sync
+  // batched decode (fdm_moe_forward_batched); per-row buffers grow on demand
+  int* b_seg = nullptr;       // [257]
+  int* b_pair_tok = nullptr;  // [FDM_MAX_TOKENS * FDM_MAX_K]
+  int* b_pair_of = nullptr;   // [FDM_MAX_TOKENS * FDM_MAX_K]
+  int* b_distinct = nullptr;  // [256]
+  int* b_ndistinct = nullptr; // [1]
+  size_t b_rows = 0;          // rows the three buffers below hold
+  float* b_act = nullptr;     // [b_rows][2048]
+  XGroup* b_act_xd = nullptr; // [b_rows][32]
+  float* b_eo = nullptr;      // [b_rows][7168]
   float* w = nullptr;         // FDM_MAX_TOKENS x 16
   float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
   XGroup* act_xd = nullptr;   // (FDM_MAX_K + 1) x 32
@@ -117,7 +127,8 @@ void free_workspace() {
   void* ptrs[] = {w.xd,       w.logits,   w.idx,     w.w,       w.act,
                   w.act_xd,   w.gu_count, w.dn_count, w.eo,
                   w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w,
-                  w.layer_cnt, w.layer_flags, w.layer_tagged};
+                  w.layer_cnt, w.layer_flags, w.layer_tagged, w.b_seg, w.b_pair_tok,
+                  w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act, w.b_act_xd, w.b_eo};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -140,6 +151,11 @@ int alloc_workspace() {
   FDM_HIP(hipMemset(w.layer_cnt, 0, (size_t)kLayerCounters * kLayerStride * sizeof(int)));
   FDM_HIP(hipMalloc(&w.layer_flags, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
   FDM_HIP(hipMemset(w.layer_flags, 0, (size_t)kLayerFlags * kLayerStride * sizeof(unsigned)));
+  FDM_HIP(hipMalloc(&w.b_seg, (FDM_N_EXPERTS + 1) * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.b_pair_tok, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.b_pair_of, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.b_distinct, FDM_N_EXPERTS * sizeof(int)));
+  FDM_HIP(hipMalloc(&w.b_ndistinct, sizeof(int)));
   FDM_HIP(hipMalloc(&w.layer_tagged, kLayerTagged * sizeof(uint64_t)));
   FDM_HIP(hipMemset(w.layer_tagged, 0, kLayerTagged * sizeof(uint64_t)));
   FDM_HIP(hipMalloc(&w.stage_x, FDM_HIDDEN * sizeof(float)));
@@ -654,6 +670,73 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
     ProfScope p(FDM_PROF_LAYER, s);
     FDM_HIP(launch_layer(a, s));
   }
+  return FDM_OK;
+}
+
+// ---- batched decode ---------------------------------------------------------------------
+namespace fdm {
+namespace {
+// Per-row buffers of the batched path, grown (never shrunk) to `rows`.
+// Callers synchronise with earlier work on the stream before a reallocation.
+int ensure_batch_rows(size_t rows, hipStream_t s) {
+  Workspace& w = g.ws;
+  if (rows <= w.b_rows) return FDM_OK;
+  FDM_HIP(hipStreamSynchronize(s));
+  if (w.b_act) (void)hipFree(w.b_act);
+  if (w.b_act_xd) (void)hipFree(w.b_act_xd);
+  if (w.b_eo) (void)hipFree(w.b_eo);
+  w.b_act = nullptr;
+  w.b_act_xd = nullptr;
+  w.b_eo = nullptr;
+  w.b_rows = 0;
+  FDM_HIP(hipMalloc(&w.b_act, rows * FDM_MOE_FFN * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.b_act_xd, rows * (FDM_MOE_FFN / 64) * sizeof(XGroup)));
+  FDM_HIP(hipMalloc(&w.b_eo, rows * FDM_HIDDEN * sizeof(float)));
+  w.b_rows = rows;
+  return FDM_OK;
+}
+}  // namespace
+}  // namespace fdm
+
+int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T, int K,
+                            float* d_hidden, int* d_idx, float* d_w, int* d_n_distinct,
+                            void* stream) {
+  Layer* y = nullptr;
+  if (int rc = get_layer(L, &y)) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (T < 1 || T > FDM_MAX_TOKENS)
+    return fail(FDM_E_INVAL, "T=%d outside 1..%d", T, FDM_MAX_TOKENS);
+  if (!d_X || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(d_X, 16)) return fail(FDM_E_INVAL, "X must be 16-byte aligned");
+  hipStream_t s = as_stream(stream);
+  const size_t rows = (size_t)T * K + (y->shared ? T : 0);
+  if (int rc = ensure_batch_rows(rows, s)) return rc;
+  int* idx = d_idx ? d_idx : g.ws.idx;
+  float* w = d_w ? d_w : g.ws.w;
+  ProfScope p(FDM_PROF_BATCH, s);
+  FDM_HIP(launch_router_logits(y->Wg, d_X, FDM_N_EXPERTS, FDM_HIDDEN, T, g.ws.logits, s));
+  FDM_HIP(launch_route(g.ws.logits, y->bias, T, K, idx, w, s));
+  BatchArgs b;
+  b.T = T;
+  b.K = K;
+  b.experts = y->experts;
+  b.expert_size = y->expert_size;
+  b.shared = y->shared;
+  b.x = d_X;
+  b.h_in = d_H_in;
+  b.out = d_hidden;
+  b.idx = idx;
+  b.w = w;
+  b.xd = g.ws.xd;
+  b.act = g.ws.b_act;
+  b.act_xd = g.ws.b_act_xd;
+  b.eo = g.ws.b_eo;
+  b.seg_start = g.ws.b_seg;
+  b.pair_tok = g.ws.b_pair_tok;
+  b.pair_of = g.ws.b_pair_of;
+  b.distinct = g.ws.b_distinct;
+  b.n_distinct = d_n_distinct ? d_n_distinct : g.ws.b_ndistinct;
+  FDM_HIP(launch_batched_experts(b, y->down_q6, s));
   return FDM_OK;
 }
 

@@ -95,6 +95,32 @@ struct LayerArgs {
 };
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
 
+// batched_kernels.hip
+// Batched decode of T tokens through one layer with token -> expert
+// dispatch (each selected expert's weights read once per step).  Routing
+// (idx, w: [T][K]) is computed beforehand by the router kernels.
+struct BatchArgs {
+  int T, K;
+  const uint8_t* experts;  // 256 packed blobs
+  size_t expert_size;
+  const uint8_t* shared;   // shared expert blob or null
+  const float* x;          // h_post [T][7168]
+  const float* h_in;       // residual [T][7168] or null
+  float* out;              // hidden [T][7168]
+  const int* idx;          // [T][K]
+  const float* w;          // [T][K]
+  XGroup* xd;              // workspace: digits of x [T][112]
+  float* act;              // workspace: [rows][2048], rows = T*K (+ T shared)
+  XGroup* act_xd;          // workspace: [rows][32]
+  float* eo;               // workspace: [rows][7168]
+  int* seg_start;          // workspace: [257] pair segment of each expert
+  int* pair_tok;           // workspace: [T*K] token of each pair position
+  int* pair_of;            // workspace: [T*K] position of pair (t, k), -1 if invalid id
+  int* distinct;           // workspace: [256] distinct experts, ascending
+  int* n_distinct;         // out: number of distinct experts (device int)
+};
+hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s);
+
 // synth_kernels.hip
 hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);
 hipError_t launch_synth_q6k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);

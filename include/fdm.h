@@ -150,6 +150,19 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
 
+/* ---- batched decode: T tokens through the MoE branch of layer L in one
+ * step, with token -> expert dispatch so that each selected expert's weights
+ * are read once per step (config 3; the reference decodes one token at a
+ * time, infer.m:2219-2229).  Per token t the result is fdm_moe_layer's:
+ *   hidden[t] = h_in[t] + sum_k w[t][k] E_k(h_post[t]) + S(h_post[t])
+ * with route() per token (bit-exact idx / w).  d_X, d_H_in, d_hidden:
+ * [T][7168] fp32 (d_H_in may be NULL).  d_idx / d_w ([T][K], optional)
+ * receive the routing; d_n_distinct (optional, device int) the number of
+ * distinct routed experts of the step.  1 <= T <= FDM_MAX_TOKENS. */
+int fdm_moe_forward_batched(int L, const float *d_X, const float *d_H_in, int T, int K,
+                            float *d_hidden, int *d_idx, float *d_w, int *d_n_distinct,
+                            void *stream);
+
 /* ---- per-kernel GPU timing: replaces the host-clock moe_prof_t ring
  * (infer.m:177-261) with HIP events recorded on the launch stream around
  * every kernel of the entry points above.  fdm_prof_read synchronises on
@@ -161,7 +174,8 @@ int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, floa
 #define FDM_PROF_XDIGITS 3  /* activation digits (routing given)        */
 #define FDM_PROF_MATVEC 4   /* fdm_matvec_q4k / _q6k kernel             */
 #define FDM_PROF_LAYER 5    /* fdm_moe_layer: the whole layer, 1 launch */
-#define FDM_PROF_PHASES 6
+#define FDM_PROF_BATCH 6    /* fdm_moe_forward_batched: the whole step  */
+#define FDM_PROF_PHASES 7
 int fdm_prof_enable(int on);
 int fdm_prof_reset(void);
 int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);

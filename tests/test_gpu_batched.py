@@ -1,0 +1,100 @@
+"""Batched decode (fdm_moe_forward_batched): T tokens through one resident
+R1-shape layer in one step with token -> expert dispatch, against the
+oracle applied token by token -- routing bit-exact per token, outputs
+within 1e-3 relative L2 of the float64 truth, and the distinct-expert count
+equal to the number of distinct routed ids."""
+import numpy as np
+import pytest
+
+from tests._helpers import empty_f32, rel_l2, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+@pytest.fixture(scope="module", params=[False, True], ids=["q4k_down", "q6k_down"])
+def layer(request, fdm):
+    from flash_deepseek_amd.synthetic import make_layer
+    L = 11 if request.param else 10
+    say(f"building layer L={L} down_q6={request.param}")
+    lay = make_layer(2000 + L, down_q6=request.param)
+    fdm.attach_layer(L, lay.experts, lay.expert_size, lay.Wg, lay.bias, lay.shared)
+    yield L, lay
+    fdm.release_layer(L)
+
+
+def check_tokens(fdm, oracle, L, lay, T, K, seed, tokens_checked):
+    import torch
+    X = np.stack([oracle.synth_normal(7168, 0.0, 1.0, seed + t) for t in range(T)])
+    Hin = np.stack([oracle.synth_normal(7168, 0.0, 1.0, seed + 1000 + t) for t in range(T)])
+    out = empty_f32(T * 7168)
+    idx = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    w = empty_f32(T * K)
+    nd = torch.zeros(1, dtype=torch.int32, device="cuda")
+    say(f"moe_forward_batched L={L} T={T} K={K}")
+    fdm.moe_forward_batched(L, to_dev(X.ravel()), to_dev(Hin.ravel()), T, K, out, idx, w, nd)
+    got = to_host(out).reshape(T, 7168)
+    gi = to_host(idx).reshape(T, K)
+    gw = to_host(w).reshape(T, K)
+    assert int(to_host(nd)[0]) == len(np.unique(gi))
+    Wg, bias = to_host(lay.Wg), to_host(lay.bias)
+    cache = {}
+
+    def ffn(e):
+        if e not in cache:
+            cache[e] = oracle.expert_ffn(lay.expert_bytes(e), lay.down_q6, X_t)
+        return cache[e]
+
+    for t in tokens_checked:
+        X_t = X[t]
+        cache.clear()
+        ri, rw = oracle.route(oracle.router_logits(Wg, X_t), bias, K=K)
+        assert np.array_equal(gi[t], ri), t
+        assert np.array_equal(gw[t].view(np.uint32), rw.view(np.uint32)), t
+        moe = np.zeros(7168)
+        for k in range(K):
+            moe += np.float64(rw[k]) * ffn(int(ri[k]))
+        want = Hin[t].astype(np.float64) + moe + ffn(-1)
+        err = rel_l2(got[t], want)
+        assert err <= TOL, (t, err)
+    # every token's routing is checked (cheap); outputs on the sampled tokens
+    for t in range(T):
+        ri, rw = oracle.route(oracle.router_logits(Wg, X[t]), bias, K=K)
+        assert np.array_equal(gi[t], ri), t
+
+
+@pytest.mark.parametrize("T,K", [(1, 8), (16, 8), (5, 3)])
+def test_batched_matches_per_token_oracle(fdm, oracle, layer, T, K):
+    L, lay = layer
+    check_tokens(fdm, oracle, L, lay, T, K, 9000 + 17 * T, tokens_checked=sorted({0, T // 2, T - 1}))
+
+
+def test_batched_equals_single_token_layer(fdm, oracle, layer):
+    """Each token of a batch gets the same routing as fdm_moe_layer and an
+    output within the digit error of it."""
+    import torch
+    L, lay = layer
+    T, K = 12, 8
+    X = np.stack([oracle.synth_normal(7168, 0.0, 1.0, 777 + t) for t in range(T)]).astype(np.float32)
+    out = empty_f32(T * 7168)
+    idx = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    fdm.moe_forward_batched(L, to_dev(X.ravel()), None, T, K, out, idx, None, None)
+    got = to_host(out).reshape(T, 7168)
+    gi = to_host(idx).reshape(T, K)
+    for t in (0, 7, 11):
+        one = empty_f32(7168)
+        i1 = torch.empty(K, dtype=torch.int32, device="cuda")
+        fdm.moe_layer(L, to_dev(X[t]), None, K, one, i1)
+        assert np.array_equal(to_host(i1), gi[t])
+        assert rel_l2(got[t], to_host(one).astype(np.float64)) <= 1e-4
+
+
+def test_batched_errors(fdm, layer):
+    L, _ = layer
+    x = empty_f32(7168)
+    with pytest.raises(fdm.FdmError):
+        fdm.moe_forward_batched(L, x, None, 0, 8, empty_f32(7168))
+    with pytest.raises(fdm.FdmError):
+        fdm.moe_forward_batched(L, x, None, 513, 8, empty_f32(7168))
+    with pytest.raises(fdm.FdmError):
+        fdm.moe_forward_batched(L, x, None, 1, 17, empty_f32(7168))
