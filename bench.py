@@ -109,6 +109,44 @@ def bench_batched(F, torch, layers, args, stream, K, steps=20, warmup=3):
     return out
 
 
+def bench_prefill(F, torch, layers, args, stream, K, n_layers=4, iters=5):
+    """Prefill of args.prefill tokens through n_layers resident layers
+    (h <- h + MoE(rms_norm(h, w)) per layer, in place); each timed iteration
+    starts from the same seeded activations."""
+    from flash_deepseek_amd.synthetic import make_tokens
+    T = args.prefill
+    H0 = make_tokens(T, 9100)
+    H = torch.empty_like(H0)
+    norms = [make_tokens(1, 9200 + l, mean=1.0, std=0.1)[0] for l in range(n_layers)]
+    ids = [3 + l for l in range(n_layers)]
+    nd = []
+    times = []
+    for i in range(iters + 1):
+        H.copy_(H0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        F.moe_prefill(ids, H, T, K, norms, stream=stream)
+        torch.cuda.synchronize()
+        if i:
+            times.append(time.perf_counter() - t0)
+    dt = sorted(times)[len(times) // 2]
+    es = layers[0].expert_size
+    # every layer reads its selected experts (nearly all 256 at this T) + shared + router
+    idx = torch.empty((n_layers, T, K), dtype=torch.int32, device="cuda")
+    H.copy_(H0)
+    F.moe_prefill(ids, H, T, K, norms, idx=idx, stream=stream)
+    torch.cuda.synchronize()
+    d = [len(torch.unique(idx[l])) for l in range(n_layers)]
+    step_bytes = sum((dl + 1) * es for dl in d) + n_layers * (ROUTER_BYTES + T * HIDDEN * 4 * 2)
+    flops = n_layers * T * (K + 1) * 3 * 2 * HIDDEN * FFN
+    return {"tokens": T, "layers": n_layers, "ms": round(dt * 1e3, 3),
+            "tokens_per_s": round(T / dt, 1), "distinct_experts": d,
+            "gbps": round(step_bytes / dt / 1e9, 1),
+            "frac": round(step_bytes / dt / 1e9 / HBM_PEAK_GBPS, 4),
+            "tflops": round(flops / dt / 1e12, 2),
+            "mfma_util_est": round(flops / dt / 2.5e15, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -121,6 +159,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--batched", default="",
                     help="also time batched decode (config 3) at these token counts, e.g. 16,64,256")
+    ap.add_argument("--prefill", type=int, default=0,
+                    help="also time prefill of this many tokens through 4 resident layers (config 4)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter-collection run: a few layer steps, then plain 256 MiB "
                          "copies (read + write of known size) that calibrate the counters")
@@ -235,6 +275,8 @@ def main():
     }
     if args.batched:
         result["batched"] = bench_batched(F, torch, layers, args, stream, K)
+    if args.prefill:
+        result["prefill"] = bench_prefill(F, torch, layers, args, stream, K)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.down, args.cpu_seconds, K)
         cb = result["cpu_baseline"]["value"]

@@ -162,10 +162,24 @@ def moe_forward_batched(L, X, H_in, T, K, hidden, idx=None, w=None, n_distinct=N
          _p(n_distinct), _stream(stream))
 
 
+def rms_norm(x, w, out, T, d=HIDDEN, stream=None):
+    """out[t] = rms_norm(x[t], w) on the device (infer.m:369-374), bit-exact."""
+    call("fdm_rms_norm", _p(x), _p(w), _p(out), T, d, _stream(stream))
+
+
+def moe_prefill(layers, H, T, K, norm_w, idx=None, stream=None):
+    """In place on H [T][7168]: for each layer l, H += MoE_l(rms_norm(H, norm_w[l]))."""
+    n = len(layers)
+    lay = (ctypes.c_int * n)(*layers)
+    nw = (ctypes.c_void_p * n)(*[_p(w) for w in norm_w]) if norm_w is not None else None
+    call("fdm_moe_prefill", ctypes.cast(lay, ctypes.c_void_p),  n, _p(H), T, K,
+         ctypes.cast(nw, ctypes.c_void_p) if nw is not None else None, _p(idx), _stream(stream))
+
+
 # ---- per-kernel GPU timing (HIP events; the moe_prof_t counterpart) --------------------
 PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
           "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER,
-          "batch": _lib.PROF_BATCH}
+          "batch": _lib.PROF_BATCH, "prefill": _lib.PROF_PREFILL}
 
 
 def prof_enable(on=True):

@@ -18,7 +18,8 @@ FDM_E_NOMEM = -5
 FDM_E_SIZE = -6
 FDM_E_IO = -7
 
-PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER, PROF_BATCH = range(7)
+(PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER, PROF_BATCH,
+ PROF_PREFILL) = range(8)
 
 QK_K = 256
 Q4K_BLOCK_SIZE = 144
@@ -68,6 +69,8 @@ SIGNATURES = {
     "fdm_moe_forward_host": [_i, _vp, _vp, _vp, _i, _vp],
     "fdm_moe_layer": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
     "fdm_moe_forward_batched": [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp],
+    "fdm_rms_norm": [_vp, _vp, _vp, _i, _i, _vp],
+    "fdm_moe_prefill": [_vp, _i, _vp, _i, _i, _vp, _vp, _vp],
     "fdm_prof_enable": [_i],
     "fdm_prof_reset": [],
     "fdm_prof_read": [_i, ctypes.POINTER(_i), ctypes.POINTER(ctypes.c_double),

@@ -25,6 +25,7 @@ SOURCES = [
     "moe_kernels.hip",
     "layer_kernel.hip",
     "batched_kernels.hip",
+    "prefill_kernels.hip",
     "synth_kernels.hip",
     "capi.hip",
 ]

@@ -199,7 +199,8 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
 
 // ---- combine ------------------------------------------------------------------------------
 // hidden[t] = (h_in[t] + sum_k w[t][k] E_{idx[t][k]}) + S[t], slots in route()
-// order (infer.m:1689-1695, 1922).
+// order (infer.m:1689-1695, 1922).  out may alias h_in (each element is read
+// before it is written, by the same thread).
 __global__ __launch_bounds__(256) void k_bcombine(BatchArgs b) {
   const int t = blockIdx.y;
   const int r = blockIdx.x * 256 + threadIdx.x;
@@ -214,6 +215,16 @@ __global__ __launch_bounds__(256) void k_bcombine(BatchArgs b) {
   const float sd = b.shared ? b.eo[(size_t)(P + t) * kHidden + r] : 0.0f;
   const float hin = b.h_in ? b.h_in[(size_t)t * kHidden + r] : 0.0f;
   b.out[(size_t)t * kHidden + r] = (hin + moe) + sd;
+}
+
+hipError_t launch_dispatch(const BatchArgs& b, hipStream_t s) {
+  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
+hipError_t launch_combine(const BatchArgs& b, hipStream_t s) {
+  hipLaunchKernelGGL(k_bcombine, dim3(kHidden / 256, b.T), dim3(256), 0, s, b);
+  return hipGetLastError();
 }
 
 hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s) {

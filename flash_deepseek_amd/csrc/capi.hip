@@ -53,6 +53,12 @@ struct Workspace {
   float* b_act = nullptr;     // [b_rows][2048]
   XGroup* b_act_xd = nullptr; // [b_rows][32]
   float* b_eo = nullptr;      // [b_rows][7168]
+  // prefill (fdm_moe_prefill)
+  int p_tokens = 0;           // tokens the buffers below hold
+  float* p_hpost = nullptr;   // [p_tokens][7168] rms_norm output
+  __bf16* p_xb = nullptr;     // 2 x [p_tokens][7168]: its bf16 pair (hi, lo)
+  size_t p_rows = 0;
+  __bf16* p_actb = nullptr;   // [p_rows][2048]
   float* w = nullptr;         // FDM_MAX_TOKENS x 16
   float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
   XGroup* act_xd = nullptr;   // (FDM_MAX_K + 1) x 32
@@ -128,7 +134,8 @@ void free_workspace() {
                   w.act_xd,   w.gu_count, w.dn_count, w.eo,
                   w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w,
                   w.layer_cnt, w.layer_flags, w.layer_tagged, w.b_seg, w.b_pair_tok,
-                  w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act, w.b_act_xd, w.b_eo};
+                  w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act, w.b_act_xd, w.b_eo,
+                  w.p_hpost, w.p_xb, w.p_actb};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -697,6 +704,104 @@ int ensure_batch_rows(size_t rows, hipStream_t s) {
 }
 }  // namespace
 }  // namespace fdm
+
+namespace fdm {
+namespace {
+// Prefill buffers for T tokens and `rows` expert rows (grown on demand).
+int ensure_prefill(int T, size_t rows, hipStream_t s) {
+  Workspace& w = g.ws;
+  if (T > w.p_tokens) {
+    FDM_HIP(hipStreamSynchronize(s));
+    if (w.p_hpost) (void)hipFree(w.p_hpost);
+    if (w.p_xb) (void)hipFree(w.p_xb);
+    w.p_hpost = nullptr;
+    w.p_xb = nullptr;
+    w.p_tokens = 0;
+    FDM_HIP(hipMalloc(&w.p_hpost, (size_t)T * FDM_HIDDEN * sizeof(float)));
+    FDM_HIP(hipMalloc(&w.p_xb, 2 * (size_t)T * FDM_HIDDEN * sizeof(__bf16)));
+    w.p_tokens = T;
+  }
+  if (rows > w.p_rows) {
+    FDM_HIP(hipStreamSynchronize(s));
+    if (w.p_actb) (void)hipFree(w.p_actb);
+    w.p_actb = nullptr;
+    w.p_rows = 0;
+    FDM_HIP(hipMalloc(&w.p_actb, rows * FDM_MOE_FFN * sizeof(__bf16)));
+    w.p_rows = rows;
+  }
+  return FDM_OK;
+}
+}  // namespace
+}  // namespace fdm
+
+int fdm_rms_norm(const float* d_x, const float* d_w, float* d_o, int T, int d, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_x || !d_o) return fail(FDM_E_INVAL, "null pointer");
+  if (T < 1 || d < 1 || d > FDM_HIDDEN) return fail(FDM_E_INVAL, "T=%d d=%d (d <= %d)", T, d, FDM_HIDDEN);
+  FDM_HIP(launch_rms_norm(d_x, d_w, d_o, nullptr, T, d, as_stream(stream)));
+  return FDM_OK;
+}
+
+int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
+                    const float* const* d_norm_w, int* d_idx, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (!layers || !d_H || n_layers < 1) return fail(FDM_E_INVAL, "no layers or null H");
+  if (T < 1 || T > FDM_MAX_TOKENS) return fail(FDM_E_INVAL, "T=%d outside 1..%d", T, FDM_MAX_TOKENS);
+  if (!aligned(d_H, 16)) return fail(FDM_E_INVAL, "H must be 16-byte aligned");
+  for (int l = 0; l < n_layers; ++l) {
+    Layer* y = nullptr;
+    if (int rc = get_layer(layers[l], &y)) return rc;
+    if (y->down_q6) return fail(FDM_E_INVAL, "prefill runs Q4_K-down layers (layer %d is Q6_K)", layers[l]);
+  }
+  hipStream_t s = as_stream(stream);
+  const size_t rows = (size_t)T * K + T;
+  if (int rc = ensure_prefill(T, rows, s)) return rc;
+  if (int rc = ensure_batch_rows(rows, s)) return rc;
+  ProfScope prof(FDM_PROF_PREFILL, s);
+  for (int l = 0; l < n_layers; ++l) {
+    Layer* y = nullptr;
+    (void)get_layer(layers[l], &y);
+    int* idx = d_idx ? d_idx + (size_t)l * T * K : g.ws.idx;
+    FDM_HIP(launch_rms_norm(d_H, d_norm_w ? d_norm_w[l] : nullptr, g.ws.p_hpost, g.ws.p_xb, T,
+                            FDM_HIDDEN, s));
+    FDM_HIP(launch_router_logits(y->Wg, g.ws.p_hpost, FDM_N_EXPERTS, FDM_HIDDEN, T, g.ws.logits, s));
+    FDM_HIP(launch_route(g.ws.logits, y->bias, T, K, idx, g.ws.w, s));
+    BatchArgs b{};
+    b.T = T;
+    b.K = K;
+    b.experts = y->experts;
+    b.expert_size = y->expert_size;
+    b.shared = y->shared;
+    b.h_in = d_H;
+    b.out = d_H;  // residual in place
+    b.idx = idx;
+    b.w = g.ws.w;
+    b.eo = g.ws.b_eo;
+    b.seg_start = g.ws.b_seg;
+    b.pair_tok = g.ws.b_pair_tok;
+    b.pair_of = g.ws.b_pair_of;
+    b.distinct = g.ws.b_distinct;
+    b.n_distinct = g.ws.b_ndistinct;
+    FDM_HIP(launch_dispatch(b, s));
+    PrefillArgs p;
+    p.T = T;
+    p.K = K;
+    p.experts = y->experts;
+    p.expert_size = y->expert_size;
+    p.shared = y->shared;
+    p.xb = g.ws.p_xb;
+    p.actb = g.ws.p_actb;
+    p.eo = g.ws.b_eo;
+    p.seg_start = g.ws.b_seg;
+    p.pair_tok = g.ws.b_pair_tok;
+    p.distinct = g.ws.b_distinct;
+    p.n_distinct = g.ws.b_ndistinct;
+    FDM_HIP(launch_prefill_experts(p, s));
+    FDM_HIP(launch_combine(b, s));
+  }
+  return FDM_OK;
+}
 
 int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T, int K,
                             float* d_hidden, int* d_idx, float* d_w, int* d_n_distinct,

@@ -120,6 +120,32 @@ struct BatchArgs {
   int* n_distinct;         // out: number of distinct experts (device int)
 };
 hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s);
+// The dispatch and the combine of the batched path on their own (prefill).
+hipError_t launch_dispatch(const BatchArgs& b, hipStream_t s);
+hipError_t launch_combine(const BatchArgs& b, hipStream_t s);
+
+// prefill_kernels.hip
+// rms_norm per token (infer.m:369-374), bit-exact: o = x * inv * w; also
+// the bf16 pair of o into xb when not null: hi [T][d], then lo [T][d].
+// d <= 7168.
+hipError_t launch_rms_norm(const float* x, const float* w, float* o, __bf16* xb, int T, int d,
+                           hipStream_t s);
+// Grouped expert GEMMs of one prefill layer (Q4_K down): gate/up + SwiGLU
+// into actb, down into eo.  Rows: pair position p (routed), T*K + t (shared).
+struct PrefillArgs {
+  int T, K;
+  const uint8_t* experts;
+  size_t expert_size;
+  const uint8_t* shared;
+  const __bf16* xb;        // rms_norm output as bf16 pairs: hi [T][7168], lo [T][7168]
+  __bf16* actb;            // [rows][2048]
+  float* eo;               // [rows][7168]
+  const int* seg_start;    // from the dispatch
+  const int* pair_tok;
+  const int* distinct;
+  const int* n_distinct;
+};
+hipError_t launch_prefill_experts(const PrefillArgs& p, hipStream_t s);
 
 // synth_kernels.hip
 hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);

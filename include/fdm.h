@@ -163,6 +163,23 @@ int fdm_moe_forward_batched(int L, const float *d_X, const float *d_H_in, int T,
                             float *d_hidden, int *d_idx, float *d_w, int *d_n_distinct,
                             void *stream);
 
+/* ---- rms_norm on the device (infer.m:369-374, the h_post of infer.m:1850):
+ * o[t] = x[t] * (1 / sqrt(sum_i x[t][i]^2 / d + 1e-6)) * w, bit-exact with
+ * the reference's sequential loop.  d_w may be NULL (w = 1); d_o may alias
+ * d_x.  [T][d] fp32, d <= 7168. */
+int fdm_rms_norm(const float *d_x, const float *d_w, float *d_o, int T, int d, void *stream);
+
+/* ---- prefill: T tokens through n_layers resident MoE layers,
+ *   h <- h + MoE_l(rms_norm(h, norm_w[l]))   for l = 0 .. n_layers-1
+ * (infer.m:1850, 1878-1922), in place on d_H [T][7168] fp32.  Routing is
+ * route() per token on the fp32 rms_norm output (bit-exact); the expert
+ * GEMMs dequantise Q4_K to bf16 and run on MFMA with fp32 accumulation
+ * (layers must have Q4_K down).  layers / d_norm_w: host arrays of
+ * n_layers layer ids / device pointers to [7168] fp32.  d_idx (optional,
+ * [n_layers][T][K]) receives every layer's routing.  1 <= T <= FDM_MAX_TOKENS. */
+int fdm_moe_prefill(const int *layers, int n_layers, float *d_H, int T, int K,
+                    const float *const *d_norm_w, int *d_idx, void *stream);
+
 /* ---- per-kernel GPU timing: replaces the host-clock moe_prof_t ring
  * (infer.m:177-261) with HIP events recorded on the launch stream around
  * every kernel of the entry points above.  fdm_prof_read synchronises on
@@ -175,7 +192,8 @@ int fdm_moe_forward_batched(int L, const float *d_X, const float *d_H_in, int T,
 #define FDM_PROF_MATVEC 4   /* fdm_matvec_q4k / _q6k kernel             */
 #define FDM_PROF_LAYER 5    /* fdm_moe_layer: the whole layer, 1 launch */
 #define FDM_PROF_BATCH 6    /* fdm_moe_forward_batched: the whole step  */
-#define FDM_PROF_PHASES 7
+#define FDM_PROF_PREFILL 7  /* fdm_moe_prefill: all layers              */
+#define FDM_PROF_PHASES 8
 int fdm_prof_enable(int on);
 int fdm_prof_reset(void);
 int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);
