@@ -233,7 +233,7 @@ def main():
 
     lb = layer_bytes(args.down, K)
     k_us = phases["layer"]["avg_us"]
-    achieved = lb / (k_us * 1e-6) / 1e9
+    achieved = lb / (k_us * 1e-6) / 1e9 if k_us > 0 else 0.0
     layer_gbps = lb / (us_per_token * 1e-6) / 1e9
     result = {
         "metric": METRIC,

@@ -26,10 +26,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kPTokens = 64;                       // tokens per GEMM item (4 N blocks)
-constexpr int kPNBlocks = kPTokens / 16;
-constexpr int kPGuTile = 64;                       // gate (and up) rows per gate/up workgroup
-constexpr int kPDnTile = 64;                       // down rows per down workgroup
+constexpr int kPTokens = 64;                       // tokens per shared-expert item and per down chunk
 
 // One lane's share of one Q4_K block for the MFMA A operand: the header and
 // the 8 qs bytes of each 64-element group that hold the lane's elements
@@ -55,7 +52,7 @@ __device__ __forceinline__ bf16x8 q4k_lane_bf16(const Q4KLane& r) {
   const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
   // get_scale_min_k4(S) (quant.c:26-34) on the 12 scale bytes s0|s1|s2
   int sc, m;
-  if (S < 4) {
+  if constexpr (S < 4) {
     sc = (int)((s0 >> (8 * S)) & 63u);
     m = (int)((s1 >> (8 * S)) & 63u);
   } else {
@@ -66,8 +63,11 @@ __device__ __forceinline__ bf16x8 q4k_lane_bf16(const Q4KLane& r) {
   const float d1 = half_to_float(r.hdr.x) * (float)sc;
   const float m1 = half_to_float(r.hdr.x >> 16) * (float)m;
   const uint2 w = r.qs[S >> 1];
-  const uint32_t lo = (S & 1) ? (w.x >> 4) & 0x0F0F0F0Fu : w.x & 0x0F0F0F0Fu;
-  const uint32_t hi = (S & 1) ? (w.y >> 4) & 0x0F0F0F0Fu : w.y & 0x0F0F0F0Fu;
+  uint32_t lo = (S & 1) ? (w.x >> 4) & 0x0F0F0F0Fu : w.x & 0x0F0F0F0Fu;
+  uint32_t hi = (S & 1) ? (w.y >> 4) & 0x0F0F0F0Fu : w.y & 0x0F0F0F0Fu;
+  // Opaque to the optimiser: otherwise it folds the mask into one bit-field
+  // extract per nibble instead of converting bytes 1..3 in place.
+  asm("" : "+v"(lo), "+v"(hi));
   f32x8 v;
   v[0] = d1 * (float)(lo & 0xFF) - m1;
   v[1] = d1 * (float)((lo >> 8) & 0xFF) - m1;
@@ -148,119 +148,262 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x,
   }
 }
 
+// ---- grouped GEMMs: shared structure ---------------------------------------------------------
+// A workgroup of kPWaves waves owns kPM = 16 kPWaves weight rows (wave w:
+// rows 16 w .. 16 w + 15, the A operand built from Q4_K in registers) and
+// walks the item's tokens in chunks (NB blocks of 16 tokens; only the
+// chunk's non-empty blocks do work).  Per Q4_K block (256 k) the chunk's B
+// tile -- NH halves (the hi/lo bf16 pair, or one) x 16 NB token rows x 256
+// bf16 -- is copied global -> LDS by the waves' direct LDS loads into one of
+// two buffers, so block b + 1 streams in while block b is contracted and one
+// barrier per block suffices.  The next block's A words are loaded at the
+// same point.
+//
+// LDS B rows are 512 B, unpadded; piece p (16 B, k = 8 p .. 8 p + 7) of token
+// row t sits at slot p ^ (t & 15).  An MFMA read (lanes 0..15: tokens
+// 16 nb + 0..15, one piece) then touches 16 distinct 16-byte bank groups.
+constexpr int kPWaves = 8;
+constexpr int kPM = 16 * kPWaves;                 // rows per workgroup
+constexpr int kPGuTokens = 32;                    // gate/up chunk (two A operands per wave)
+constexpr int kPRowB = kQK * 2;                   // LDS token row, bytes
+// B offsets are 32-bit: the largest, (T K + T) activation rows of 4 KiB at
+// K = 16, stays far below 4 GiB for the C API's cap of T <= 512 tokens.
+static_assert((size_t)512 * 17 * kFfn * 2 < (1ull << 31), "32-bit B offsets");
+
+// Direct LDS staging of one chunk: round k of wave w fills compact rows
+// 2 (w + 8 k) and 2 (w + 8 k) + 1 of the (half, token) space (half h, token
+// t < 16 NB: row h 16 NB + t); LDS row of (h, t) is h HT + t.  Rows past the
+// chunk's n_tok repeat its last token (their C columns are never written).
+template <int NB, int NH, int HT>
+struct BDma {
+  static constexpr int kRounds = NH * NB;  // 16 NB rows per half, 2 rows per wave round
+  uint32_t src[kRounds];                   // lane's global byte offset in block 0
+};
+
+template <int NB, int NH, int HT>
+__device__ __forceinline__ BDma<NB, NH, HT> bdma_init(const int* trow, int n_tok, uint32_t row_bytes,
+                                                      uint32_t half_bytes) {
+  BDma<NB, NH, HT> d;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < BDma<NB, NH, HT>::kRounds; ++k) {
+    const int rho = 2 * (wave + kPWaves * k) + (lane >> 5);
+    const int h = rho / (16 * NB), t = rho - h * 16 * NB;
+    const uint32_t piece = (uint32_t)((lane & 31) ^ (t & 15));
+    d.src[k] = h * half_bytes + (uint32_t)trow[min(t, n_tok - 1)] * row_bytes + 16u * piece;
+  }
+  return d;
+}
+
+template <int NB, int NH, int HT>
+__device__ __forceinline__ void bdma_issue(const BDma<NB, NH, HT>& d, const __bf16* src, __bf16* buf, int b) {
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(src) + (size_t)b * kPRowB;
+  const int wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < BDma<NB, NH, HT>::kRounds; ++k) {
+    const int rho0 = 2 * (wave + kPWaves * k);  // wave-uniform
+    const int h = rho0 / (16 * NB), t0 = rho0 - h * 16 * NB;
+    __builtin_amdgcn_global_load_lds(base + d.src[k],
+                                     reinterpret_cast<uint8_t*>(buf) + (h * HT + t0) * kPRowB, 16, 0, 0);
+  }
+}
+
+// The wave's direct LDS loads (and every other global load) have landed.
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// B operand of an MFMA from the LDS tile: token row tok = 16 nb + c16 of half
+// h, k-piece 4 S + j of the current block.
+template <int HT>
+__device__ __forceinline__ bf16x8 lds_b(const __bf16* bs, int h, int nb, int c16, int S, int j) {
+  const int t = 16 * nb + c16;
+  return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const uint8_t*>(bs) + (h * HT + t) * kPRowB +
+                                           16 * ((4 * S + j) ^ c16));
+}
+
 // ---- grouped gate/up GEMM + SwiGLU --------------------------------------------------------
-// Workgroup (tile, y): rows 64 tile .. +63 of gate AND up of item y; wave w
-// owns rows 16 w .. 16 w + 15 of both (two A operands per K step) and all
-// the item's tokens, 64 at a time (4 N blocks).  act = silu(g) * u goes out
-// as bf16 rows (the B operand of the down GEMM).
-__global__ __launch_bounds__(256) void k_pgateup(PrefillArgs p) {
-  PItem it;
-  if (!prefill_item(p, blockIdx.y, it)) return;
+// Item rows: gate AND up rows kPM tile .. +kPM-1 (two A operands per K
+// step) against the item's tokens as bf16 (hi, lo) pairs; act = silu(g) * u
+// goes out as bf16 rows (the B operand of the down GEMM).  One chunk of
+// n_tok <= 16 NB tokens.  The two B buffers are distinct LDS arrays and the
+// block loop is unrolled by two, so the compiler can tell that the reads of
+// one buffer do not depend on the direct loads still landing in the other.
+constexpr int kPGuBuf = 2 * kPGuTokens * kQK;  // bf16 per gate/up B buffer
+
+template <int NB>
+__device__ __forceinline__ void pgateup_block(const __bf16* cur, const Q4KLane& gl, const Q4KLane& ul,
+                                              f32x4 (&ag)[NB], f32x4 (&au)[NB], int c16, int j) {
+#define FDM_PGU_STEP(S)                                                  \
+  {                                                                      \
+    const bf16x8 ga = q4k_lane_bf16<S>(gl), ua = q4k_lane_bf16<S>(ul);   \
+    _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                  \
+      const bf16x8 bh = lds_b<kPGuTokens>(cur, 0, nb, c16, S, j);        \
+      const bf16x8 bl = lds_b<kPGuTokens>(cur, 1, nb, c16, S, j);        \
+      ag[nb] = mfma16(ga, bl, mfma16(ga, bh, ag[nb]));                   \
+      au[nb] = mfma16(ua, bl, mfma16(ua, bh, au[nb]));                   \
+    }                                                                    \
+  }                                                                      \
+  __builtin_amdgcn_sched_barrier(0);
+  FDM_PGU_STEP(0) FDM_PGU_STEP(1) FDM_PGU_STEP(2) FDM_PGU_STEP(3)
+  FDM_PGU_STEP(4) FDM_PGU_STEP(5) FDM_PGU_STEP(6) FDM_PGU_STEP(7)
+#undef FDM_PGU_STEP
+}
+
+template <int NB>
+__device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem& it, __bf16* bs0, __bf16* bs1,
+                                              const int* trow, int t0, int n_tok) {
+  constexpr int kBlocks = kHidden / kQK;  // 28, even
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane >> 4, c16 = lane & 15;
-  const int r = blockIdx.x * kPGuTile + wave * 16 + c16;  // the lane's A row
-  const uint8_t* grow = it.blob + (size_t)r * kQ4KRowHidden;
-  const uint8_t* urow = it.blob + kGateBytes + (size_t)r * kQ4KRowHidden;
-  const int P = p.T * p.K;
-  for (int t0 = 0; t0 < it.count; t0 += kPTokens) {
-    // B rows of the 4 N blocks: token (or pair) row of column c16
-    const __bf16* brow[kPNBlocks];
-    bool bval[kPNBlocks];
-    const size_t lo_off = (size_t)p.T * kHidden;  // lo half of the pair
+  const uint32_t roff = (uint32_t)(blockIdx.x * kPM + wave * 16 + c16) * kQ4KRowHidden;  // the lane's A row
+  const uint8_t* gbase = it.blob;
+  const uint8_t* ubase = it.blob + kGateBytes;
+  const BDma<NB, 2, kPGuTokens> dma =
+      bdma_init<NB, 2, kPGuTokens>(trow, n_tok, kHidden * 2, (uint32_t)p.T * kHidden * 2);
+  f32x4 ag[NB], au[NB];
 #pragma unroll
-    for (int nb = 0; nb < kPNBlocks; ++nb) {
-      const int t = t0 + nb * 16 + c16;
-      bval[nb] = t < it.count;
-      const int tok = !bval[nb] ? 0 : it.shared ? it.first + t : p.pair_tok[it.first + t];
-      brow[nb] = p.xb + (size_t)tok * kHidden + 8 * j;
-    }
-    f32x4 ag[kPNBlocks], au[kPNBlocks];
-#pragma unroll
-    for (int nb = 0; nb < kPNBlocks; ++nb) {
-      ag[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      au[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
-    for (int b = 0; b < kHidden / kQK; ++b) {
-      const Q4KLane gl = q4k_lane_load(grow + b * kQ4KBlock, j);
-      const Q4KLane ul = q4k_lane_load(urow + b * kQ4KBlock, j);
-#define FDM_PGU_STEP(S)                                                                   \
-  {                                                                                       \
-    const bf16x8 ga = q4k_lane_bf16<S>(gl), ua = q4k_lane_bf16<S>(ul);                    \
-    _Pragma("unroll") for (int nb = 0; nb < kPNBlocks; ++nb) {                            \
-      bf16x8 bh = {}, bl = {};                                                            \
-      if (bval[nb]) {                                                                     \
-        const __bf16* q_ = brow[nb] + b * kQK + 32 * (S);                                 \
-        bh = *reinterpret_cast<const bf16x8*>(q_);                                        \
-        bl = *reinterpret_cast<const bf16x8*>(q_ + lo_off);                               \
-      }                                                                                   \
-      ag[nb] = mfma16(ga, bl, mfma16(ga, bh, ag[nb]));                                    \
-      au[nb] = mfma16(ua, bl, mfma16(ua, bh, au[nb]));                                    \
-    }                                                                                     \
+  for (int nb = 0; nb < NB; ++nb) {
+    ag[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    au[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-      FDM_PGU_STEP(0) FDM_PGU_STEP(1) FDM_PGU_STEP(2) FDM_PGU_STEP(3)
-      FDM_PGU_STEP(4) FDM_PGU_STEP(5) FDM_PGU_STEP(6) FDM_PGU_STEP(7)
-#undef FDM_PGU_STEP
-    }
-    // C of a 16x16 block: lane (c16, j) holds token column c16, rows 4 j .. 4 j + 3
+  __syncthreads();  // both buffers free: the previous chunk's last block is read
+  bdma_issue(dma, p.xb, bs0, 0);
+  Q4KLane gn = q4k_lane_load(gbase + roff, j), un = q4k_lane_load(ubase + roff, j);
+  for (int b = 0; b < kBlocks; b += 2) {
+    // Even block b from bs0 while b + 1 lands in bs1; odd block b + 1 from
+    // bs1 while b + 2 lands in bs0 (the last pair re-stages block 27 into
+    // the idle buffer: branch-free, so the compiler's wait counts stay exact).
+    Q4KLane gl = gn, ul = un;
+    wait_vm();
+    __syncthreads();  // block b staged by every wave; bs1 read by all (block b - 1)
+    bdma_issue(dma, p.xb, bs1, b + 1);
+    gn = q4k_lane_load(gbase + (roff + (b + 1) * kQ4KBlock), j);
+    un = q4k_lane_load(ubase + (roff + (b + 1) * kQ4KBlock), j);
+    pgateup_block<NB>(bs0, gl, ul, ag, au, c16, j);
+    gl = gn;
+    ul = un;
+    const int b2 = min(b + 2, kBlocks - 1);
+    wait_vm();
+    __syncthreads();  // block b + 1 staged; bs0 read by all (block b)
+    bdma_issue(dma, p.xb, bs0, b2);
+    gn = q4k_lane_load(gbase + (roff + b2 * kQ4KBlock), j);
+    un = q4k_lane_load(ubase + (roff + b2 * kQ4KBlock), j);
+    pgateup_block<NB>(bs1, gl, ul, ag, au, c16, j);
+  }
+  wait_vm();  // the re-staged copy has landed before the buffers are reused
+  // C of a 16x16 block: lane (c16, j) holds token column c16, rows 4 j .. 4 j + 3.
+  const int P = p.T * p.K;
 #pragma unroll
-    for (int nb = 0; nb < kPNBlocks; ++nb) {
-      const int t = t0 + nb * 16 + c16;
-      if (t >= it.count) continue;
-      const int orow = it.shared ? P + it.first + t : it.first + t;
-      bf16x4 o;
+  for (int nb = 0; nb < NB; ++nb) {
+    const int t = nb * 16 + c16;
+    if (t >= n_tok) continue;
+    const int orow = it.shared ? P + it.first + t0 + t : it.first + t0 + t;
+    bf16x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = (__bf16)silu_mul(ag[nb][i], au[nb][i]);
-      *reinterpret_cast<bf16x4*>(p.actb + (size_t)orow * kFfn + blockIdx.x * kPGuTile + wave * 16 +
-                                 4 * j) = o;
-    }
+    for (int i = 0; i < 4; ++i) o[i] = (__bf16)silu_mul(ag[nb][i], au[nb][i]);
+    *reinterpret_cast<bf16x4*>(p.actb + (size_t)orow * kFfn + blockIdx.x * kPM + wave * 16 + 4 * j) = o;
+  }
+}
+
+__global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pgateup(
+    PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs0[kPGuBuf];
+  __shared__ __attribute__((aligned(16))) __bf16 bs1[kPGuBuf];
+  __shared__ int trow[kPGuTokens];
+  PItem it;
+  if (!prefill_item(p, blockIdx.y, it)) return;
+  for (int t0 = 0; t0 < it.count; t0 += kPGuTokens) {
+    const int n_tok = min(kPGuTokens, it.count - t0);
+    __syncthreads();  // the previous chunk's trow is no longer read
+    if (threadIdx.x < n_tok)
+      trow[threadIdx.x] = it.shared ? it.first + t0 + threadIdx.x : p.pair_tok[it.first + t0 + threadIdx.x];
+    __syncthreads();
+    if (n_tok > 16)
+      pgateup_chunk<2>(p, it, bs0, bs1, trow, t0, n_tok);
+    else
+      pgateup_chunk<1>(p, it, bs0, bs1, trow, t0, n_tok);
   }
 }
 
 // ---- grouped down GEMM ----------------------------------------------------------------------
-// Workgroup (tile, y): down rows 64 tile .. +63 of item y (wave w: rows
-// 16 w .. +15) against the item's bf16 activation rows; fp32 outputs.
-__global__ __launch_bounds__(256) void k_pdown(PrefillArgs p) {
-  PItem it;
-  if (!prefill_item(p, blockIdx.y, it)) return;
+// Item rows: down rows kPM tile .. +kPM-1 against the item's bf16
+// activation rows (contiguous); fp32 outputs.  Two B buffers of kPTokens
+// rows, as the gate/up GEMM.
+constexpr int kPDnBuf = kPTokens * kQK;  // bf16 per down B buffer
+
+template <int NB>
+__device__ __forceinline__ void pdown_block(const __bf16* cur, const Q4KLane& dl, f32x4 (&acc)[NB], int c16,
+                                            int j) {
+#define FDM_PDN_STEP(S)                                                                  \
+  {                                                                                      \
+    const bf16x8 da = q4k_lane_bf16<S>(dl);                                              \
+    _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                    \
+      acc[nb] = mfma16(da, lds_b<kPTokens>(cur, 0, nb, c16, S, j), acc[nb]);             \
+  }                                                                                      \
+  __builtin_amdgcn_sched_barrier(0);
+  FDM_PDN_STEP(0) FDM_PDN_STEP(1) FDM_PDN_STEP(2) FDM_PDN_STEP(3)
+  FDM_PDN_STEP(4) FDM_PDN_STEP(5) FDM_PDN_STEP(6) FDM_PDN_STEP(7)
+#undef FDM_PDN_STEP
+}
+
+template <int NB>
+__device__ __forceinline__ void pdown_chunk(const PrefillArgs& p, const PItem& it, __bf16* bs0, __bf16* bs1,
+                                            const int* trow, int row0, int n_tok) {
+  constexpr int kBlocks = kFfn / kQK;  // 8, even
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane >> 4, c16 = lane & 15;
-  const int r = blockIdx.x * kPDnTile + wave * 16 + c16;
-  const uint8_t* drow = it.blob + 2 * (size_t)kGateBytes + (size_t)r * kQ4KRowFfn;
+  const uint32_t roff = (uint32_t)(blockIdx.x * kPM + wave * 16 + c16) * kQ4KRowFfn;
+  const uint8_t* dbase = it.blob + 2 * (size_t)kGateBytes;
+  const BDma<NB, 1, kPTokens> dma = bdma_init<NB, 1, kPTokens>(trow, n_tok, kFfn * 2, 0);
+  f32x4 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  __syncthreads();
+  bdma_issue(dma, p.actb, bs0, 0);
+  Q4KLane dn = q4k_lane_load(dbase + roff, j);
+  for (int b = 0; b < kBlocks; b += 2) {
+    Q4KLane dl = dn;
+    wait_vm();
+    __syncthreads();
+    bdma_issue(dma, p.actb, bs1, b + 1);
+    dn = q4k_lane_load(dbase + (roff + (b + 1) * kQ4KBlock), j);
+    pdown_block<NB>(bs0, dl, acc, c16, j);
+    dl = dn;
+    const int b2 = min(b + 2, kBlocks - 1);
+    wait_vm();
+    __syncthreads();
+    bdma_issue(dma, p.actb, bs0, b2);
+    dn = q4k_lane_load(dbase + (roff + b2 * kQ4KBlock), j);
+    pdown_block<NB>(bs1, dl, acc, c16, j);
+  }
+  wait_vm();
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int t = nb * 16 + c16;
+    if (t >= n_tok) continue;
+    *reinterpret_cast<f32x4*>(p.eo + (size_t)(row0 + t) * kHidden + blockIdx.x * kPM + wave * 16 + 4 * j) =
+        acc[nb];
+  }
+}
+
+__global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pdown(
+    PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs0[kPDnBuf];
+  __shared__ __attribute__((aligned(16))) __bf16 bs1[kPDnBuf];
+  __shared__ int trow[kPTokens];
+  PItem it;
+  if (!prefill_item(p, blockIdx.y, it)) return;
   const int P = p.T * p.K;
   const int base = it.shared ? P + it.first : it.first;  // first activation row
   for (int t0 = 0; t0 < it.count; t0 += kPTokens) {
-    const __bf16* brow[kPNBlocks];
-    bool bval[kPNBlocks];
-#pragma unroll
-    for (int nb = 0; nb < kPNBlocks; ++nb) {
-      const int t = t0 + nb * 16 + c16;
-      bval[nb] = t < it.count;
-      brow[nb] = p.actb + (size_t)(bval[nb] ? base + t : 0) * kFfn + 8 * j;
-    }
-    f32x4 acc[kPNBlocks];
-#pragma unroll
-    for (int nb = 0; nb < kPNBlocks; ++nb) acc[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int b = 0; b < kFfn / kQK; ++b) {
-      const Q4KLane dl = q4k_lane_load(drow + b * kQ4KBlock, j);
-#define FDM_PDN_STEP(S)                                                                   \
-  {                                                                                       \
-    const bf16x8 da = q4k_lane_bf16<S>(dl);                                               \
-    _Pragma("unroll") for (int nb = 0; nb < kPNBlocks; ++nb) {                            \
-      bf16x8 bv = {};                                                                     \
-      if (bval[nb]) bv = *reinterpret_cast<const bf16x8*>(brow[nb] + b * kQK + 32 * (S)); \
-      acc[nb] = mfma16(da, bv, acc[nb]);                                                  \
-    }                                                                                     \
-  }
-      FDM_PDN_STEP(0) FDM_PDN_STEP(1) FDM_PDN_STEP(2) FDM_PDN_STEP(3)
-      FDM_PDN_STEP(4) FDM_PDN_STEP(5) FDM_PDN_STEP(6) FDM_PDN_STEP(7)
-#undef FDM_PDN_STEP
-    }
-#pragma unroll
-    for (int nb = 0; nb < kPNBlocks; ++nb) {
-      const int t = t0 + nb * 16 + c16;
-      if (t >= it.count) continue;
-      *reinterpret_cast<f32x4*>(p.eo + (size_t)(base + t) * kHidden + blockIdx.x * kPDnTile +
-                                wave * 16 + 4 * j) = acc[nb];
+    const int n_tok = min(kPTokens, it.count - t0);
+    __syncthreads();
+    if (threadIdx.x < n_tok) trow[threadIdx.x] = base + t0 + threadIdx.x;
+    __syncthreads();
+    switch ((n_tok + 15) >> 4) {
+      case 1: pdown_chunk<1>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+      case 2: pdown_chunk<2>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+      case 3: pdown_chunk<3>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+      default: pdown_chunk<4>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
     }
   }
 }
@@ -273,9 +416,9 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* o, __bf16* xb,
 
 hipError_t launch_prefill_experts(const PrefillArgs& p, hipStream_t s) {
   const int items = 256 + (p.shared ? (p.T + kPTokens - 1) / kPTokens : 0);
-  hipLaunchKernelGGL(k_pgateup, dim3(kFfn / kPGuTile, items), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(k_pgateup, dim3(kFfn / kPM, items), dim3(kPWaves * 64), 0, s, p);
   if (hipError_t e = hipGetLastError()) return e;
-  hipLaunchKernelGGL(k_pdown, dim3(kHidden / kPDnTile, items), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(k_pdown, dim3(kHidden / kPM, items), dim3(kPWaves * 64), 0, s, p);
   return hipGetLastError();
 }
 
