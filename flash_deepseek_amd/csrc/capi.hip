@@ -11,6 +11,7 @@
 namespace fdm {
 
 int g_num_cus = 0;
+int g_layer_mode = FDM_LAYER_AUTO;
 
 namespace {
 
@@ -673,10 +674,24 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   a.flags = g.ws.layer_flags;
   if (++g.ws.epoch == 0) ++g.ws.epoch;  // flags start at 0: skip epoch 0 on wrap
   a.epoch = g.ws.epoch;
+  // AUTO runs the work list: it measures faster than the streamed kernel on MI355X.
+  const bool streamed = g_layer_mode == FDM_LAYER_STREAM;
   {
     ProfScope p(FDM_PROF_LAYER, s);
-    FDM_HIP(launch_layer(a, s));
+    FDM_HIP(streamed ? launch_stream_layer(a, s) : launch_layer(a, s));
   }
+  return FDM_OK;
+}
+
+int fdm_set_layer_kernel(int mode, int* prev) {
+  if (int rc = check_ready()) return rc;
+  if (mode != FDM_LAYER_AUTO && mode != FDM_LAYER_ITEMS && mode != FDM_LAYER_STREAM)
+    return fail(FDM_E_INVAL, "layer kernel mode %d", mode);
+  if (mode == FDM_LAYER_STREAM && g_num_cus < stream_layer_workgroups())
+    return fail(FDM_E_INVAL, "the streamed layer needs %d CUs, the device has %d", stream_layer_workgroups(),
+                g_num_cus);
+  if (prev) *prev = g_layer_mode;
+  g_layer_mode = mode;
   return FDM_OK;
 }
 

@@ -124,19 +124,38 @@ __device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uin
   q4k_scale_min_pair(s0, s1, s2, q4k_scale_sel(g), sc_lo, m_lo, sc_hi, m_hi);
 }
 
+// One XGroup held in registers (36 VGPRs): digits a, b and {s0, s1, xsum0, xsum1}.
+struct XDig {
+  i32x4 a0, a1, a2, a3, b0, b1, b2, b3;
+  f32x4 meta;
+};
+
+__device__ __forceinline__ XDig load_xdig(const XGroup* __restrict__ xg) {
+  const i32x4* av = reinterpret_cast<const i32x4*>(xg->a);
+  const i32x4* bv = reinterpret_cast<const i32x4*>(xg->b);
+  XDig x;
+  x.a0 = av[0];
+  x.a1 = av[1];
+  x.a2 = av[2];
+  x.a3 = av[3];
+  x.b0 = bv[0];
+  x.b1 = bv[1];
+  x.b2 = bv[2];
+  x.b3 = bv[3];
+  x.meta = *reinterpret_cast<const f32x4*>(xg->s);
+  return x;
+}
+
 // Dot product of one Q4_K group (qs bytes 32g..32g+31 of a block, i.e.
 // elements 64g..64g+63) with the digits of the matching 64 activations.
 //   hdr = first 16 bytes of the block: d | dmin | scales[0..11]
 //   q0, q1 = the group's 32 qs bytes
 // Returns sum over the 64 elements of (d*sc*q - dmin*m) * x.
 __device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, const u32x4 q1,
-                                               const Q4KScaleSel& sel,
-                                               const XGroup* __restrict__ xg) {
-  const i32x4* av = reinterpret_cast<const i32x4*>(xg->a);
-  const i32x4* bv = reinterpret_cast<const i32x4*>(xg->b);
-  const i32x4 a0 = av[0], a1 = av[1], a2 = av[2], a3 = av[3];
-  const i32x4 b0 = bv[0], b1 = bv[1], b2 = bv[2], b3 = bv[3];
-  const f32x4 meta = *reinterpret_cast<const f32x4*>(xg->s);
+                                               const Q4KScaleSel& sel, const XDig& x) {
+  const i32x4 a0 = x.a0, a1 = x.a1, a2 = x.a2, a3 = x.a3;
+  const i32x4 b0 = x.b0, b1 = x.b1, b2 = x.b2, b3 = x.b3;
+  const f32x4 meta = x.meta;
   const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
   const uint32_t alo[8] = {(uint32_t)a0.x, (uint32_t)a0.y, (uint32_t)a0.z, (uint32_t)a0.w,
                            (uint32_t)a1.x, (uint32_t)a1.y, (uint32_t)a1.z, (uint32_t)a1.w};
@@ -168,6 +187,12 @@ __device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, 
   return fmaf(d, qx, -dmin * mx);
 }
 
+__device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, const u32x4 q1,
+                                               const Q4KScaleSel& sel,
+                                               const XGroup* __restrict__ xg) {
+  return q4k_group_dot(hdr, q0, q1, sel, load_xdig(xg));
+}
+
 // Broadcast lane `src` of each group of four lanes to the whole quad (DPP
 // quad_perm [src,src,src,src]; no LDS traffic).
 template <int SRC>
@@ -194,14 +219,22 @@ __device__ __forceinline__ Q4KGroupLoad q4k_load_group(const uint8_t* blk, int g
 }
 
 // Every lane of the quad must call this (it exchanges header dwords).
-__device__ __forceinline__ float q4k_group_dot_ld(const Q4KGroupLoad& r, const Q4KScaleSel& sel,
-                                                  const XGroup* __restrict__ xg) {
+__device__ __forceinline__ u32x4 q4k_quad_hdr(const Q4KGroupLoad& r) {
   u32x4 h;
   h.x = quad_bcast<0>(r.hdr_part);
   h.y = quad_bcast<1>(r.hdr_part);
   h.z = quad_bcast<2>(r.hdr_part);
   h.w = quad_bcast<3>(r.hdr_part);
-  return q4k_group_dot(h, r.q0, r.q1, sel, xg);
+  return h;
+}
+
+__device__ __forceinline__ float q4k_group_dot_ld(const Q4KGroupLoad& r, const Q4KScaleSel& sel,
+                                                  const XGroup* __restrict__ xg) {
+  return q4k_group_dot(q4k_quad_hdr(r), r.q0, r.q1, sel, xg);
+}
+
+__device__ __forceinline__ float q4k_group_dot_ld(const Q4KGroupLoad& r, const Q4KScaleSel& sel, const XDig& x) {
+  return q4k_group_dot(q4k_quad_hdr(r), r.q0, r.q1, sel, x);
 }
 
 // funnel: the 4 bytes starting `byte_shift` (0..3) bytes into the 8-byte

@@ -94,6 +94,9 @@ struct LayerArgs {
   unsigned epoch;          // non-zero, different from every earlier call's
 };
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
+// The same layer streamed by stream_layer_workgroups() resident workgroups.
+hipError_t launch_stream_layer(const LayerArgs& a, hipStream_t s);
+int stream_layer_workgroups();
 
 // batched_kernels.hip
 // Batched decode of T tokens through one layer with token -> expert

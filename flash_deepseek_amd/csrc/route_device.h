@@ -307,4 +307,116 @@ __device__ __forceinline__ void route_set_wave(const float score[4], const float
   if (lane < K) prov_idx[lane] = id;
 }
 
+// ---- the exact slot order without the sequential scan ---------------------------------------
+// The scan of slot_scan keeps, after each expert, the top-K of the keys seen
+// so far: expert e ENTERS a slot iff fewer than K earlier experts have a key
+// >= its own (and its key exceeds -1e30).  Among the entering experts
+// x_1, x_2, ... (index order) the first K fill slots 0 .. K-1 in order (the
+// empty slots are the first minima); each later x_m replaces the current
+// minimum, i.e. the earlier entry with exactly K-1 larger earlier entries,
+// and takes over its slot.  A slot ends with its last entry.  With all
+// entering keys distinct this reproduces the scan exactly; otherwise (or
+// with more than 63 entries) the scan itself runs.
+struct __attribute__((aligned(16))) RouteScratch {
+  int key[256];    // order-preserving keys of the masked choices (route_keys)
+  float sc[256];   // unbiased sigmoid scores
+  int enter[256];  // 1: the expert enters a slot at some point
+};
+
+// Four waves (threads t < 256, expert e = t): the enter flag of every expert.
+// Each wave scans the keys of experts below its last one (a uniform bound).
+__device__ __forceinline__ void route_enter_flags_aux(RouteScratch& r, int K, int t) {
+  const int e = t, ke = r.key[e];
+  const int n4 = 16 * ((t >> 6) + 1);  // 4-key steps covering experts 0 .. 64 w + 63
+  const int4* k4 = reinterpret_cast<const int4*>(r.key);
+  int cnt = 0;
+  for (int i = 0; i < n4; ++i) {
+    const int4 v = k4[i];
+    const int j = 4 * i;
+    cnt += (j + 0 < e && v.x >= ke) ? 1 : 0;
+    cnt += (j + 1 < e && v.y >= ke) ? 1 : 0;
+    cnt += (j + 2 < e && v.z >= ke) ? 1 : 0;
+    cnt += (j + 3 < e && v.w >= ke) ? 1 : 0;
+  }
+  r.enter[e] = (ke > sort_key(-1e30f) && cnt < K) ? 1 : 0;
+}
+
+// Wave 0, after route_enter_flags_aux: lane k (k < K) receives slot k's expert id
+// and weight, as slot_scan (vk, score: the wave's registers for the fallback).
+__device__ __forceinline__ void route_exact_slots(const RouteScratch& r, const int vk[4], const float score[4],
+                                                  int K, float scale, int& id_out, float& w_out) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  // compaction of the entering experts, in index order: entry i in lane i
+  int key = INT_MIN, id = 0, E = 0;
+  float sc = 0.0f;
+  bool fits = true;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned long long m = __ballot(r.enter[64 * j + lane] != 0);
+    const int n = __popcll(m);
+    if (E + n > 63) fits = false;  // lane 63 takes the pushes of unselected lanes
+    if (fits) {
+      const bool mine = (m >> lane) & 1ull;
+      const int pos = E + (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u));
+      const int src = 64 * j + lane;
+      const int kk = __builtin_amdgcn_ds_permute((mine ? pos : 63) * 4, r.key[src]);
+      const int ii = __builtin_amdgcn_ds_permute((mine ? pos : 63) * 4, src);
+      const int ss = __builtin_amdgcn_ds_permute((mine ? pos : 63) * 4, __float_as_int(r.sc[src]));
+      if (lane >= E && lane < E + n) {
+        key = kk;
+        id = ii;
+        sc = __int_as_float(ss);
+      }
+    }
+    E += n;
+  }
+  bool tie = !fits;
+  int cnt = 0;     // entries before the current one with a larger key (lanes < m)
+  int slot = -1;
+  for (int m = 0; m < E && !tie; ++m) {
+    const int km = __builtin_amdgcn_readlane(key, m);
+    const bool before = lane < m;
+    tie = __ballot(before && key == km) != 0ull;
+    const int larger = __popcll(__ballot(before && key > km));
+    int sm;
+    if (m < K) {
+      sm = m;
+    } else {
+      const unsigned long long ev = __ballot(before && cnt == K - 1);
+      tie = tie || __popcll(ev) != 1;
+      sm = __builtin_amdgcn_readlane(slot, ev ? __ffsll((unsigned long long)ev) - 1 : 0);
+    }
+    if (lane == m) {
+      slot = sm;
+      cnt = larger;
+    }
+    if (before && km > key) ++cnt;
+  }
+  if (tie) {
+    slot_scan(vk, score, K, scale, id_out, w_out);
+    return;
+  }
+  // slot k's last entry; a slot never filled keeps expert 0 (and its score)
+  int sid = 0;
+  float ssc = readlane_f(score[0], 0);
+  for (int k = 0; k < K; ++k) {
+    const unsigned long long b = __ballot(lane < E && slot == k);
+    if (b) {
+      const int last = 63 - __clzll(b);
+      const int idk = __builtin_amdgcn_readlane(id, last);
+      const float sck = readlane_f(sc, last);
+      if (lane == k) {
+        sid = idk;
+        ssc = sck;
+      }
+    }
+  }
+  float sum = 0.0f;
+  for (int k = 0; k < K; ++k) sum += readlane_f(ssc, k);
+  const float f = sum > 0.0f ? __fdiv_rn(scale, sum) : 1.0f;
+  id_out = sid;
+  w_out = sum > 0.0f ? ssc * f : ssc;
+}
+
 }  // namespace fdm

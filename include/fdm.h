@@ -150,6 +150,17 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
 
+/* Kernel behind fdm_moe_layer (no counterpart in the reference, which has
+ * one Metal path; a tuning and test switch): FDM_LAYER_ITEMS runs the
+ * ordered work list, FDM_LAYER_STREAM streams the layer through 256
+ * resident workgroups (fails with FDM_E_INVAL on a device with fewer than
+ * 256 CUs) and FDM_LAYER_AUTO picks the faster one, currently ITEMS.
+ * Stores the previous mode in *prev when prev is not NULL. */
+#define FDM_LAYER_AUTO 0
+#define FDM_LAYER_ITEMS 1
+#define FDM_LAYER_STREAM 2
+int fdm_set_layer_kernel(int mode, int *prev);
+
 /* ---- batched decode: T tokens through the MoE branch of layer L in one
  * step, with token -> expert dispatch so that each selected expert's weights
  * are read once per step (config 3; the reference decodes one token at a
