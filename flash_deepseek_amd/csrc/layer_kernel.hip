@@ -244,14 +244,17 @@ __device__ __forceinline__ void wait_scores(const LayerArgs& a, float sc[4]) {
 }
 
 // ---- route: the expert set ------------------------------------------------------------
+// On the critical path of every routed weight load: the bias is fetched
+// before the wait, and the wave issues ahead of the SIMD's expert waves.
 __device__ __forceinline__ void route_item(const LayerArgs& a) {
   const int lane = threadIdx.x & 63;
-  float sc[4];
-  wait_scores(a, sc);
-  if (threadIdx.x >= 64) return;
+  __builtin_amdgcn_s_setprio(3);
   float bj[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) bj[j] = a.bias ? a.bias[64 * j + lane] : 0.0f;
+  float sc[4];
+  wait_scores(a, sc);
+  if (threadIdx.x >= 64) return;
   const int id = route_set_lane(sc, bj, a.K);
   if (lane < a.K) put_tagged(a.prov + lane, a.epoch, (uint32_t)id);
 }

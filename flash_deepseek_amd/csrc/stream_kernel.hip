@@ -39,8 +39,10 @@
 // nor inserts waits for them; every wait on them is an explicit s_waitcnt.
 //
 // Requires all 256 workgroups to be resident at once (one per CU: the LDS
-// footprint allows no second one); the host uses it only on devices with
-// at least 256 CUs.  Every cross-workgroup wait is bounded like the item
+// footprint allows no second one); the host runs it only when selected
+// (fdm_set_layer_kernel) and only on devices with at least 256 CUs.  It
+// measures slower than the item kernel on MI355X (~77 vs ~61 us per
+// token), so it is not the default.  Every cross-workgroup wait is bounded like the item
 // kernel's: a timeout records the call's epoch in the error flag, which
 // releases every other wait, and the launch completes.
 #include "fdm_internal.h"
