@@ -17,6 +17,7 @@ FDM_E_STATE = -4
 FDM_E_NOMEM = -5
 FDM_E_SIZE = -6
 FDM_E_IO = -7
+FDM_E_FORMAT = -8
 
 (PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER, PROF_BATCH,
  PROF_PREFILL) = range(8)
@@ -79,6 +80,22 @@ SIGNATURES = {
     "fdm_synth_q4k": [_vp, _sz, _u64, _vp],
     "fdm_synth_q6k": [_vp, _sz, _u64, _vp],
     "fdm_synth_normal": [_vp, _sz, _f, _f, _u64, _vp],
+    "fdm_gguf_open": [ctypes.POINTER(ctypes.c_char_p), _i, ctypes.POINTER(_vp)],
+    "fdm_gguf_close": [_vp],
+    "fdm_gguf_count": [_vp, ctypes.POINTER(_i), ctypes.POINTER(_u64)],
+    "fdm_gguf_shard_info": [_vp, _i, ctypes.POINTER(_u32), ctypes.POINTER(_u64),
+                            ctypes.POINTER(_u64), ctypes.POINTER(_u64), ctypes.POINTER(_u64)],
+    "fdm_gguf_find": [_vp, ctypes.c_char_p, _vp],
+    "fdm_gguf_tensor_at": [_vp, _u64, ctypes.c_char_p, _sz, _vp],
+    "fdm_gguf_find_kv": [_vp, _i, ctypes.c_char_p, ctypes.POINTER(_i), ctypes.POINTER(_i),
+                         ctypes.POINTER(_u64)],
+    "fdm_gguf_kv_int": [_vp, _i, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)],
+    "fdm_gguf_kv_float": [_vp, _i, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)],
+    "fdm_gguf_kv_str": [_vp, _i, ctypes.c_char_p, ctypes.c_char_p, _sz],
+    "fdm_gguf_read": [_vp, ctypes.c_char_p, _vp, _u64, _u64],
+    "fdm_ggml_type_geometry": [_i, ctypes.POINTER(_u64), ctypes.POINTER(_u64)],
+    "fdm_layer_load_gguf": [_i, _vp, _i, ctypes.POINTER(_i)],
+    "fdm_layer_load_packed": [_i, ctypes.c_char_p, _vp, _i, ctypes.POINTER(_i)],
 }
 _RESTYPES = {"fdm_strerror": ctypes.c_char_p, "fdm_last_error": ctypes.c_char_p}
 

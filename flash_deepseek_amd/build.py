@@ -28,6 +28,7 @@ SOURCES = [
     "batched_kernels.hip",
     "prefill_kernels.hip",
     "synth_kernels.hip",
+    "gguf_host.hip",
     "capi.hip",
 ]
 

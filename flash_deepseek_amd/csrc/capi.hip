@@ -1,9 +1,15 @@
 // capi.hip -- the C ABI declared in include/fdm.h: argument checks, the
 // per-device workspace, the resident-layer table and the kernel sequences.
 // The kernels themselves live in *_kernels.hip.
+#include <errno.h>
+#include <fcntl.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <initializer_list>
 
 #include "../../include/fdm.h"
 #include "fdm_internal.h"
@@ -256,7 +262,211 @@ SlotTable slots_for(const Layer& L, const int* idx, const float* w, int K, bool 
   return t;
 }
 
+// ---- ingest helpers -------------------------------------------------------------------
+
+// Host -> device copies through a ring of pinned staging buffers: each
+// chunk is read from its file (pread) into the next free buffer and its
+// copy queued on a private stream, so the file reads overlap the PCIe
+// copies of the chunks before.
+class Uploader {
+ public:
+  static constexpr size_t kChunk = 16u << 20;
+  static constexpr int kBufs = 3;
+  ~Uploader() {
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    for (int i = 0; i < kBufs; ++i) {
+      if (ev_[i]) (void)hipEventDestroy(ev_[i]);
+      if (buf_[i]) (void)hipHostFree(buf_[i]);
+    }
+    if (stream_) (void)hipStreamDestroy(stream_);
+  }
+  int init() {
+    FDM_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    for (int i = 0; i < kBufs; ++i) {
+      FDM_HIP(hipHostMalloc(&buf_[i], kChunk, hipHostMallocDefault));
+      FDM_HIP(hipEventCreateWithFlags(&ev_[i], hipEventDisableTiming));
+    }
+    return FDM_OK;
+  }
+  // n bytes produced by read(host_dst, bytes, offset) -> dev
+  template <typename Read>
+  int copy(void* dev, uint64_t n, Read&& read) {
+    for (uint64_t off = 0; off < n; off += kChunk) {
+      const size_t m = (size_t)(n - off < kChunk ? n - off : kChunk);
+      const int i = next_++ % kBufs;
+      if (used_[i]) FDM_HIP(hipEventSynchronize(ev_[i]));
+      if (int rc = read(buf_[i], (uint64_t)m, off)) return rc;
+      FDM_HIP(hipMemcpyAsync(static_cast<uint8_t*>(dev) + off, buf_[i], m, hipMemcpyHostToDevice,
+                             stream_));
+      FDM_HIP(hipEventRecord(ev_[i], stream_));
+      used_[i] = true;
+      bytes_ += m;
+    }
+    return FDM_OK;
+  }
+  int finish() {
+    FDM_HIP(hipStreamSynchronize(stream_));
+    return FDM_OK;
+  }
+
+ private:
+  hipStream_t stream_ = nullptr;
+  void* buf_[kBufs] = {};
+  hipEvent_t ev_[kBufs] = {};
+  bool used_[kBufs] = {};
+  int next_ = 0;
+  uint64_t bytes_ = 0;
+};
+
+// IEEE half -> float by integer construction (every finite, infinite and
+// NaN pattern; subnormals normalised).
+float half_bits_to_float(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1Fu, f = h & 0x3FFu;
+  uint32_t bits;
+  if (e == 0x1Fu) {
+    bits = sign | 0x7F800000u | (f << 13);
+  } else if (e) {
+    bits = sign | ((e + 112u) << 23) | (f << 13);
+  } else if (!f) {
+    bits = sign;
+  } else {
+    const uint32_t p = 31u - (uint32_t)__builtin_clz(f), shift = 10u - p;
+    bits = sign | ((113u - shift) << 23) | (((f << shift) & 0x3FFu) << 13);
+  }
+  float v;
+  memcpy(&v, &bits, 4);
+  return v;
+}
+
+// A GGUF tensor with the expected type set and shape.
+int expect_tensor(const GgufManifest& m, const char* name, const GgufTensor** out,
+                  std::initializer_list<uint32_t> types, std::initializer_list<uint64_t> dims) {
+  const GgufTensor* t = m.find(name);
+  if (!t) return fail(FDM_E_FORMAT, "tensor %s not in the GGUF", name);
+  bool type_ok = false;
+  for (uint32_t ty : types) type_ok = type_ok || t->type == ty;
+  if (!type_ok) return fail(FDM_E_FORMAT, "tensor %s has ggml type %u", name, t->type);
+  if (t->n_dims != dims.size()) return fail(FDM_E_FORMAT, "tensor %s has %u dims", name, t->n_dims);
+  int d = 0;
+  for (uint64_t want : dims) {
+    if (t->dims[d] != want)
+      return fail(FDM_E_FORMAT, "tensor %s: ne[%d] = %llu, expected %llu", name, d,
+                  (unsigned long long)t->dims[d], (unsigned long long)want);
+    ++d;
+  }
+  *out = t;
+  return FDM_OK;
+}
+
+// An F32 / F16 / BF16 tensor of n elements, widened to fp32 on the host.
+int read_f32(const GgufManifest& m, const GgufTensor& t, std::vector<float>& out) {
+  const uint64_t n = t.nbytes / (t.type == FDM_GGML_F32 ? 4 : 2);
+  out.resize(n);
+  if (t.type == FDM_GGML_F32) return m.read(t, out.data(), t.nbytes, 0);
+  std::vector<uint16_t> raw(n);
+  if (int rc = m.read(t, raw.data(), t.nbytes, 0)) return rc;
+  for (uint64_t i = 0; i < n; ++i) {
+    if (t.type == FDM_GGML_F16) {
+      out[i] = half_bits_to_float(raw[i]);
+    } else {
+      const uint32_t b = (uint32_t)raw[i] << 16;
+      memcpy(&out[i], &b, 4);
+    }
+  }
+  return FDM_OK;
+}
+
+// Router weights, bias and (optionally) the shared expert's three tensors of
+// layer L, checked against the R1 shapes; the shared down type must be q6.
+struct LayerTensors {
+  const GgufTensor *router = nullptr, *bias = nullptr;
+  const GgufTensor *sgate = nullptr, *sup = nullptr, *sdown = nullptr;
+};
+int find_layer_common(const GgufManifest& m, int L, bool with_shared, bool q6, LayerTensors* lt) {
+  char name[128];
+  const std::initializer_list<uint32_t> fp = {FDM_GGML_F32, FDM_GGML_F16, FDM_GGML_BF16};
+  snprintf(name, sizeof name, "blk.%d.ffn_gate_inp.weight", L);
+  if (int rc = expect_tensor(m, name, &lt->router, fp, {FDM_HIDDEN, FDM_N_EXPERTS})) return rc;
+  // the correction bias is optional (route() then adds nothing); .bias or .weight
+  snprintf(name, sizeof name, "blk.%d.exp_probs_b.bias", L);
+  if (!m.find(name)) snprintf(name, sizeof name, "blk.%d.exp_probs_b.weight", L);
+  if (m.find(name))
+    if (int rc = expect_tensor(m, name, &lt->bias, fp, {FDM_N_EXPERTS})) return rc;
+  if (!with_shared) return FDM_OK;
+  snprintf(name, sizeof name, "blk.%d.ffn_gate_shexp.weight", L);
+  if (int rc = expect_tensor(m, name, &lt->sgate, {FDM_GGML_Q4_K}, {FDM_HIDDEN, FDM_MOE_FFN})) return rc;
+  snprintf(name, sizeof name, "blk.%d.ffn_up_shexp.weight", L);
+  if (int rc = expect_tensor(m, name, &lt->sup, {FDM_GGML_Q4_K}, {FDM_HIDDEN, FDM_MOE_FFN})) return rc;
+  snprintf(name, sizeof name, "blk.%d.ffn_down_shexp.weight", L);
+  if (int rc = expect_tensor(m, name, &lt->sdown, {FDM_GGML_Q4_K, FDM_GGML_Q6_K}, {FDM_MOE_FFN, FDM_HIDDEN}))
+    return rc;
+  if ((lt->sdown->type == FDM_GGML_Q6_K) != q6)
+    return fail(FDM_E_FORMAT, "layer %d: the shared expert's down type differs from the routed experts'", L);
+  return FDM_OK;
+}
+
+// Device buffers of one layer under construction; freed unless committed.
+struct LayerBuffers {
+  void *experts = nullptr, *Wg = nullptr, *bias = nullptr, *shared = nullptr;
+  ~LayerBuffers() {
+    for (void* p : {experts, Wg, bias, shared})
+      if (p) (void)hipFree(p);
+  }
+  int alloc(size_t es, bool bias_, bool shared_, int L) {
+    const size_t eb = es * FDM_N_EXPERTS, wb = (size_t)FDM_N_EXPERTS * FDM_HIDDEN * sizeof(float);
+    if (hipMalloc(&experts, eb) != hipSuccess || hipMalloc(&Wg, wb) != hipSuccess ||
+        (bias_ && hipMalloc(&bias, FDM_N_EXPERTS * sizeof(float)) != hipSuccess) ||
+        (shared_ && hipMalloc(&shared, es) != hipSuccess))
+      return fail(FDM_E_NOMEM, "cannot allocate %zu bytes for layer %d", eb + wb + es, L);
+    return FDM_OK;
+  }
+};
+
+// Router, bias and shared expert of a layer under construction.
+int upload_layer_common(const GgufManifest& m, const LayerTensors& lt, LayerBuffers& b, Uploader& up,
+                        size_t down_bytes) {
+  std::vector<float> v;
+  if (int rc = read_f32(m, *lt.router, v)) return rc;
+  FDM_HIP(hipMemcpy(b.Wg, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+  if (lt.bias) {
+    if (int rc = read_f32(m, *lt.bias, v)) return rc;
+    FDM_HIP(hipMemcpy(b.bias, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+  }
+  if (lt.sgate) {
+    const GgufTensor* parts[3] = {lt.sgate, lt.sup, lt.sdown};
+    const uint64_t at[3] = {0, (uint64_t)kGateBytes, 2ull * kGateBytes};
+    for (int p = 0; p < 3; ++p) {
+      const uint64_t n = p < 2 ? (uint64_t)kGateBytes : down_bytes;
+      if (int rc = up.copy(static_cast<uint8_t*>(b.shared) + at[p], n,
+                           [&](void* dst, uint64_t k, uint64_t off) { return m.read(*parts[p], dst, k, off); }))
+        return rc;
+    }
+  }
+  return FDM_OK;
+}
+
+int commit_layer(int L, LayerBuffers& b, size_t es, bool q6) {
+  release_layer(g.layers[L]);
+  Layer& y = g.layers[L];
+  y.resident = true;
+  y.owned = true;
+  y.experts = static_cast<const uint8_t*>(b.experts);
+  y.expert_size = es;
+  y.n_experts = FDM_N_EXPERTS;
+  y.down_q6 = q6;
+  y.Wg = static_cast<const float*>(b.Wg);
+  y.bias = static_cast<const float*>(b.bias);
+  y.shared = static_cast<const uint8_t*>(b.shared);
+  b = LayerBuffers();  // ownership moved to the layer table
+  return FDM_OK;
+}
+
 }  // namespace
+
+void set_last_error(const char* msg) {
+  snprintf(t_err, sizeof t_err, "%s", msg);
+}
+
 }  // namespace fdm
 
 using namespace fdm;
@@ -317,6 +527,7 @@ const char* fdm_strerror(int code) {
     case FDM_E_NOMEM: return "device allocation failed";
     case FDM_E_SIZE: return "expert size matches neither R1 layout";
     case FDM_E_IO: return "file error";
+    case FDM_E_FORMAT: return "malformed model file";
     default: return "unknown error";
   }
 }
@@ -578,6 +789,94 @@ int fdm_layer_upload(int L, const void* h_experts, size_t expert_size, int n_exp
   y.bias = static_cast<const float*>(db);
   y.shared = static_cast<const uint8_t*>(ds);
   return FDM_OK;
+}
+
+int fdm_layer_load_gguf(int L, const fdm_gguf* mh, int with_shared, int* down_is_q6) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  const GgufManifest* m = gguf_manifest(mh);
+  if (!m) return fail(FDM_E_INVAL, "null manifest");
+  char name[128];
+  const GgufTensor *tg = nullptr, *tu = nullptr, *td = nullptr;
+  snprintf(name, sizeof name, "blk.%d.ffn_gate_exps.weight", L);
+  if (int rc = expect_tensor(*m, name, &tg, {FDM_GGML_Q4_K}, {FDM_HIDDEN, FDM_MOE_FFN, FDM_N_EXPERTS}))
+    return rc;
+  snprintf(name, sizeof name, "blk.%d.ffn_up_exps.weight", L);
+  if (int rc = expect_tensor(*m, name, &tu, {FDM_GGML_Q4_K}, {FDM_HIDDEN, FDM_MOE_FFN, FDM_N_EXPERTS}))
+    return rc;
+  snprintf(name, sizeof name, "blk.%d.ffn_down_exps.weight", L);
+  if (int rc = expect_tensor(*m, name, &td, {FDM_GGML_Q4_K, FDM_GGML_Q6_K},
+                             {FDM_MOE_FFN, FDM_HIDDEN, FDM_N_EXPERTS}))
+    return rc;
+  const bool q6 = td->type == FDM_GGML_Q6_K;
+  const size_t down_bytes = td->nbytes / FDM_N_EXPERTS;
+  const size_t es = 2 * (size_t)kGateBytes + down_bytes;
+  LayerTensors lt;
+  if (int rc = find_layer_common(*m, L, with_shared != 0, q6, &lt)) return rc;
+  LayerBuffers b;
+  if (int rc = b.alloc(es, lt.bias != nullptr, with_shared != 0, L)) return rc;
+  Uploader up;
+  if (int rc = up.init()) return rc;
+  // expert e of each stacked tensor is one contiguous slice: scatter them
+  // into the packed blobs [gate | up | down] at e * expert_size
+  const GgufTensor* parts[3] = {tg, tu, td};
+  const uint64_t sz[3] = {(uint64_t)kGateBytes, (uint64_t)kGateBytes, down_bytes};
+  const uint64_t at[3] = {0, (uint64_t)kGateBytes, 2ull * kGateBytes};
+  for (int e = 0; e < FDM_N_EXPERTS; ++e)
+    for (int p = 0; p < 3; ++p) {
+      const uint64_t src = (uint64_t)e * sz[p];
+      if (int rc = up.copy(static_cast<uint8_t*>(b.experts) + (size_t)e * es + at[p], sz[p],
+                           [&](void* dst, uint64_t k, uint64_t off) { return m->read(*parts[p], dst, k, src + off); }))
+        return rc;
+    }
+  if (int rc = upload_layer_common(*m, lt, b, up, down_bytes)) return rc;
+  if (int rc = up.finish()) return rc;
+  if (down_is_q6) *down_is_q6 = q6 ? 1 : 0;
+  return commit_layer(L, b, es, q6);
+}
+
+int fdm_layer_load_packed(int L, const char* layer_file, const fdm_gguf* mh, int with_shared,
+                          int* down_is_q6) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  const GgufManifest* m = gguf_manifest(mh);
+  if (!m || !layer_file) return fail(FDM_E_INVAL, "null manifest or layer file");
+  const int fd = open(layer_file, O_RDONLY);
+  if (fd < 0) return fail(FDM_E_IO, "open %s: %s", layer_file, strerror(errno));
+  struct FdCloser {
+    int fd;
+    ~FdCloser() { close(fd); }
+  } closer{fd};
+  struct stat st;
+  if (fstat(fd, &st) != 0) return fail(FDM_E_IO, "fstat %s: %s", layer_file, strerror(errno));
+  // 256 blobs; the expert size, hence the down type, from the file size
+  if (st.st_size <= 0 || st.st_size % FDM_N_EXPERTS)
+    return fail(FDM_E_SIZE, "%s: %lld bytes is not 256 expert blobs", layer_file, (long long)st.st_size);
+  const size_t es = (size_t)st.st_size / FDM_N_EXPERTS;
+  bool q6 = false;
+  if (int rc = down_type(es, &q6)) return rc;
+  LayerTensors lt;
+  if (int rc = find_layer_common(*m, L, with_shared != 0, q6, &lt)) return rc;
+  LayerBuffers b;
+  if (int rc = b.alloc(es, lt.bias != nullptr, with_shared != 0, L)) return rc;
+  Uploader up;
+  if (int rc = up.init()) return rc;
+  // the packed layout is the library's: one contiguous copy
+  if (int rc = up.copy(b.experts, (uint64_t)st.st_size, [&](void* dst, uint64_t k, uint64_t off) {
+        uint64_t got = 0;
+        while (got < k) {
+          const ssize_t r = pread(fd, static_cast<uint8_t*>(dst) + got, k - got, (off_t)(off + got));
+          if (r < 0 && errno == EINTR) continue;
+          if (r <= 0) return fail(FDM_E_IO, "read of %s: %s", layer_file, r < 0 ? strerror(errno) : "end of file");
+          got += (uint64_t)r;
+        }
+        return (int)FDM_OK;
+      }))
+    return rc;
+  if (int rc = upload_layer_common(*m, lt, b, up, es - 2 * (size_t)kGateBytes)) return rc;
+  if (int rc = up.finish()) return rc;
+  if (down_is_q6) *down_is_q6 = q6 ? 1 : 0;
+  return commit_layer(L, b, es, q6);
 }
 
 int fdm_layer_release(int L) {

@@ -7,7 +7,14 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+#include <unordered_map>
+#include <utility>
+#include <vector>
+
 #include "fdm_device.h"
+
+struct fdm_gguf;  // the C ABI's opaque manifest handle
 
 namespace fdm {
 
@@ -158,5 +165,46 @@ hipError_t launch_synth_normal(float* dst, size_t n, float mean, float std_dev, 
 
 // grid sizing: number of CUs of the current device (set by fdm_init)
 extern int g_num_cus;
+
+// capi.hip: the thread's fdm_last_error() text
+void set_last_error(const char* msg);
+
+// gguf_host.hip: GGUF shards and the multi-shard manifest (host side)
+struct GgufKv {
+  std::string key;
+  uint32_t type = 0;      // FDM_GGUF_* value type
+  uint64_t raw = 0;       // scalar payload, little-endian bits
+  std::string str;        // string payload
+  uint32_t arr_type = 0;  // array element type
+  uint64_t arr_n = 0;     // array length
+};
+struct GgufTensor {
+  std::string name;
+  uint32_t n_dims = 0;
+  uint64_t dims[4] = {1, 1, 1, 1};
+  uint32_t type = 0;      // ggml type id
+  uint64_t rel_offset = 0, abs_offset = 0, nbytes = 0;
+  int shard = -1;
+};
+struct GgufShard {
+  std::string path;
+  int fd = -1;
+  uint32_t version = 0;
+  uint64_t alignment = 32, data_start = 0, file_size = 0;
+  std::vector<GgufKv> kvs;
+  std::vector<GgufTensor> tensors;
+};
+struct GgufManifest {
+  std::vector<GgufShard> shards;
+  std::unordered_map<std::string, std::pair<int, size_t>> index;  // name -> (shard, tensor)
+  std::vector<std::pair<int, size_t>> order;                       // shard order, file order
+  ~GgufManifest();
+  const GgufTensor* find(const char* name) const;
+  const GgufKv* find_kv(int shard, const char* key) const;
+  // n bytes of t starting `rel` bytes in, into host memory
+  int read(const GgufTensor& t, void* dst, uint64_t n, uint64_t rel) const;
+};
+uint64_t ggml_nbytes(uint32_t type, const uint64_t* dims, uint32_t n_dims);
+const GgufManifest* gguf_manifest(const fdm_gguf* g);
 
 }  // namespace fdm

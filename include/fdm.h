@@ -58,6 +58,7 @@ extern "C" {
 #define FDM_E_NOMEM (-5)   /* device allocation failed                      */
 #define FDM_E_SIZE (-6)    /* expert size matches neither R1 layout          */
 #define FDM_E_IO (-7)      /* file open/read failed (host ingest)           */
+#define FDM_E_FORMAT (-8)  /* malformed GGUF or layer file                  */
 
 /* ---- lifecycle: replaces metal_init (infer.m:1276-1400) -------------------
  * fdm_init selects `device`, checks it is gfx950 and allocates the
@@ -126,6 +127,87 @@ int fdm_layer_upload(int L, const void *h_experts, size_t expert_size, int n_exp
                      const float *h_Wg, const float *h_bias, const void *h_shared);
 int fdm_layer_release(int L);
 int fdm_layer_query(int L, size_t *expert_size, int *down_is_q6, int *n_experts);
+
+/* ---- real-weight ingest: GGUF shards (replaces gguf_load_manifest,
+ * gguf_find, gguf_find_kv and gguf_tensor_pread, gguf.h:163-192,
+ * gguf.c:285-551).  Host-side only; none of these calls needs fdm_init.
+ * GGUF v2 and v3; general.alignment (u32 or u64, default 32) places the
+ * data section.  Errors (FDM_E_FORMAT): bad magic or version, 0 or more
+ * than 4 dims, a shape that is not whole blocks of its type, a tensor past
+ * the end of its file, the same tensor name in two shards. */
+typedef struct fdm_gguf fdm_gguf;
+
+/* metadata value types (the GGUF format's) */
+#define FDM_GGUF_UINT8 0
+#define FDM_GGUF_INT8 1
+#define FDM_GGUF_UINT16 2
+#define FDM_GGUF_INT16 3
+#define FDM_GGUF_UINT32 4
+#define FDM_GGUF_INT32 5
+#define FDM_GGUF_FLOAT32 6
+#define FDM_GGUF_BOOL 7
+#define FDM_GGUF_STRING 8
+#define FDM_GGUF_ARRAY 9
+#define FDM_GGUF_UINT64 10
+#define FDM_GGUF_INT64 11
+#define FDM_GGUF_FLOAT64 12
+
+/* ggml tensor types used by the MoE path (ids are ggml's) */
+#define FDM_GGML_F32 0
+#define FDM_GGML_F16 1
+#define FDM_GGML_Q4_K 12
+#define FDM_GGML_Q6_K 14
+#define FDM_GGML_BF16 30
+
+typedef struct fdm_gguf_tensor_info {
+  int type;           /* ggml type id */
+  int n_dims;         /* 1..4 */
+  uint64_t dims[4];   /* ne[0] (innermost) .. ne[3]; 1 beyond n_dims */
+  uint64_t nbytes;    /* from type and shape */
+  uint64_t offset;    /* absolute byte offset of the data in its shard file */
+  int shard;          /* index into the paths given to fdm_gguf_open */
+} fdm_gguf_tensor_info;
+
+int fdm_gguf_open(const char *const *paths, int n_paths, fdm_gguf **out);
+int fdm_gguf_close(fdm_gguf *m);
+int fdm_gguf_count(const fdm_gguf *m, int *n_shards, uint64_t *n_tensors);
+int fdm_gguf_shard_info(const fdm_gguf *m, int shard, uint32_t *version, uint64_t *alignment,
+                        uint64_t *data_start, uint64_t *n_kv, uint64_t *n_tensors);
+/* tensor by name (FDM_E_STATE if absent), or the i-th in shard, then file, order */
+int fdm_gguf_find(const fdm_gguf *m, const char *name, fdm_gguf_tensor_info *info);
+int fdm_gguf_tensor_at(const fdm_gguf *m, uint64_t i, char *name, size_t name_cap,
+                       fdm_gguf_tensor_info *info);
+/* metadata of one shard: type (FDM_GGUF_*), array element type and length */
+int fdm_gguf_find_kv(const fdm_gguf *m, int shard, const char *key, int *type, int *arr_type,
+                     uint64_t *arr_n);
+int fdm_gguf_kv_int(const fdm_gguf *m, int shard, const char *key, int64_t *v);
+int fdm_gguf_kv_float(const fdm_gguf *m, int shard, const char *key, double *v);
+int fdm_gguf_kv_str(const fdm_gguf *m, int shard, const char *key, char *buf, size_t cap);
+/* n bytes of a tensor starting `rel` bytes in, into host memory (FDM_E_INVAL
+ * past the tensor's end) */
+int fdm_gguf_read(const fdm_gguf *m, const char *name, void *h_buf, uint64_t n, uint64_t rel);
+/* elements and bytes per block of a ggml type (ggml_blck_size / ggml_type_size) */
+int fdm_ggml_type_geometry(int type, uint64_t *block_elems, uint64_t *block_bytes);
+
+/* ---- a resident MoE layer straight from the model's files: replaces
+ * repack_experts.c (stacked expert tensors -> per-expert blobs,
+ * repack_experts.c:124-258) and the MoE part of load_layer_weights
+ * (infer.m:1794-1823).  The library allocates the layer (as
+ * fdm_layer_upload) and assembles the packed layout in HBM.
+ *  - from GGUF: blk.L.ffn_{gate,up,down}_exps.weight (gate/up Q4_K
+ *    [7168, 2048, 256], down Q4_K or Q6_K [2048, 7168, 256]: the down type is
+ *    taken from the tensor, as repack_experts.c:140-155), the router
+ *    blk.L.ffn_gate_inp.weight [7168, 256] and blk.L.exp_probs_b.bias (or
+ *    .weight) [256] (F32, F16 or BF16, widened to fp32), and with
+ *    with_shared the shared expert blk.L.ffn_{gate,up,down}_shexp.weight
+ *    packed as one more blob (its down type must match the routed one).
+ *  - from a packed layer file (repack_experts.c's layer_NN.bin, 256 blobs;
+ *    the expert size and down type from the file size, infer.m:1806-1821),
+ *    with the router, bias and shared expert from the GGUF.
+ * Synchronous.  *down_is_q6 (optional) receives the layer's down type. */
+int fdm_layer_load_gguf(int L, const fdm_gguf *m, int with_shared, int *down_is_q6);
+int fdm_layer_load_packed(int L, const char *layer_file, const fdm_gguf *m, int with_shared,
+                          int *down_is_q6);
 
 /* ---- MoE forward with routing given: replaces metal_moe_forward
  * (infer.m:1604-1700).  moe_out = sum_k w[k] * E_{idx[k]}(h_post), summed in
