@@ -70,9 +70,11 @@ constexpr int kLayerMaxSlots = 17;               // FDM_MAX_K routed + 1 shared
 constexpr int kLayerCounters = 1;                // arrivals of the digit items
 constexpr int kLayerFlags = 4;                   // digits ready, -, error, -
 constexpr int kLayerFlagErr = 2;                 // flag slot of the timed-out epoch
+constexpr int kLayerMaxParts = 8;               // down matrices split in <= 8 column parts
 // tagged words: scores 256, prov 16, route_w 16, route_perm 16,
-// act 17 x 2048, eo 17 x 7168
-constexpr size_t kLayerTagged = 256 + 3 * 16 + (size_t)kLayerMaxSlots * (2048 + 7168);
+// act 17 x 2048, eo 17 x 8 x 7168 (per-part down outputs)
+constexpr size_t kLayerTagged =
+    256 + 3 * 16 + (size_t)kLayerMaxSlots * (2048 + (size_t)kLayerMaxParts * 7168);
 struct LayerArgs {
   const float* Wg;         // router weights [256][7168] fp32
   const float* bias;       // [256] or null
@@ -95,7 +97,7 @@ struct LayerArgs {
   uint64_t* route_w;       // tagged: weights in the reference's slot order [K]
   uint64_t* route_perm;    // tagged: slot running the k-th expert of that order [K]
   uint64_t* act;           // tagged: [kLayerMaxSlots][2048]
-  uint64_t* eo;            // tagged: [kLayerMaxSlots][7168]
+  uint64_t* eo;            // tagged: [kLayerMaxSlots][kLayerMaxParts][7168] down partial sums
   int* counters;           // kLayerCounters x kLayerStride ints, zero at first use
   unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
   unsigned epoch;          // non-zero, different from every earlier call's

@@ -14,18 +14,20 @@
 //   digits of h_post (28: four 64-element groups each)
 //   router row e (256)
 //   route: the expert set (1);  the exact route() (1)
-//   shared expert gate/up runs, shared expert down runs
-//   routed gate/up runs, slot-major
-//   routed down runs, slot-major
-// (a run is kGuPer / kDnPer consecutive row tiles of one slot)
+//   shared expert: gate/up items of every column part, then its down parts
+//   routed experts, part-major: gate/up items of part q of every slot,
+//     then the down items of part q - lag of every slot, q = 0, 1, ...
 //   combine tiles (224)
 //
-// (Interleaving each slot's down tiles right behind its gate/up tiles was
-// measured slower: down tiles dispatched early hold workgroup slots while
-// they wait for activations, starving the remaining gate/up tiles.  The
-// shared expert's gate/up tiles likewise wait for the digits before they
-// load, so their weights do not compete with the router rows, which are on
-// the route's critical path.)
+// Every down matrix is split into column parts (2 by default): down part p
+// of a slot needs only the slot's activations of part p, so the downs of
+// part 0 stream alongside the gate/up items of part 1 instead of waiting
+// for the slot's last activation.  The combine sums a slot's parts in part
+// order.  (Measured on MI355X: 2 parts beat 1, 4 and 8; finer parts read
+// 144-byte row slices that share 64-byte sectors with the neighbour part.)
+// (The shared expert's gate/up items wait for the digits before they load,
+// so their weights do not compete with the router rows, which are on the
+// route's critical path.)
 //
 // Items only wait for items earlier in the list, and a waiting item has
 // already issued every weight load it can (down tiles load their weights
@@ -57,13 +59,38 @@ constexpr int kStride = kLayerStride;        // ints between counters / flags (2
 constexpr int kRows = 256;                   // router rows (R1 experts)
 constexpr int kXdItems = kHidden / 64 / 4;   // 28 digit items of 4 groups
 constexpr int kGuTileRows = 8;               // gate (and up) rows per gate/up tile
-constexpr int kGuTileCount = kFfn / kGuTileRows;      // 256
-// down tile: 16 rows per pass of the four waves; two passes for Q4_K rows
-// (1152 B), one for the larger Q6_K rows (1680 B, more registers per row)
-__host__ __device__ constexpr int dn_passes(bool q6) { return q6 ? 1 : 2; }
-__host__ __device__ constexpr int dn_tiles(bool q6) { return kHidden / (16 * dn_passes(q6)); }
-constexpr int kGuPer = 2;                    // gate/up tiles per work item
-constexpr int kDnPer = 2;                    // down tiles per work item
+#ifndef FDM_LAYER_PARTS
+#define FDM_LAYER_PARTS 2  // measured on MI355X: 2 parts, lag 1, one tile per item
+#endif
+#ifndef FDM_LAYER_LAG
+#define FDM_LAYER_LAG 1
+#endif
+#ifndef FDM_LAYER_GUPER
+#define FDM_LAYER_GUPER 1
+#endif
+// Column parts of every down matrix: part p of slot s needs only the slot's
+// activations kPartCols p .. kPartCols (p + 1) - 1, so it runs while gate/up
+// of the slot's later rows is still streaming.
+constexpr int kParts = FDM_LAYER_PARTS;
+static_assert(kParts == 1 || kParts == 2 || kParts == 4 || kParts == 8, "parts: 1, 2, 4 or 8");
+static_assert(kParts <= kLayerMaxParts, "tagged eo holds kLayerMaxParts parts");
+constexpr int kLag = FDM_LAYER_LAG;          // down parts follow gate/up parts this many parts later
+static_assert(kLag >= 0 && kLag <= kParts, "lag: 0 .. parts");
+constexpr int kGuPer = FDM_LAYER_GUPER;      // gate/up tiles per work item
+constexpr int kPartCols = kFfn / kParts;     // activations per part
+constexpr int kPartGroups = kPartCols / 64;  // digit records per part
+constexpr int kGuPerPart = kPartCols / kGuTileRows / kGuPer;  // gate/up items per (slot, part)
+static_assert(kGuPerPart * kGuTileRows * kGuPer == kPartCols, "gate/up items tile a part");
+// Q4_K down item: one lane per 64-element group of a row's part, kDnRowsQ4L
+// rows per lane.  Q6_K down item: one lane per 128-element half block.
+constexpr int kDnLanesQ4 = kPartGroups;                     // lanes per row
+constexpr int kDnRowsQ4L = 7;                               // rows per lane
+constexpr int kDnRowsQ4 = 4 * kDnRowsQ4L * (64 / kDnLanesQ4);  // rows per item (448)
+constexpr int kDnLanesQ6 = kPartCols / 128;
+constexpr int kDnRowsQ6L = 2;
+constexpr int kDnRowsQ6 = 4 * kDnRowsQ6L * (64 / kDnLanesQ6);  // 256
+static_assert(kHidden % kDnRowsQ4 == 0 && kHidden % kDnRowsQ6 == 0, "down items tile the rows");
+__host__ __device__ constexpr int dn_per_part(bool q6) { return kHidden / (q6 ? kDnRowsQ6 : kDnRowsQ4); }
 constexpr int kCombRows = 32;                // rows per combine tile
 constexpr int kCombTiles = kHidden / kCombRows;       // 224
 constexpr unsigned kSpinLimit = 1u << 17;    // polls of one wait (each >= ~1 us)
@@ -95,7 +122,10 @@ __device__ __forceinline__ float tagged_f(uint64_t v) { return __uint_as_float((
 __device__ __forceinline__ int tagged_i(uint64_t v) { return (int)(uint32_t)v; }
 
 struct LayerSmem {
-  XGroup xs[kHidden / 64];  // digits of h_post (gate/up) or of one slot's activations (down)
+  union {
+    XGroup xs[kHidden / 64];  // digits of h_post (gate/up) or of a part's activations (down)
+    float part[kLayerMaxSlots][kParts][kCombRows];  // combine: per-part down outputs
+  };
   float red[4];
   int eid;                  // expert of the item's slot
 };
@@ -203,19 +233,20 @@ __device__ __forceinline__ void router_row(const LayerArgs& a, int e, LayerSmem&
   const int t = 64 * wave + lane;
   const float4* w4 = reinterpret_cast<const float4*>(a.Wg + (size_t)e * kHidden);
   const float4* x4 = reinterpret_cast<const float4*>(a.h);
-  float4 wv[kHidden / 1024], xv[kHidden / 1024];
+  u32x4 wv[kHidden / 1024];
+  float4 xv[kHidden / 1024];
 #pragma unroll
   for (int i = 0; i < kHidden / 1024; ++i) {
-    wv[i] = w4[t + 256 * i];
+    wv[i] = *reinterpret_cast<const u32x4*>(w4 + t + 256 * i);
     xv[i] = x4[t + 256 * i];
   }
   float acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < kHidden / 1024; ++i) {
-    acc = fmaf(wv[i].x, xv[i].x, acc);
-    acc = fmaf(wv[i].y, xv[i].y, acc);
-    acc = fmaf(wv[i].z, xv[i].z, acc);
-    acc = fmaf(wv[i].w, xv[i].w, acc);
+    acc = fmaf(__uint_as_float(wv[i].x), xv[i].x, acc);
+    acc = fmaf(__uint_as_float(wv[i].y), xv[i].y, acc);
+    acc = fmaf(__uint_as_float(wv[i].z), xv[i].z, acc);
+    acc = fmaf(__uint_as_float(wv[i].w), xv[i].w, acc);
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
@@ -255,8 +286,11 @@ __device__ __forceinline__ void route_item(const LayerArgs& a) {
   float sc[4];
   wait_scores(a, sc);
   if (threadIdx.x >= 64) return;
-  const int id = route_set_lane(sc, bj, a.K);
-  if (lane < a.K) put_tagged(a.prov + lane, a.epoch, (uint32_t)id);
+  // each slot goes out as soon as it is certain: the first after two
+  // extractions, so slot 0's weights stream while the set is completed
+  route_set_publish(sc, bj, a.K, [&](int slot, int id) {
+    if (lane == 0) put_tagged(a.prov + slot, a.epoch, (uint32_t)id);
+  });
 }
 
 // ---- the exact route() ----------------------------------------------------------------
@@ -334,28 +368,30 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
   }
 }
 
-// ---- down run: kDnPer consecutive tiles of 16 * P rows of one slot's down matrix ----
-// Wave w owns rows 4P w .. 4P w + 4P-1 of each tile as row groups of 16
-// lanes (row 4P w + 4j + lane/16 in pass j).  The first tile's weights are
-// loaded before the slot's 2048 tagged activations (8 per thread) are
-// waited for and turned into digits in LDS, once per run; the row outputs
-// go out tagged.
+// ---- down item: rows of one column part of one slot's down matrix --------------------
+// Part p covers columns kPartCols p .. kPartCols (p+1) - 1.  The weights are
+// loaded before the part's tagged activations (one per thread at 8 parts)
+// are waited for and turned into digits in LDS; each row's partial sum goes
+// out tagged into eo[slot][p][row].
+//  Q4_K: kDnLanesQ4 lanes per row (one 64-element group each), lane row
+//        group rr = lane / kDnLanesQ4, rows rr + 16 j (j < 7) at 8 parts.
+//  Q6_K: kDnLanesQ6 lanes per row (one 128-element half block each).
 template <bool Q6>
-__device__ __forceinline__ void down_run(const LayerArgs& a, int slot, int tile0, bool routed,
-                                         LayerSmem& sm) {
-  constexpr int kDnPasses = dn_passes(Q6);
+__device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part, int item,
+                                          bool routed, LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l16 = lane & 15;
   if (routed) wait_route_xd(a, slot, true, false, sm);
   const uint8_t* blob = routed ? expert_blob(a, sm.eid) : a.shared;
   const uint8_t* dbase = blob ? blob + 2 * (size_t)kGateBytes : nullptr;
-  const uint64_t* act = a.act + (size_t)slot * kFfn;
+  const uint64_t* act = a.act + (size_t)slot * kFfn + part * kPartCols;
+  uint64_t* eo = a.eo + ((size_t)slot * kLayerMaxParts + part) * kHidden;
   auto stage_act = [&] {
-    float v[kFfn / 256];
+    constexpr int kPer = kPartCols / 256;
+    float v[kPer];
     poll_all(a, [&] {
       bool ok = true;
 #pragma unroll
-      for (int i = 0; i < kFfn / 256; ++i) {
+      for (int i = 0; i < kPer; ++i) {
         const uint64_t t = get_tagged(act + threadIdx.x + 256 * i);
         ok = ok && tag_is(t, a.epoch);
         v[i] = tagged_f(t);
@@ -364,75 +400,89 @@ __device__ __forceinline__ void down_run(const LayerArgs& a, int slot, int tile0
     });
     // element 256 i + 64 w + lane lives in wave w's lanes: record 4 i + w
 #pragma unroll
-    for (int i = 0; i < kFfn / 256; ++i) digits_to_lds(v[i], sm.xs[4 * i + wave]);
+    for (int i = 0; i < kPer; ++i) digits_to_lds(v[i], sm.xs[4 * i + wave]);
     __syncthreads();
   };
-  for (int t = 0; t < kDnPer; ++t) {
-    const int row0 = (tile0 + t) * 16 * kDnPasses + wave * 4 * kDnPasses + (lane >> 4);  // + 4j
-    float acc[kDnPasses] = {};
-    if (!Q6) {
-      Q4KGroupLoad ld[kDnPasses][2];
-      if (blob) {
+  if (!Q6) {
+    constexpr int LR = kDnLanesQ4, RPW = 64 / LR;
+    const int gl = lane % LR;  // group of the row's part
+    const int row0 = item * kDnRowsQ4 + wave * (kDnRowsQ4L * RPW) + lane / LR;  // + RPW j
+    const int boff = (part * kPartGroups + gl) / 4 * kQ4KBlock;
+    Q4KGroupLoad ld[kDnRowsQ4L];
+    if (blob) {
 #pragma unroll
-        for (int j = 0; j < kDnPasses; ++j) {
-          const uint8_t* rowp = dbase + (size_t)(row0 + 4 * j) * kQ4KRowFfn;
+      for (int j = 0; j < kDnRowsQ4L; ++j)
+        ld[j] = q4k_load_group(dbase + (size_t)(row0 + RPW * j) * kQ4KRowFfn + boff, gl & 3);
+    }
+    stage_act();
+    float acc[kDnRowsQ4L] = {};
+    if (blob) {
+      const Q4KScaleSel sel = q4k_scale_sel(gl & 3);
 #pragma unroll
-          for (int i = 0; i < 2; ++i)
-            ld[j][i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
-        }
-      }
-      if (t == 0) stage_act();
-      if (blob) {
-        const Q4KScaleSel sel = q4k_scale_sel(l16 & 3);
-#pragma unroll
-        for (int j = 0; j < kDnPasses; ++j)
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            acc[j] += q4k_group_dot_ld(ld[j][i], sel, &sm.xs[16 * i + l16]);
-            __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
-          }
-      }
-    } else {
-      // 16 halves of 128 elements per 2048-column row: one per lane
-      Q6KHalfLoad l6[kDnPasses];
-      if (blob) {
-#pragma unroll
-        for (int j = 0; j < kDnPasses; ++j)
-          l6[j] = q6k_load_half(dbase + (size_t)(row0 + 4 * j) * kQ6KRowFfn + (l16 >> 1) * kQ6KBlock,
-                                l16 & 1);
-      }
-      if (t == 0) stage_act();
-      if (blob) {
-#pragma unroll
-        for (int j = 0; j < kDnPasses; ++j) {
-          acc[j] = q6k_half_dot_ld(l6[j], &sm.xs[2 * l16]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+      for (int j = 0; j < kDnRowsQ4L; ++j) {
+        acc[j] = q4k_group_dot_ld(ld[j], sel, &sm.xs[gl]);
+        __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
       }
     }
 #pragma unroll
-    for (int j = 0; j < kDnPasses; ++j) {
-      const float sres = sum16(acc[j]);
-      if (l16 == 0)
-        put_tagged(a.eo + (size_t)slot * kHidden + row0 + 4 * j, a.epoch, __float_as_uint(sres));
+    for (int j = 0; j < kDnRowsQ4L; ++j) {
+      float v = acc[j];
+#pragma unroll
+      for (int m = LR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+      if (gl == 0) put_tagged(eo + row0 + RPW * j, a.epoch, __float_as_uint(v));
     }
-
-    // the next tile's loads are issued here, not hoisted above this tile's
-    // staging and math (they would hold a second tile of registers)
-    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    constexpr int LR = kDnLanesQ6, RPW = 64 / LR;
+    const int gl = lane % LR;  // half block of the row's part
+    const int row0 = item * kDnRowsQ6 + wave * (kDnRowsQ6L * RPW) + lane / LR;
+    const int H = part * kDnLanesQ6 + gl;  // half block of the row
+    Q6KHalfLoad l6[kDnRowsQ6L];
+    if (blob) {
+#pragma unroll
+      for (int j = 0; j < kDnRowsQ6L; ++j)
+        l6[j] = q6k_load_half(dbase + (size_t)(row0 + RPW * j) * kQ6KRowFfn + (H >> 1) * kQ6KBlock,
+                              H & 1);
+    }
+    stage_act();
+    float acc[kDnRowsQ6L] = {};
+    if (blob) {
+#pragma unroll
+      for (int j = 0; j < kDnRowsQ6L; ++j) {
+        acc[j] = q6k_half_dot_ld(l6[j], &sm.xs[2 * gl]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kDnRowsQ6L; ++j) {
+      float v = acc[j];
+#pragma unroll
+      for (int m = LR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+      if (gl == 0) put_tagged(eo + row0 + RPW * j, a.epoch, __float_as_uint(v));
+    }
   }
 }
 
 // ---- combine tile: rows 32*tile .. 32*tile+31 ------------------------------------------
-// Waits for every slot's output of its rows and for the exact route, then
-// sums the routed experts in the reference's slot order and adds the shared
-// expert and the residual.
-__device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile) {
-  const int r = tile * kCombRows + threadIdx.x;
+// Thread (part p = t / 32, row r = t % 32) waits for every slot's part-p
+// output of its row; the parts of a slot are summed p = 0, 1, ... in LDS;
+// then the routed experts are summed in the reference's slot order and the
+// shared expert and the residual added.
+__device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile, LayerSmem& sm) {
+  const int rr = threadIdx.x & (kCombRows - 1), p = threadIdx.x / kCombRows;
+  const int r = tile * kCombRows + rr;
+  const bool mine = p < kParts;
+  float v[kLayerMaxSlots];
   poll_all(a, [&] {
-    if (threadIdx.x >= kCombRows) return true;
+    if (!mine) return true;
     bool ok = true;
-    for (int s = 0; s < a.n_slots; ++s) ok = ok && tag_is(get_tagged(a.eo + (size_t)s * kHidden + r), a.epoch);
+#pragma unroll
+    for (int s = 0; s < kLayerMaxSlots; ++s) {
+      if (s < a.n_slots) {
+        const uint64_t t = get_tagged(a.eo + ((size_t)s * kLayerMaxParts + p) * kHidden + r);
+        ok = ok && tag_is(t, a.epoch);
+        v[s] = tagged_f(t);
+      }
+    }
     return ok;
   });
   // the exact route is finished long before the last expert output
@@ -441,40 +491,86 @@ __device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile) {
     return tag_is(get_tagged(a.route_w + threadIdx.x), a.epoch) &&
            tag_is(get_tagged(a.route_perm + threadIdx.x), a.epoch);
   });
+  if (mine) {
+#pragma unroll
+    for (int s = 0; s < kLayerMaxSlots; ++s)
+      if (s < a.n_slots) sm.part[s][p][rr] = v[s];
+  }
+  __syncthreads();
   if (threadIdx.x >= kCombRows) return;
+  auto expert_out = [&](int s) {
+    float e = sm.part[s][0][rr];
+#pragma unroll
+    for (int q = 1; q < kParts; ++q) e += sm.part[s][q][rr];
+    return e;
+  };
   float moe = 0.0f;
   for (int k = 0; k < a.K; ++k) {
     const int sl = tagged_i(get_tagged(a.route_perm + k));
-    moe = fmaf(tagged_f(get_tagged(a.route_w + k)), tagged_f(get_tagged(a.eo + (size_t)sl * kHidden + r)),
-               moe);
+    moe = fmaf(tagged_f(get_tagged(a.route_w + k)), expert_out(sl), moe);
   }
-  const float sd = a.n_slots > a.K ? tagged_f(get_tagged(a.eo + (size_t)a.K * kHidden + r)) : 0.0f;
+  const float sd = a.n_slots > a.K ? expert_out(a.K) : 0.0f;
   const float hin = a.h_in ? a.h_in[r] : 0.0f;
   a.out[r] = (hin + moe) + sd;
   if (a.moe_out) a.moe_out[r] = moe;
 }
 
-// First workgroup of each section of the work list.
+// First workgroup of each section of the work list:
+//   digits | router rows | route set | exact route
+//   | shared expert: gate/up of parts 0..P-1, then down of parts 0..P-1
+//   | routed experts, part-major: step q holds gate/up of part q of every
+//     slot (q < P), then down of part q - lag of every slot (q >= lag)
+//   | combine tiles
 struct LayerList {
-  int router, route, exact, sgu, sdn, gu, dn, comb, total;
-  int gu_items, dn_items;  // work items per slot
+  int route, exact, router, xd, shared, routed, comb, total;
+  int gup, dnp;  // gate/up and down items per (slot, part)
 };
 
 __host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6) {
   const int hs = n_slots - K;  // 1 with a shared expert
   LayerList l;
-  l.gu_items = kGuTileCount / kGuPer;
-  l.dn_items = dn_tiles(q6) / kDnPer;
+  l.gup = kGuPerPart;
+  l.dnp = dn_per_part(q6);
+  l.xd = 0;
   l.router = kXdItems;
   l.route = l.router + kRows;
   l.exact = l.route + 1;
-  l.sgu = l.exact + 1;
-  l.sdn = l.sgu + hs * l.gu_items;
-  l.gu = l.sdn + hs * l.dn_items;
-  l.dn = l.gu + K * l.gu_items;
-  l.comb = l.dn + K * l.dn_items;
+  l.shared = l.exact + 1;
+  l.routed = l.shared + hs * kParts * (l.gup + l.dnp);
+  l.comb = l.routed + K * kParts * (l.gup + l.dnp);
   l.total = l.comb + kCombTiles;
   return l;
+}
+
+// Routed item `off` (0-based within the routed section): gate/up (dn = false,
+// idx = gate/up item) or down (dn = true, idx = down item) of (slot, part).
+__device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, bool& dn, int& slot,
+                                            int& part, int& idx) {
+  const int G = K * l.gup, D = K * l.dnp;
+  int q, r;
+  if (off < kLag * G) {
+    q = off / G;
+    r = off % G;
+  } else if (off < kLag * G + (kParts - kLag) * (G + D)) {
+    const int o = off - kLag * G;
+    q = kLag + o / (G + D);
+    r = o % (G + D);
+  } else {
+    const int o = off - kLag * G - (kParts - kLag) * (G + D);
+    q = kParts + o / D;
+    r = G + o % D;  // a step past the last gate/up part holds down items only
+  }
+  dn = r >= G && q >= kLag;
+  if (q >= kParts) dn = true;
+  if (!dn) {
+    part = q;
+    slot = r / l.gup;
+    idx = r % l.gup;
+  } else {
+    part = q - kLag;
+    slot = (r - G) / l.dnp;
+    idx = (r - G) % l.dnp;
+  }
 }
 
 }  // namespace
@@ -484,23 +580,29 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
   const LayerList l = layer_list(a.K, a.n_slots, Q6);
   const int it = blockIdx.x;
   if (it < l.router) {
-    xd_item(a, it);
+    xd_item(a, it - l.xd);
   } else if (it < l.route) {
     router_row(a, it - l.router, sm);
   } else if (it == l.route) {
     route_item(a);
   } else if (it == l.exact) {
     exact_item(a);
-  } else if (it < l.sdn) {
-    gateup_run(a, a.K, (it - l.sgu) * kGuPer, false, sm);
-  } else if (it < l.gu) {
-    down_run<Q6>(a, a.K, (it - l.sdn) * kDnPer, false, sm);
-  } else if (it < l.dn) {
-    gateup_run(a, (it - l.gu) / l.gu_items, (it - l.gu) % l.gu_items * kGuPer, true, sm);
+  } else if (it < l.routed) {
+    const int off = it - l.shared;
+    if (off < kParts * l.gup)
+      gateup_run(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, false, sm);
+    else
+      down_part<Q6>(a, a.K, (off - kParts * l.gup) / l.dnp, (off - kParts * l.gup) % l.dnp, false, sm);
   } else if (it < l.comb) {
-    down_run<Q6>(a, (it - l.dn) / l.dn_items, (it - l.dn) % l.dn_items * kDnPer, true, sm);
+    bool dn;
+    int slot, part, idx;
+    routed_item(l, a.K, it - l.routed, dn, slot, part, idx);
+    if (!dn)
+      gateup_run(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, true, sm);
+    else
+      down_part<Q6>(a, slot, part, idx, true, sm);
   } else {
-    combine_tile(a, it - l.comb);
+    combine_tile(a, it - l.comb, sm);
   }
 }
 

@@ -282,29 +282,99 @@ __device__ __forceinline__ bool topk_set(const int vk[4], int K, int& id_out) {
   return true;
 }
 
-// Critical-path routing for the batch-1 layer: group limit and the expert
-// set (topk_set) from the sigmoid scores; lane k (k < K) receives the k-th
-// expert of the set.  When the set is ambiguous (a tie at the K-th key, or
-// fewer than K candidates), the exact reference scan runs instead and the
-// lanes hold the reference slot order.
-__device__ __forceinline__ int route_set_lane(const float score[4], const float bj[4], int K) {
-#pragma clang fp contract(off)
-  int vk[4];
-  route_keys(score, bj, vk);
-  int id = 0;
-  const bool ok = topk_set(vk, K, id);
-  if (!ok) {
-    float wv;
-    slot_scan(vk, score, K, 2.5f, id, wv);
-  }
-  return id;
+// ---- the expert set, largest first, published slot by slot -------------------------------
+// Maximum of an int over the whole wave (uniform result).
+__device__ __forceinline__ int wave_max_i32(int v) {
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x111, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x112, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x114, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x118, 0xF, 0xF, false));
+  const int a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
+  const int c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
+  return max(max(a, b), max(c, d));
 }
 
-__device__ __forceinline__ void route_set_wave(const float score[4], const float bj[4], int K,
-                                      int* __restrict__ prov_idx) {
+// The set route() selects, found by repeated extraction of the largest
+// masked key (lowest expert id first among equal keys), K + 1 times.  The
+// reference's scan keeps the K largest keys; which of several EQUAL keys it
+// keeps depends on its slot order, so the extracted set is the reference's
+// set unless the K-th and (K+1)-th keys are equal (or fewer than K keys
+// exceed -1e30).  Slot s (s-th largest key) is certain as soon as a strictly
+// smaller key follows it, and is handed to publish(s, id) at that point:
+// the first slots go out after two extractions, long before the set is
+// complete.  In the ambiguous case the exact scan runs and the slots not
+// yet published receive the rest of the reference's (multi)set.
+template <typename Publish>
+__device__ __forceinline__ void route_set_publish(const float score[4], const float bj[4], int K,
+                                                  Publish&& publish) {
+#pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int id = route_set_lane(score, bj, K);
-  if (lane < K) prov_idx[lane] = id;
+  int vk[4];
+  route_keys(score, bj, vk);
+  const int floor = sort_key(-1e30f);
+  int key[4] = {vk[0], vk[1], vk[2], vk[3]};
+  int m = max(max(key[0], key[1]), max(key[2], key[3]));
+  int prev_key = INT_MAX;
+  int ext = 0;    // lane k: the k-th extracted expert
+  int n_pub = 0;  // slots 0 .. n_pub-1 published
+  bool ambiguous = false;
+  for (int k = 0; k <= K; ++k) {
+    const int wm = wave_max_i32(m);
+    if (wm <= floor) {
+      ambiguous = k < K;  // fewer than K candidates
+      break;
+    }
+    if (k == K) {
+      ambiguous = wm == prev_key;  // the K-th key is tied with the (K+1)-th
+      break;
+    }
+    // lowest expert id (64 j + lane) holding wm
+    int jj = 3, ll = 0;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {
+      const unsigned long long b = __ballot(key[j] == wm);
+      if (b) {
+        jj = j;
+        ll = __ffsll(b) - 1;
+      }
+    }
+    if (k > 0 && prev_key > wm) {
+      // every slot so far holds a key >= prev_key > wm: all certain
+      for (int s = n_pub; s < k; ++s) publish(s, __builtin_amdgcn_readlane(ext, s));
+      n_pub = k;
+    }
+    prev_key = wm;
+    if (lane == k) ext = 64 * jj + ll;
+    if (lane == ll) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) key[j] = j == jj ? INT_MIN : key[j];
+      m = max(max(key[0], key[1]), max(key[2], key[3]));
+    }
+  }
+  if (!ambiguous) {
+    for (int s = n_pub; s < K; ++s) publish(s, __builtin_amdgcn_readlane(ext, s));
+    return;
+  }
+  // Ambiguous: the exact scan gives the reference's slots (lane k: slot k's
+  // id; slots never filled hold expert 0, possibly several times).  The
+  // published experts are strictly above the K-th key, so each is in it;
+  // match each published slot to one exact slot and hand the unmatched
+  // exact slots to the remaining slots.
+  int eid;
+  float ew;
+  slot_scan(vk, score, K, 2.5f, eid, ew);
+  bool matched = lane >= K;
+  for (int s = 0; s < n_pub; ++s) {
+    const int pid = __builtin_amdgcn_readlane(ext, s);
+    const unsigned long long hit = __ballot(!matched && eid == pid);
+    if (hit && lane == __ffsll(hit) - 1) matched = true;
+  }
+  unsigned long long rest = __ballot(!matched);
+  for (int s = n_pub; s < K && rest; ++s) {
+    const int l = __ffsll(rest) - 1;
+    publish(s, __builtin_amdgcn_readlane(eid, l));
+    rest &= rest - 1;
+  }
 }
 
 // ---- the exact slot order without the sequential scan ---------------------------------------
