@@ -29,7 +29,7 @@ __all__ = [
     "init", "shutdown", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
     "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
-    "moe_forward_host", "moe_layer", "set_layer_kernel", "LAYER_AUTO", "LAYER_ITEMS", "LAYER_STREAM", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "moe_forward_host", "moe_layer", "set_layer_kernel", "LAYER_AUTO", "LAYER_ITEMS", "LAYER_STREAM", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -157,6 +157,20 @@ def set_layer_kernel(mode):
     currently ITEMS).  Returns the previous mode."""
     prev = ctypes.c_int(-1)
     call("fdm_set_layer_kernel", mode, ctypes.byref(prev))
+    return prev.value
+
+
+BATCH_AUTO, BATCH_DOT4, BATCH_MFMA = 0, 1, 2
+BATCH_MFMA_MIN_T = 96
+
+
+def set_batch_kernel(mode):
+    """Expert kernels behind moe_forward_batched: BATCH_DOT4 (per-token int8
+    digit dot products), BATCH_MFMA (grouped GEMMs on MFMA, bf16 hi/lo pairs)
+    or BATCH_AUTO (MFMA from BATCH_MFMA_MIN_T tokens).  Returns the previous
+    mode."""
+    prev = ctypes.c_int(-1)
+    call("fdm_set_batch_kernel", mode, ctypes.byref(prev))
     return prev.value
 
 

@@ -227,6 +227,19 @@ hipError_t launch_combine(const BatchArgs& b, hipStream_t s) {
   return hipGetLastError();
 }
 
+hipError_t launch_batched_down(const BatchArgs& b, bool down_q6, hipStream_t s) {
+  const int P = b.T * b.K;
+  const int rows = P + (b.shared ? b.T : 0);
+  const int max_items = (P < kExperts ? P : kExperts) + (b.shared ? 1 : 0);
+  const int gy = max_items < 16 ? max_items : 16;
+  if (hipError_t e = launch_xdigits(b.act, (size_t)rows * (kFfn / 64), b.act_xd, s)) return e;
+  if (down_q6)
+    hipLaunchKernelGGL(k_bdown<true>, dim3(kBDnTiles, gy), dim3(256), 0, s, b);
+  else
+    hipLaunchKernelGGL(k_bdown<false>, dim3(kBDnTiles, gy), dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
 hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s) {
   const int P = b.T * b.K;
   const int rows = P + (b.shared ? b.T : 0);

@@ -18,6 +18,7 @@ namespace fdm {
 
 int g_num_cus = 0;
 int g_layer_mode = FDM_LAYER_AUTO;
+int g_batch_mode = FDM_BATCH_AUTO;
 
 namespace {
 
@@ -1040,7 +1041,8 @@ int ensure_prefill(int T, size_t rows, hipStream_t s) {
     if (w.p_actb) (void)hipFree(w.p_actb);
     w.p_actb = nullptr;
     w.p_rows = 0;
-    FDM_HIP(hipMalloc(&w.p_actb, rows * FDM_MOE_FFN * sizeof(__bf16)));
+    // two planes: the bf16 pair (hi, lo) of batched decode; prefill uses one
+    FDM_HIP(hipMalloc(&w.p_actb, 2 * rows * FDM_MOE_FFN * sizeof(__bf16)));
     w.p_rows = rows;
   }
   return FDM_OK;
@@ -1106,12 +1108,14 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     p.shared = y->shared;
     p.xb = g.ws.p_xb;
     p.actb = g.ws.p_actb;
+    p.act_rows = g.ws.p_rows;
+    p.actf = nullptr;
     p.eo = g.ws.b_eo;
     p.seg_start = g.ws.b_seg;
     p.pair_tok = g.ws.b_pair_tok;
     p.distinct = g.ws.b_distinct;
     p.n_distinct = g.ws.b_ndistinct;
-    FDM_HIP(launch_prefill_experts(p, s));
+    FDM_HIP(launch_prefill_experts(p, false, s));
     FDM_HIP(launch_combine(b, s));
   }
   return FDM_OK;
@@ -1155,7 +1159,43 @@ int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T,
   b.pair_of = g.ws.b_pair_of;
   b.distinct = g.ws.b_distinct;
   b.n_distinct = d_n_distinct ? d_n_distinct : g.ws.b_ndistinct;
-  FDM_HIP(launch_batched_experts(b, y->down_q6, s));
+  const bool mfma = g_batch_mode == FDM_BATCH_MFMA ||
+                    (g_batch_mode == FDM_BATCH_AUTO && T >= FDM_BATCH_MFMA_MIN_T);
+  if (!mfma) {
+    FDM_HIP(launch_batched_experts(b, y->down_q6, s));
+    return FDM_OK;
+  }
+  // grouped MFMA GEMMs at pair precision (a Q6_K down runs on the dot4 kernel)
+  if (int rc = ensure_prefill(T, rows, s)) return rc;
+  FDM_HIP(launch_dispatch(b, s));
+  FDM_HIP(launch_bf16_pair(d_X, g.ws.p_xb, (size_t)T * FDM_HIDDEN, s));
+  PrefillArgs q;
+  q.T = T;
+  q.K = K;
+  q.experts = y->experts;
+  q.expert_size = y->expert_size;
+  q.shared = y->shared;
+  q.xb = g.ws.p_xb;
+  q.actb = g.ws.p_actb;
+  q.act_rows = g.ws.p_rows;
+  q.actf = y->down_q6 ? g.ws.b_act : nullptr;
+  q.eo = g.ws.b_eo;
+  q.seg_start = g.ws.b_seg;
+  q.pair_tok = g.ws.b_pair_tok;
+  q.distinct = g.ws.b_distinct;
+  q.n_distinct = b.n_distinct;
+  FDM_HIP(launch_prefill_experts(q, true, s));
+  if (y->down_q6) FDM_HIP(launch_batched_down(b, true, s));
+  FDM_HIP(launch_combine(b, s));
+  return FDM_OK;
+}
+
+int fdm_set_batch_kernel(int mode, int* prev) {
+  if (int rc = check_ready()) return rc;
+  if (mode != FDM_BATCH_AUTO && mode != FDM_BATCH_DOT4 && mode != FDM_BATCH_MFMA)
+    return fail(FDM_E_INVAL, "batch kernel mode %d", mode);
+  if (prev) *prev = g_batch_mode;
+  g_batch_mode = mode;
   return FDM_OK;
 }
 

@@ -132,6 +132,8 @@ struct BatchArgs {
   int* n_distinct;         // out: number of distinct experts (device int)
 };
 hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s);
+// The grouped down (digits of b.act, then the dot4 down kernel) on its own.
+hipError_t launch_batched_down(const BatchArgs& b, bool down_q6, hipStream_t s);
 // The dispatch and the combine of the batched path on their own (prefill).
 hipError_t launch_dispatch(const BatchArgs& b, hipStream_t s);
 hipError_t launch_combine(const BatchArgs& b, hipStream_t s);
@@ -150,14 +152,22 @@ struct PrefillArgs {
   size_t expert_size;
   const uint8_t* shared;
   const __bf16* xb;        // rms_norm output as bf16 pairs: hi [T][7168], lo [T][7168]
-  __bf16* actb;            // [rows][2048]
+  __bf16* actb;            // [rows][2048] (pair precision: hi plane, then lo plane at + act_rows)
+  size_t act_rows;         // rows of each actb plane
+  float* actf;             // pair precision only, optional: fp32 SwiGLU activations [rows][2048]
+                           // written instead of actb (a Q6_K down runs on the dot4 kernels)
   float* eo;               // [rows][7168]
   const int* seg_start;    // from the dispatch
   const int* pair_tok;
   const int* distinct;
   const int* n_distinct;
 };
-hipError_t launch_prefill_experts(const PrefillArgs& p, hipStream_t s);
+// pair = false: prefill precision (bf16 weights, 1e-2).  pair = true: batched
+// decode precision (bf16 hi/lo weights and activations, ~1e-5), Q4_K down;
+// with actf set only the gate/up GEMM runs.
+hipError_t launch_prefill_experts(const PrefillArgs& p, bool pair, hipStream_t s);
+// x [n] fp32 -> its bf16 pair: hi at xb[i], lo at xb[n + i]
+hipError_t launch_bf16_pair(const float* x, __bf16* xb, size_t n, hipStream_t s);
 
 // synth_kernels.hip
 hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);

@@ -16,6 +16,13 @@
 // x into output errors of up to a few 1e-2; the pair leaves ~2^-16.  The
 // weights and the SwiGLU activations are single bf16 (their rounding costs
 // ~1e-3).
+//
+// Batched decode runs the same GEMMs at pair precision: the dequantised
+// weight w enters as hi = bf16(w) and lo = bf16(w - hi) (16 significant
+// bits) and every activation as a bf16 pair, contracted as hi*hi + hi*lo +
+// lo*hi (three MFMAs per step; the lo*lo term is below 2^-16).  Outputs then
+// carry ~1e-5 relative error, inside decode's 1e-3 bar, and each expert's
+// weights are dequantised once per 32-token chunk instead of once per token.
 #include "fdm_internal.h"
 
 namespace fdm {
@@ -45,10 +52,15 @@ __device__ __forceinline__ Q4KLane q4k_lane_load(const uint8_t* blk, int j) {
   return r;
 }
 
-// The lane's 8 weights of sub-block S as bf16 (d*sc*q - dmin*m, rounded once
-// to bf16 after the fp32 dequant of quant.c:49-57).
-template <int S>
-__device__ __forceinline__ bf16x8 q4k_lane_bf16(const Q4KLane& r) {
+// The lane's 8 weights of sub-block S (d*sc*q - dmin*m in fp32 after the
+// dequant of quant.c:49-57) as bf16: hi = bf16(w) and, with PAIR, the
+// remainder lo = bf16(w - hi).
+struct W8 {
+  bf16x8 hi, lo;
+};
+
+template <int S, bool PAIR>
+__device__ __forceinline__ W8 q4k_lane_w(const Q4KLane& r) {
   const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
   // get_scale_min_k4(S) (quant.c:26-34) on the 12 scale bytes s0|s1|s2
   int sc, m;
@@ -77,7 +89,10 @@ __device__ __forceinline__ bf16x8 q4k_lane_bf16(const Q4KLane& r) {
   v[5] = d1 * (float)((hi >> 8) & 0xFF) - m1;
   v[6] = d1 * (float)((hi >> 16) & 0xFF) - m1;
   v[7] = d1 * (float)(hi >> 24) - m1;
-  return __builtin_convertvector(v, bf16x8);
+  W8 o;
+  o.hi = __builtin_convertvector(v, bf16x8);
+  if constexpr (PAIR) o.lo = __builtin_convertvector(v - __builtin_convertvector(o.hi, f32x8), bf16x8);
+  return o;
 }
 
 __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
@@ -195,6 +210,13 @@ __device__ __forceinline__ BDma<NB, NH, HT> bdma_init(const int* trow, int n_tok
   return d;
 }
 
+// One 16-byte direct global -> LDS load per lane.  (A plain function: the
+// host compilation pass rejects the builtin inside some template
+// instantiations, not inside a non-template body.)
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, lds_dst, 16, 0, 0);
+}
+
 template <int NB, int NH, int HT>
 __device__ __forceinline__ void bdma_issue(const BDma<NB, NH, HT>& d, const __bf16* src, __bf16* buf, int b) {
   const uint8_t* base = reinterpret_cast<const uint8_t*>(src) + (size_t)b * kPRowB;
@@ -203,8 +225,7 @@ __device__ __forceinline__ void bdma_issue(const BDma<NB, NH, HT>& d, const __bf
   for (int k = 0; k < BDma<NB, NH, HT>::kRounds; ++k) {
     const int rho0 = 2 * (wave + kPWaves * k);  // wave-uniform
     const int h = rho0 / (16 * NB), t0 = rho0 - h * 16 * NB;
-    __builtin_amdgcn_global_load_lds(base + d.src[k],
-                                     reinterpret_cast<uint8_t*>(buf) + (h * HT + t0) * kPRowB, 16, 0, 0);
+    lds_dma16(base + d.src[k], reinterpret_cast<uint8_t*>(buf) + (h * HT + t0) * kPRowB);
   }
 }
 
@@ -229,17 +250,21 @@ __device__ __forceinline__ bf16x8 lds_b(const __bf16* bs, int h, int nb, int c16
 // one buffer do not depend on the direct loads still landing in the other.
 constexpr int kPGuBuf = 2 * kPGuTokens * kQK;  // bf16 per gate/up B buffer
 
-template <int NB>
+template <int NB, bool PAIR>
 __device__ __forceinline__ void pgateup_block(const __bf16* cur, const Q4KLane& gl, const Q4KLane& ul,
                                               f32x4 (&ag)[NB], f32x4 (&au)[NB], int c16, int j) {
 #define FDM_PGU_STEP(S)                                                  \
   {                                                                      \
-    const bf16x8 ga = q4k_lane_bf16<S>(gl), ua = q4k_lane_bf16<S>(ul);   \
+    const W8 ga = q4k_lane_w<S, PAIR>(gl), ua = q4k_lane_w<S, PAIR>(ul); \
     _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                  \
       const bf16x8 bh = lds_b<kPGuTokens>(cur, 0, nb, c16, S, j);        \
       const bf16x8 bl = lds_b<kPGuTokens>(cur, 1, nb, c16, S, j);        \
-      ag[nb] = mfma16(ga, bl, mfma16(ga, bh, ag[nb]));                   \
-      au[nb] = mfma16(ua, bl, mfma16(ua, bh, au[nb]));                   \
+      ag[nb] = mfma16(ga.hi, bl, mfma16(ga.hi, bh, ag[nb]));             \
+      au[nb] = mfma16(ua.hi, bl, mfma16(ua.hi, bh, au[nb]));             \
+      if constexpr (PAIR) {                                              \
+        ag[nb] = mfma16(ga.lo, bh, ag[nb]);                              \
+        au[nb] = mfma16(ua.lo, bh, au[nb]);                              \
+      }                                                                  \
     }                                                                    \
   }                                                                      \
   __builtin_amdgcn_sched_barrier(0);
@@ -248,7 +273,7 @@ __device__ __forceinline__ void pgateup_block(const __bf16* cur, const Q4KLane& 
 #undef FDM_PGU_STEP
 }
 
-template <int NB>
+template <int NB, bool PAIR>
 __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem& it, __bf16* bs0, __bf16* bs1,
                                               const int* trow, int t0, int n_tok) {
   constexpr int kBlocks = kHidden / kQK;  // 28, even
@@ -278,7 +303,7 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
     bdma_issue(dma, p.xb, bs1, b + 1);
     gn = q4k_lane_load(gbase + (roff + (b + 1) * kQ4KBlock), j);
     un = q4k_lane_load(ubase + (roff + (b + 1) * kQ4KBlock), j);
-    pgateup_block<NB>(bs0, gl, ul, ag, au, c16, j);
+    pgateup_block<NB, PAIR>(bs0, gl, ul, ag, au, c16, j);
     gl = gn;
     ul = un;
     const int b2 = min(b + 2, kBlocks - 1);
@@ -287,7 +312,7 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
     bdma_issue(dma, p.xb, bs0, b2);
     gn = q4k_lane_load(gbase + (roff + b2 * kQ4KBlock), j);
     un = q4k_lane_load(ubase + (roff + b2 * kQ4KBlock), j);
-    pgateup_block<NB>(bs1, gl, ul, ag, au, c16, j);
+    pgateup_block<NB, PAIR>(bs1, gl, ul, ag, au, c16, j);
   }
   wait_vm();  // the re-staged copy has landed before the buffers are reused
   // C of a 16x16 block: lane (c16, j) holds token column c16, rows 4 j .. 4 j + 3.
@@ -297,18 +322,24 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
     const int t = nb * 16 + c16;
     if (t >= n_tok) continue;
     const int orow = it.shared ? P + it.first + t0 + t : it.first + t0 + t;
-    bf16x4 o;
+    const size_t off = (size_t)orow * kFfn + blockIdx.x * kPM + wave * 16 + 4 * j;
+    f32x4 a;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = (__bf16)silu_mul(ag[nb][i], au[nb][i]);
-    *reinterpret_cast<bf16x4*>(p.actb + (size_t)orow * kFfn + blockIdx.x * kPM + wave * 16 + 4 * j) = o;
+    for (int i = 0; i < 4; ++i) a[i] = silu_mul(ag[nb][i], au[nb][i]);
+    if (PAIR && p.actf) {
+      *reinterpret_cast<f32x4*>(p.actf + off) = a;
+      continue;
+    }
+    const bf16x4 hi = __builtin_convertvector(a, bf16x4);
+    *reinterpret_cast<bf16x4*>(p.actb + off) = hi;
+    if (PAIR)
+      *reinterpret_cast<bf16x4*>(p.actb + p.act_rows * kFfn + off) =
+          __builtin_convertvector(a - __builtin_convertvector(hi, f32x4), bf16x4);
   }
 }
 
-__global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pgateup(
-    PrefillArgs p) {
-  __shared__ __attribute__((aligned(16))) __bf16 bs0[kPGuBuf];
-  __shared__ __attribute__((aligned(16))) __bf16 bs1[kPGuBuf];
-  __shared__ int trow[kPGuTokens];
+template <bool PAIR>
+__device__ __forceinline__ void pgateup_body(const PrefillArgs& p, __bf16* bs0, __bf16* bs1, int* trow) {
   PItem it;
   if (!prefill_item(p, blockIdx.y, it)) return;
   for (int t0 = 0; t0 < it.count; t0 += kPGuTokens) {
@@ -318,26 +349,36 @@ __global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4)
       trow[threadIdx.x] = it.shared ? it.first + t0 + threadIdx.x : p.pair_tok[it.first + t0 + threadIdx.x];
     __syncthreads();
     if (n_tok > 16)
-      pgateup_chunk<2>(p, it, bs0, bs1, trow, t0, n_tok);
+      pgateup_chunk<2, PAIR>(p, it, bs0, bs1, trow, t0, n_tok);
     else
-      pgateup_chunk<1>(p, it, bs0, bs1, trow, t0, n_tok);
+      pgateup_chunk<1, PAIR>(p, it, bs0, bs1, trow, t0, n_tok);
   }
 }
 
 // ---- grouped down GEMM ----------------------------------------------------------------------
 // Item rows: down rows kPM tile .. +kPM-1 against the item's bf16
-// activation rows (contiguous); fp32 outputs.  Two B buffers of kPTokens
-// rows, as the gate/up GEMM.
-constexpr int kPDnBuf = kPTokens * kQK;  // bf16 per down B buffer
+// activation rows (contiguous; at pair precision hi and lo planes); fp32
+// outputs.  Two B buffers of kPDnTok<PAIR> token rows per plane (the same
+// LDS either way), as the gate/up GEMM.
+template <bool PAIR>
+constexpr int kPDnTok = PAIR ? kPTokens / 2 : kPTokens;  // tokens per down chunk
+constexpr int kPDnBuf = kPTokens * kQK;                   // bf16 per down B buffer (both precisions)
 
-template <int NB>
+template <int NB, bool PAIR>
 __device__ __forceinline__ void pdown_block(const __bf16* cur, const Q4KLane& dl, f32x4 (&acc)[NB], int c16,
                                             int j) {
+  constexpr int HT = kPDnTok<PAIR>;
 #define FDM_PDN_STEP(S)                                                                  \
   {                                                                                      \
-    const bf16x8 da = q4k_lane_bf16<S>(dl);                                              \
-    _Pragma("unroll") for (int nb = 0; nb < NB; ++nb)                                    \
-      acc[nb] = mfma16(da, lds_b<kPTokens>(cur, 0, nb, c16, S, j), acc[nb]);             \
+    const W8 da = q4k_lane_w<S, PAIR>(dl);                                               \
+    _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                  \
+      const bf16x8 bh = lds_b<HT>(cur, 0, nb, c16, S, j);                                \
+      acc[nb] = mfma16(da.hi, bh, acc[nb]);                                              \
+      if constexpr (PAIR) {                                                              \
+        acc[nb] = mfma16(da.hi, lds_b<HT>(cur, 1, nb, c16, S, j), acc[nb]);              \
+        acc[nb] = mfma16(da.lo, bh, acc[nb]);                                            \
+      }                                                                                  \
+    }                                                                                    \
   }                                                                                      \
   __builtin_amdgcn_sched_barrier(0);
   FDM_PDN_STEP(0) FDM_PDN_STEP(1) FDM_PDN_STEP(2) FDM_PDN_STEP(3)
@@ -345,15 +386,17 @@ __device__ __forceinline__ void pdown_block(const __bf16* cur, const Q4KLane& dl
 #undef FDM_PDN_STEP
 }
 
-template <int NB>
+template <int NB, bool PAIR>
 __device__ __forceinline__ void pdown_chunk(const PrefillArgs& p, const PItem& it, __bf16* bs0, __bf16* bs1,
                                             const int* trow, int row0, int n_tok) {
   constexpr int kBlocks = kFfn / kQK;  // 8, even
+  constexpr int NH = PAIR ? 2 : 1, HT = kPDnTok<PAIR>;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane >> 4, c16 = lane & 15;
   const uint32_t roff = (uint32_t)(blockIdx.x * kPM + wave * 16 + c16) * kQ4KRowFfn;
   const uint8_t* dbase = it.blob + 2 * (size_t)kGateBytes;
-  const BDma<NB, 1, kPTokens> dma = bdma_init<NB, 1, kPTokens>(trow, n_tok, kFfn * 2, 0);
+  const BDma<NB, NH, HT> dma =
+      bdma_init<NB, NH, HT>(trow, n_tok, kFfn * 2, PAIR ? (uint32_t)(p.act_rows * kFfn * 2) : 0u);
   f32x4 acc[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -366,14 +409,14 @@ __device__ __forceinline__ void pdown_chunk(const PrefillArgs& p, const PItem& i
     __syncthreads();
     bdma_issue(dma, p.actb, bs1, b + 1);
     dn = q4k_lane_load(dbase + (roff + (b + 1) * kQ4KBlock), j);
-    pdown_block<NB>(bs0, dl, acc, c16, j);
+    pdown_block<NB, PAIR>(bs0, dl, acc, c16, j);
     dl = dn;
     const int b2 = min(b + 2, kBlocks - 1);
     wait_vm();
     __syncthreads();
     bdma_issue(dma, p.actb, bs0, b2);
     dn = q4k_lane_load(dbase + (roff + b2 * kQ4KBlock), j);
-    pdown_block<NB>(bs1, dl, acc, c16, j);
+    pdown_block<NB, PAIR>(bs1, dl, acc, c16, j);
   }
   wait_vm();
 #pragma unroll
@@ -385,27 +428,65 @@ __device__ __forceinline__ void pdown_chunk(const PrefillArgs& p, const PItem& i
   }
 }
 
+template <bool PAIR>
+__device__ __forceinline__ void pdown_body(const PrefillArgs& p, __bf16* bs0, __bf16* bs1, int* trow) {
+  constexpr int CT = kPDnTok<PAIR>;
+  PItem it;
+  if (!prefill_item(p, blockIdx.y, it)) return;
+  const int P = p.T * p.K;
+  const int base = it.shared ? P + it.first : it.first;  // first activation row
+  for (int t0 = 0; t0 < it.count; t0 += CT) {
+    const int n_tok = min(CT, it.count - t0);
+    __syncthreads();
+    if (threadIdx.x < n_tok) trow[threadIdx.x] = base + t0 + threadIdx.x;
+    __syncthreads();
+    switch ((n_tok + 15) >> 4) {
+      case 1: pdown_chunk<1, PAIR>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+      case 2: pdown_chunk<2, PAIR>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+      case 3: if constexpr (!PAIR) pdown_chunk<3, PAIR>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+      default: if constexpr (!PAIR) pdown_chunk<4, PAIR>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
+    }
+  }
+}
+
+__global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pgateup(
+    PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs0[kPGuBuf];
+  __shared__ __attribute__((aligned(16))) __bf16 bs1[kPGuBuf];
+  __shared__ int trow[kPGuTokens];
+  pgateup_body<false>(p, bs0, bs1, trow);
+}
+__global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pgateup_pair(
+    PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs0[kPGuBuf];
+  __shared__ __attribute__((aligned(16))) __bf16 bs1[kPGuBuf];
+  __shared__ int trow[kPGuTokens];
+  pgateup_body<true>(p, bs0, bs1, trow);
+}
 __global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pdown(
     PrefillArgs p) {
   __shared__ __attribute__((aligned(16))) __bf16 bs0[kPDnBuf];
   __shared__ __attribute__((aligned(16))) __bf16 bs1[kPDnBuf];
   __shared__ int trow[kPTokens];
-  PItem it;
-  if (!prefill_item(p, blockIdx.y, it)) return;
-  const int P = p.T * p.K;
-  const int base = it.shared ? P + it.first : it.first;  // first activation row
-  for (int t0 = 0; t0 < it.count; t0 += kPTokens) {
-    const int n_tok = min(kPTokens, it.count - t0);
-    __syncthreads();
-    if (threadIdx.x < n_tok) trow[threadIdx.x] = base + t0 + threadIdx.x;
-    __syncthreads();
-    switch ((n_tok + 15) >> 4) {
-      case 1: pdown_chunk<1>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
-      case 2: pdown_chunk<2>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
-      case 3: pdown_chunk<3>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
-      default: pdown_chunk<4>(p, it, bs0, bs1, trow, base + t0, n_tok); break;
-    }
-  }
+  pdown_body<false>(p, bs0, bs1, trow);
+}
+__global__ __launch_bounds__(kPWaves * 64) __attribute__((amdgpu_waves_per_eu(4))) void k_pdown_pair(
+    PrefillArgs p) {
+  __shared__ __attribute__((aligned(16))) __bf16 bs0[kPDnBuf];
+  __shared__ __attribute__((aligned(16))) __bf16 bs1[kPDnBuf];
+  __shared__ int trow[kPTokens];
+  pdown_body<true>(p, bs0, bs1, trow);
+}
+
+// x -> (hi, lo) bf16 pair planes
+__global__ __launch_bounds__(256) void k_bf16_pair(const float* __restrict__ x, __bf16* __restrict__ xb,
+                                                   size_t n) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = x[i];
+  const __bf16 hi = (__bf16)v;
+  xb[i] = hi;
+  xb[n + i] = (__bf16)(v - (float)hi);
 }
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* o, __bf16* xb, int T, int d,
@@ -414,11 +495,23 @@ hipError_t launch_rms_norm(const float* x, const float* w, float* o, __bf16* xb,
   return hipGetLastError();
 }
 
-hipError_t launch_prefill_experts(const PrefillArgs& p, hipStream_t s) {
+hipError_t launch_prefill_experts(const PrefillArgs& p, bool pair, hipStream_t s) {
   const int items = 256 + (p.shared ? (p.T + kPTokens - 1) / kPTokens : 0);
-  hipLaunchKernelGGL(k_pgateup, dim3(kFfn / kPM, items), dim3(kPWaves * 64), 0, s, p);
+  if (pair)
+    hipLaunchKernelGGL(k_pgateup_pair, dim3(kFfn / kPM, items), dim3(kPWaves * 64), 0, s, p);
+  else
+    hipLaunchKernelGGL(k_pgateup, dim3(kFfn / kPM, items), dim3(kPWaves * 64), 0, s, p);
   if (hipError_t e = hipGetLastError()) return e;
-  hipLaunchKernelGGL(k_pdown, dim3(kHidden / kPM, items), dim3(kPWaves * 64), 0, s, p);
+  if (pair && p.actf) return hipSuccess;  // the down runs on the dot4 kernels
+  if (pair)
+    hipLaunchKernelGGL(k_pdown_pair, dim3(kHidden / kPM, items), dim3(kPWaves * 64), 0, s, p);
+  else
+    hipLaunchKernelGGL(k_pdown, dim3(kHidden / kPM, items), dim3(kPWaves * 64), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_bf16_pair(const float* x, __bf16* xb, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(k_bf16_pair, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, xb, n);
   return hipGetLastError();
 }
 

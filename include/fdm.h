@@ -256,6 +256,19 @@ int fdm_moe_forward_batched(int L, const float *d_X, const float *d_H_in, int T,
                             float *d_hidden, int *d_idx, float *d_w, int *d_n_distinct,
                             void *stream);
 
+/* Expert kernels behind fdm_moe_forward_batched (no counterpart in the
+ * reference; a tuning and test switch).  FDM_BATCH_DOT4: per-token int8
+ * digit dot products, each expert tile held in registers while its tokens
+ * stream through LDS.  FDM_BATCH_MFMA: the grouped GEMMs on MFMA at pair
+ * precision (weights and activations as bf16 hi/lo pairs, ~1e-5 relative
+ * error).  FDM_BATCH_AUTO: MFMA from FDM_BATCH_MFMA_MIN_T tokens per step,
+ * DOT4 below.  Stores the previous mode in *prev when prev is not NULL. */
+#define FDM_BATCH_AUTO 0
+#define FDM_BATCH_DOT4 1
+#define FDM_BATCH_MFMA 2
+#define FDM_BATCH_MFMA_MIN_T 96
+int fdm_set_batch_kernel(int mode, int *prev);
+
 /* ---- rms_norm on the device (infer.m:369-374, the h_post of infer.m:1850):
  * o[t] = x[t] * (1 / sqrt(sum_i x[t][i]^2 / d + 1e-6)) * w, bit-exact with
  * the reference's sequential loop.  d_w may be NULL (w = 1); d_o may alias

@@ -23,7 +23,17 @@ def layer(request, fdm):
     fdm.release_layer(L)
 
 
-def check_tokens(fdm, oracle, L, lay, T, K, seed, tokens_checked):
+@pytest.fixture(params=["dot4", "mfma"])
+def batch_kernel(request, fdm):
+    """Runs the test under each expert path behind moe_forward_batched: the
+    per-token digit dot products and the grouped MFMA GEMMs (pair precision)."""
+    mode = fdm.BATCH_DOT4 if request.param == "dot4" else fdm.BATCH_MFMA
+    prev = fdm.set_batch_kernel(mode)
+    yield request.param
+    fdm.set_batch_kernel(prev)
+
+
+def check_tokens(fdm, oracle, L, lay, T, K, seed, tokens_checked, tol=TOL):
     import torch
     X = np.stack([oracle.synth_normal(7168, 0.0, 1.0, seed + t) for t in range(T)])
     Hin = np.stack([oracle.synth_normal(7168, 0.0, 1.0, seed + 1000 + t) for t in range(T)])
@@ -56,20 +66,51 @@ def check_tokens(fdm, oracle, L, lay, T, K, seed, tokens_checked):
             moe += np.float64(rw[k]) * ffn(int(ri[k]))
         want = Hin[t].astype(np.float64) + moe + ffn(-1)
         err = rel_l2(got[t], want)
-        assert err <= TOL, (t, err)
+        assert err <= tol, (t, err)
     # every token's routing is checked (cheap); outputs on the sampled tokens
     for t in range(T):
         ri, rw = oracle.route(oracle.router_logits(Wg, X[t]), bias, K=K)
         assert np.array_equal(gi[t], ri), t
 
 
-@pytest.mark.parametrize("T,K", [(1, 8), (16, 8), (5, 3)])
-def test_batched_matches_per_token_oracle(fdm, oracle, layer, T, K):
+@pytest.mark.parametrize("T,K", [(1, 8), (16, 8), (5, 3), (70, 8)])
+def test_batched_matches_per_token_oracle(fdm, oracle, layer, batch_kernel, T, K):
+    """T = 70: several tokens per expert (32-token GEMM chunks) and a shared
+    expert spread over two 64-token items."""
     L, lay = layer
-    check_tokens(fdm, oracle, L, lay, T, K, 9000 + 17 * T, tokens_checked=sorted({0, T // 2, T - 1}))
+    # the pair-precision GEMMs carry ~1e-5 error: held to 1e-4; the int8
+    # digits of the dot4 path lose up to ~7e-4 on heavy-tailed activations
+    tol = 1e-4 if batch_kernel == "mfma" else TOL
+    check_tokens(fdm, oracle, L, lay, T, K, 9000 + 17 * T, tokens_checked=sorted({0, T // 2, T - 1}),
+                 tol=tol)
 
 
-def test_batched_equals_single_token_layer(fdm, oracle, layer):
+def test_batched_paths_agree(fdm, layer):
+    """The two expert paths on the same 96-token step: identical routing,
+    outputs within the 1e-3 bar of each other (the dot4 path's digits
+    dominate the difference)."""
+    import torch
+    from flash_deepseek_amd.synthetic import make_tokens
+    L, _ = layer
+    T, K = 96, 8
+    X = make_tokens(T, 4321)
+    outs = []
+    for mode in (fdm.BATCH_DOT4, fdm.BATCH_MFMA):
+        prev = fdm.set_batch_kernel(mode)
+        try:
+            out = empty_f32(T * 7168)
+            idx = torch.empty(T * K, dtype=torch.int32, device="cuda")
+            say(f"moe_forward_batched L={L} T={T} mode={mode}")
+            fdm.moe_forward_batched(L, X, None, T, K, out, idx, None, None)
+            outs.append((to_host(out).reshape(T, 7168), to_host(idx)))
+        finally:
+            fdm.set_batch_kernel(prev)
+    assert np.array_equal(outs[0][1], outs[1][1])
+    for t in range(T):
+        assert rel_l2(outs[1][0][t], outs[0][0][t].astype(np.float64)) <= TOL, t
+
+
+def test_batched_equals_single_token_layer(fdm, oracle, layer, batch_kernel):
     """Each token of a batch gets the same routing as fdm_moe_layer and an
     output within the digit error of it."""
     import torch
@@ -86,7 +127,8 @@ def test_batched_equals_single_token_layer(fdm, oracle, layer):
         i1 = torch.empty(K, dtype=torch.int32, device="cuda")
         fdm.moe_layer(L, to_dev(X[t]), None, K, one, i1)
         assert np.array_equal(to_host(i1), gi[t])
-        assert rel_l2(got[t], to_host(one).astype(np.float64)) <= 1e-4
+        # the same digits as the layer kernel (dot4) or the pair GEMMs (mfma)
+        assert rel_l2(got[t], to_host(one).astype(np.float64)) <= (1e-4 if batch_kernel == "dot4" else TOL)
 
 
 def test_batched_errors(fdm, layer):
@@ -98,3 +140,5 @@ def test_batched_errors(fdm, layer):
         fdm.moe_forward_batched(L, x, None, 513, 8, empty_f32(7168))
     with pytest.raises(fdm.FdmError):
         fdm.moe_forward_batched(L, x, None, 1, 17, empty_f32(7168))
+    with pytest.raises(fdm.FdmError):
+        fdm.set_batch_kernel(3)
