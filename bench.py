@@ -157,10 +157,10 @@ def main():
     ap.add_argument("--prof-steps", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--batched", default="",
-                    help="also time batched decode (config 3) at these token counts, e.g. 16,64,256")
-    ap.add_argument("--prefill", type=int, default=0,
-                    help="also time prefill of this many tokens through 4 resident layers (config 4)")
+    ap.add_argument("--batched", default="16,64,256",
+                    help="also time batched decode at these token counts ('' to skip)")
+    ap.add_argument("--prefill", type=int, default=512,
+                    help="also time prefill of this many tokens through 4 resident layers (0 to skip)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter-collection run: a few layer steps, then plain 256 MiB "
                          "copies (read + write of known size) that calibrate the counters")
