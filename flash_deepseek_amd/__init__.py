@@ -29,7 +29,7 @@ __all__ = [
     "init", "shutdown", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
     "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
-    "moe_forward_host", "moe_layer", "set_layer_kernel", "LAYER_AUTO", "LAYER_ITEMS", "LAYER_STREAM", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "moe_forward_host", "moe_layer", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -146,18 +146,6 @@ def moe_forward_host(L, h_post, exp_idx, exp_w, K, moe_out):
     """metal_moe_forward's exact convention: numpy host arrays, synchronous."""
     call("fdm_moe_forward_host", L, h_post.ctypes.data, exp_idx.ctypes.data,
          exp_w.ctypes.data, K, moe_out.ctypes.data)
-
-
-LAYER_AUTO, LAYER_ITEMS, LAYER_STREAM = 0, 1, 2
-
-
-def set_layer_kernel(mode):
-    """Kernel behind moe_layer: LAYER_ITEMS (ordered work list), LAYER_STREAM
-    (256 resident workgroups; needs >= 256 CUs) or LAYER_AUTO (the faster,
-    currently ITEMS).  Returns the previous mode."""
-    prev = ctypes.c_int(-1)
-    call("fdm_set_layer_kernel", mode, ctypes.byref(prev))
-    return prev.value
 
 
 BATCH_AUTO, BATCH_DOT4, BATCH_MFMA = 0, 1, 2

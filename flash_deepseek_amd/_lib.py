@@ -49,7 +49,6 @@ SIGNATURES = {
     "fdm_strerror": [_i],
     "fdm_last_error": [],
     "fdm_device_cus": [],
-    "fdm_set_layer_kernel": [_i, ctypes.POINTER(ctypes.c_int)],
     "fdm_set_batch_kernel": [_i, ctypes.POINTER(ctypes.c_int)],
     "fdm_malloc": [ctypes.POINTER(_vp), _sz],
     "fdm_free": [_vp],

@@ -24,7 +24,6 @@ SOURCES = [
     "router_kernels.hip",
     "moe_kernels.hip",
     "layer_kernel.hip",
-    "stream_kernel.hip",
     "batched_kernels.hip",
     "prefill_kernels.hip",
     "synth_kernels.hip",

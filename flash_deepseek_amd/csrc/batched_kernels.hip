@@ -9,6 +9,8 @@
 //   k_router_logits / k_route   per token (router_kernels.hip)
 //   k_dispatch                  group the T*K (token, slot) pairs by expert
 //   k_xdigits                   digits of the T tokens
+// Experts are read in the resident expert layout (rel_load_group).
+//
 //   k_bgateup                   per (distinct expert or shared, 8-row tile): the
 //                               weight tile stays in registers while the
 //                               expert's tokens stream through LDS
@@ -124,9 +126,9 @@ __global__ __launch_bounds__(256) void k_bgateup(BatchArgs b) {
     const ItemRows r = item_rows(b, d, D, &e);
     const uint8_t* blob = r.shared ? b.shared : b.experts + (size_t)e * b.expert_size;
     Q4KGroupLoad ld[7];
-    const uint8_t* rowp = blob + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
+    const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
 #pragma unroll
-    for (int i = 0; i < 7; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
+    for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     for (int i = 0; i < r.count; ++i) {
       const int tok = r.shared ? i : b.pair_tok[r.first + i];
       const int out_row = r.shared ? P + i : r.first + i;
@@ -172,9 +174,8 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
     Q4KGroupLoad ld[2];
     Q6KHalfLoad l6;
     if (!Q6) {
-      const uint8_t* rowp = dbase + (size_t)row * kQ4KRowFfn;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
+      for (int i = 0; i < 2; ++i) ld[i] = rel_load_group<true>(dbase, row, 4 * i + (l16 >> 2), l16 & 3);
     } else {
       l6 = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (l16 >> 1) * kQ6KBlock, l16 & 1);
     }

@@ -17,7 +17,6 @@
 namespace fdm {
 
 int g_num_cus = 0;
-int g_layer_mode = FDM_LAYER_AUTO;
 int g_batch_mode = FDM_BATCH_AUTO;
 
 namespace {
@@ -81,7 +80,8 @@ struct Workspace {
 
 struct Layer {
   bool resident = false;
-  bool owned = false;  // buffers allocated by fdm_layer_upload
+  bool owned = false;  // router weights and bias allocated by the library (upload / load)
+  // experts and shared expert: library-owned, in the resident expert layout
   const uint8_t* experts = nullptr;
   size_t expert_size = 0;
   int n_experts = 0;
@@ -181,13 +181,44 @@ int alloc_workspace() {
 }
 
 void release_layer(Layer& L) {
-  if (L.resident && L.owned) {
+  if (L.resident) {
     (void)hipFree(const_cast<uint8_t*>(L.experts));
-    (void)hipFree(const_cast<float*>(L.Wg));
-    if (L.bias) (void)hipFree(const_cast<float*>(L.bias));
     if (L.shared) (void)hipFree(const_cast<uint8_t*>(L.shared));
+    if (L.owned) {
+      (void)hipFree(const_cast<float*>(L.Wg));
+      if (L.bias) (void)hipFree(const_cast<float*>(L.bias));
+    }
   }
   L = Layer();
+}
+
+// Packed expert blobs (the 256 experts at src + e * src_stride, and the
+// shared one) -> freshly allocated buffers in the resident expert layout.
+// Synchronous.  On failure nothing stays allocated.
+int make_resident_experts(const uint8_t* src, size_t src_stride, const uint8_t* src_shared, size_t es, bool q6,
+                          int L, uint8_t** rel, uint8_t** rel_shared) {
+  *rel = nullptr;
+  *rel_shared = nullptr;
+  // the source may still be written by work queued on any stream
+  FDM_HIP(hipDeviceSynchronize());
+  void *e = nullptr, *sh = nullptr;
+  const size_t eb = es * FDM_N_EXPERTS;
+  if (hipMalloc(&e, eb) != hipSuccess || (src_shared && hipMalloc(&sh, es) != hipSuccess)) {
+    if (e) (void)hipFree(e);
+    return fail(FDM_E_NOMEM, "cannot allocate %zu bytes for the experts of layer %d", eb + es, L);
+  }
+  hipError_t r = launch_rel_pack(src, src_stride, static_cast<uint8_t*>(e), es, FDM_N_EXPERTS, q6, nullptr);
+  if (r == hipSuccess && src_shared)
+    r = launch_rel_pack(src_shared, es, static_cast<uint8_t*>(sh), es, 1, q6, nullptr);
+  if (r == hipSuccess) r = hipStreamSynchronize(nullptr);
+  if (r != hipSuccess) {
+    (void)hipFree(e);
+    if (sh) (void)hipFree(sh);
+    return hip_fail(r, "repacking the experts of a layer");
+  }
+  *rel = static_cast<uint8_t*>(e);
+  *rel_shared = static_cast<uint8_t*>(sh);
+  return FDM_OK;
 }
 
 int get_layer(int L, Layer** out) {
@@ -260,6 +291,7 @@ SlotTable slots_for(const Layer& L, const int* idx, const float* w, int K, bool 
   t.w = w;
   t.K = K;
   t.n_slots = K + ((with_shared && L.shared) ? 1 : 0);
+  t.rel = true;
   return t;
 }
 
@@ -447,18 +479,23 @@ int upload_layer_common(const GgufManifest& m, const LayerTensors& lt, LayerBuff
 }
 
 int commit_layer(int L, LayerBuffers& b, size_t es, bool q6) {
+  uint8_t *rel = nullptr, *rel_shared = nullptr;
+  if (int rc = make_resident_experts(static_cast<const uint8_t*>(b.experts), es,
+                                     static_cast<const uint8_t*>(b.shared), es, q6, L, &rel, &rel_shared))
+    return rc;
   release_layer(g.layers[L]);
   Layer& y = g.layers[L];
   y.resident = true;
   y.owned = true;
-  y.experts = static_cast<const uint8_t*>(b.experts);
+  y.experts = rel;
   y.expert_size = es;
   y.n_experts = FDM_N_EXPERTS;
   y.down_q6 = q6;
   y.Wg = static_cast<const float*>(b.Wg);
   y.bias = static_cast<const float*>(b.bias);
-  y.shared = static_cast<const uint8_t*>(b.shared);
-  b = LayerBuffers();  // ownership moved to the layer table
+  y.shared = rel_shared;
+  b.Wg = nullptr;  // moved to the layer table; the packed staging copies are freed with b
+  b.bias = nullptr;
   return FDM_OK;
 }
 
@@ -677,6 +714,7 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   t.w = nullptr;
   t.K = 0;
   t.n_slots = 1;
+  t.rel = false;  // the caller's blob: packed layout
   {
     ProfScope p(FDM_PROF_XDIGITS, s);
     FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, g.ws.xd, s));
@@ -731,17 +769,22 @@ int fdm_layer_attach(int L, const void* d_experts, size_t expert_size, int n_exp
   if (int rc = down_type(expert_size, &q6)) return rc;
   if (!aligned(d_experts, 16) || !aligned(d_Wg, 16) || (d_shared && !aligned(d_shared, 16)))
     return fail(FDM_E_INVAL, "layer buffers must be 16-byte aligned");
+  uint8_t *rel = nullptr, *rel_shared = nullptr;
+  if (int rc = make_resident_experts(static_cast<const uint8_t*>(d_experts), expert_size,
+                                     static_cast<const uint8_t*>(d_shared), expert_size, q6, L, &rel,
+                                     &rel_shared))
+    return rc;
   release_layer(g.layers[L]);
   Layer& y = g.layers[L];
   y.resident = true;
   y.owned = false;
-  y.experts = static_cast<const uint8_t*>(d_experts);
+  y.experts = rel;
   y.expert_size = expert_size;
   y.n_experts = n_experts;
   y.down_q6 = q6;
   y.Wg = d_Wg;
   y.bias = d_bias;
-  y.shared = static_cast<const uint8_t*>(d_shared);
+  y.shared = rel_shared;
   return FDM_OK;
 }
 
@@ -778,17 +821,25 @@ int fdm_layer_upload(int L, const void* h_experts, size_t expert_size, int n_exp
     cleanup();
     return hip_fail(e, "layer upload");
   }
+  uint8_t *rel = nullptr, *rel_shared = nullptr;
+  if (int rc = make_resident_experts(static_cast<const uint8_t*>(de), expert_size,
+                                     static_cast<const uint8_t*>(ds), expert_size, q6, L, &rel, &rel_shared)) {
+    cleanup();
+    return rc;
+  }
+  (void)hipFree(de);  // the packed staging copies
+  if (ds) (void)hipFree(ds);
   release_layer(g.layers[L]);
   Layer& y = g.layers[L];
   y.resident = true;
   y.owned = true;
-  y.experts = static_cast<const uint8_t*>(de);
+  y.experts = rel;
   y.expert_size = expert_size;
   y.n_experts = n_experts;
   y.down_q6 = q6;
   y.Wg = static_cast<const float*>(dw);
   y.bias = static_cast<const float*>(db);
-  y.shared = static_cast<const uint8_t*>(ds);
+  y.shared = rel_shared;
   return FDM_OK;
 }
 
@@ -974,24 +1025,10 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   a.flags = g.ws.layer_flags;
   if (++g.ws.epoch == 0) ++g.ws.epoch;  // flags start at 0: skip epoch 0 on wrap
   a.epoch = g.ws.epoch;
-  // AUTO runs the work list: it measures faster than the streamed kernel on MI355X.
-  const bool streamed = g_layer_mode == FDM_LAYER_STREAM;
   {
     ProfScope p(FDM_PROF_LAYER, s);
-    FDM_HIP(streamed ? launch_stream_layer(a, s) : launch_layer(a, s));
+    FDM_HIP(launch_layer(a, s));
   }
-  return FDM_OK;
-}
-
-int fdm_set_layer_kernel(int mode, int* prev) {
-  if (int rc = check_ready()) return rc;
-  if (mode != FDM_LAYER_AUTO && mode != FDM_LAYER_ITEMS && mode != FDM_LAYER_STREAM)
-    return fail(FDM_E_INVAL, "layer kernel mode %d", mode);
-  if (mode == FDM_LAYER_STREAM && g_num_cus < stream_layer_workgroups())
-    return fail(FDM_E_INVAL, "the streamed layer needs %d CUs, the device has %d", stream_layer_workgroups(),
-                g_num_cus);
-  if (prev) *prev = g_layer_mode;
-  g_layer_mode = mode;
   return FDM_OK;
 }
 

@@ -22,6 +22,10 @@ namespace fdm {
 hipError_t launch_fp16_to_fp32(const uint16_t* src, float* dst, size_t n, hipStream_t s);
 hipError_t launch_dequant_q4k(const uint8_t* src, float* dst, size_t n_blocks, hipStream_t s);
 hipError_t launch_dequant_q6k(const uint8_t* src, float* dst, size_t n_blocks, hipStream_t s);
+// n packed expert blobs (src + b * src_stride) -> the resident expert layout
+// (dst + b * expert_size): gate, up and a Q4_K down permuted, a Q6_K down copied.
+hipError_t launch_rel_pack(const uint8_t* src, size_t src_stride, uint8_t* dst, size_t expert_size,
+                           int n_blobs, bool down_q6, hipStream_t s);
 
 // matvec_kernels.hip
 // Digits of `n_groups` consecutive 64-element groups of x.
@@ -47,6 +51,7 @@ struct SlotTable {
   const float* w;          // K routing weights (device)
   int K;                   // routed slots
   int n_slots;             // K or K + 1 (shared)
+  bool rel;                // blobs in the resident expert layout (else packed)
 };
 // gate/up matvecs + SwiGLU for every slot; writes act[slot][2048] and the
 // digits of act (act_xd[slot][32]).  counters: (FDM_MAX_K + 1) x 64 ints,
@@ -103,9 +108,6 @@ struct LayerArgs {
   unsigned epoch;          // non-zero, different from every earlier call's
 };
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
-// The same layer streamed by stream_layer_workgroups() resident workgroups.
-hipError_t launch_stream_layer(const LayerArgs& a, hipStream_t s);
-int stream_layer_workgroups();
 
 // batched_kernels.hip
 // Batched decode of T tokens through one layer with token -> expert

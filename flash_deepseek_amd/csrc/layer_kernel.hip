@@ -341,9 +341,10 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
     const int row = (tile0 + t) * kGuTileRows + 2 * wave + (q & 1);
     Q4KGroupLoad ld[7];
     if (blob) {
-      const uint8_t* rowp = blob + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
+      // resident expert layout: each half-wave load reads one 512-byte run
+      const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
 #pragma unroll
-      for (int i = 0; i < 7; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
+      for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     }
     if (t == 0) {
       // the digit record: 16-byte loads with the coherent (sc1) cache policy
@@ -407,12 +408,12 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
     constexpr int LR = kDnLanesQ4, RPW = 64 / LR;
     const int gl = lane % LR;  // group of the row's part
     const int row0 = item * kDnRowsQ4 + wave * (kDnRowsQ4L * RPW) + lane / LR;  // + RPW j
-    const int boff = (part * kPartGroups + gl) / 4 * kQ4KBlock;
+    const int blk = (part * kPartGroups + gl) / 4;
     Q4KGroupLoad ld[kDnRowsQ4L];
     if (blob) {
+      // resident expert layout: a wave's load (4 rows x one block quad) reads one 1 KB run
 #pragma unroll
-      for (int j = 0; j < kDnRowsQ4L; ++j)
-        ld[j] = q4k_load_group(dbase + (size_t)(row0 + RPW * j) * kQ4KRowFfn + boff, gl & 3);
+      for (int j = 0; j < kDnRowsQ4L; ++j) ld[j] = rel_load_group<true>(dbase, row0 + RPW * j, blk, gl & 3);
     }
     stage_act();
     float acc[kDnRowsQ4L] = {};

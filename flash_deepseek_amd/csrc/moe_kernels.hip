@@ -54,9 +54,12 @@ __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __res
   const int row = tile * kGuRows + 2 * wave + (q & 1);
   Q4KGroupLoad ld[7];
   if (blob) {
-    const uint8_t* rowp = blob + (q >= 2 ? kGateBytes : 0) + (size_t)row * kQ4KRowHidden;
+    const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
+    const uint8_t* rowp = mat + (size_t)row * kQ4KRowHidden;
 #pragma unroll
-    for (int i = 0; i < 7; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
+    for (int i = 0; i < 7; ++i)
+      ld[i] = t.rel ? rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g)
+                    : q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
   }
   stage_groups(xs, xd, kHidden / 64);
   __syncthreads();
@@ -120,9 +123,12 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
   if (!Q6) {
     Q4KGroupLoad ld[2];
     if (blob) {
-      const uint8_t* rowp = blob + 2 * (size_t)kGateBytes + (size_t)row * kQ4KRowFfn;
+      const uint8_t* mat = blob + 2 * (size_t)kGateBytes;
+      const uint8_t* rowp = mat + (size_t)row * kQ4KRowFfn;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) ld[i] = q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
+      for (int i = 0; i < 2; ++i)
+        ld[i] = t.rel ? rel_load_group<true>(mat, row, 4 * i + (l16 >> 2), l16 & 3)
+                      : q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
     }
     stage_groups(xs, act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
     __syncthreads();

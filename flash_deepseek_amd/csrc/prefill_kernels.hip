@@ -38,17 +38,25 @@ constexpr int kPTokens = 64;                       // tokens per shared-expert i
 // One lane's share of one Q4_K block for the MFMA A operand: the header and
 // the 8 qs bytes of each 64-element group that hold the lane's elements
 // (k = 32 s + 8 j .. +8 of sub-block s, j = lane / 16: bytes 32 (s/2) + 8 j,
-// low nibbles for even s, high for odd s).
+// low nibbles for even s, high for odd s), read from a matrix in the
+// resident expert layout (rel_step / rel_piece: the header dwords of a block
+// are consecutive pieces, qs bytes 32 g .. 32 g + 15 sit in the first half
+// of the step, 32 g + 16 .. 32 g + 31 in the second).
 struct Q4KLane {
   u32x4 hdr;
   uint2 qs[4];
 };
 
-__device__ __forceinline__ Q4KLane q4k_lane_load(const uint8_t* blk, int j) {
+template <bool DOWN>
+__device__ __forceinline__ Q4KLane q4k_lane_load(const uint8_t* mat, int row, int block, int j) {
+  constexpr int N = DOWN ? kRelDnPieces : kRelGuPieces;
+  const uint8_t* st = rel_step<DOWN>(mat, row, block);
+  const int L = rel_piece<DOWN>(row, block, 0);
+  const uint8_t* q = st + (j < 2 ? 0 : 16 * N) + 8 * (j & 1);
   Q4KLane r;
-  r.hdr = *reinterpret_cast<const u32x4_a4*>(blk);
+  r.hdr = *reinterpret_cast<const u32x4*>(st + 32 * N + 4 * L);
 #pragma unroll
-  for (int g = 0; g < 4; ++g) r.qs[g] = *reinterpret_cast<const uint2*>(blk + 16 + 32 * g + 8 * j);
+  for (int g = 0; g < 4; ++g) r.qs[g] = *reinterpret_cast<const uint2*>(q + 16 * (L + g));
   return r;
 }
 
@@ -279,7 +287,7 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
   constexpr int kBlocks = kHidden / kQK;  // 28, even
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane >> 4, c16 = lane & 15;
-  const uint32_t roff = (uint32_t)(blockIdx.x * kPM + wave * 16 + c16) * kQ4KRowHidden;  // the lane's A row
+  const int arow = blockIdx.x * kPM + wave * 16 + c16;  // the lane's A row
   const uint8_t* gbase = it.blob;
   const uint8_t* ubase = it.blob + kGateBytes;
   const BDma<NB, 2, kPGuTokens> dma =
@@ -292,7 +300,7 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
   }
   __syncthreads();  // both buffers free: the previous chunk's last block is read
   bdma_issue(dma, p.xb, bs0, 0);
-  Q4KLane gn = q4k_lane_load(gbase + roff, j), un = q4k_lane_load(ubase + roff, j);
+  Q4KLane gn = q4k_lane_load<false>(gbase, arow, 0, j), un = q4k_lane_load<false>(ubase, arow, 0, j);
   for (int b = 0; b < kBlocks; b += 2) {
     // Even block b from bs0 while b + 1 lands in bs1; odd block b + 1 from
     // bs1 while b + 2 lands in bs0 (the last pair re-stages block 27 into
@@ -301,8 +309,8 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
     wait_vm();
     __syncthreads();  // block b staged by every wave; bs1 read by all (block b - 1)
     bdma_issue(dma, p.xb, bs1, b + 1);
-    gn = q4k_lane_load(gbase + (roff + (b + 1) * kQ4KBlock), j);
-    un = q4k_lane_load(ubase + (roff + (b + 1) * kQ4KBlock), j);
+    gn = q4k_lane_load<false>(gbase, arow, b + 1, j);
+    un = q4k_lane_load<false>(ubase, arow, b + 1, j);
     pgateup_block<NB, PAIR>(bs0, gl, ul, ag, au, c16, j);
     gl = gn;
     ul = un;
@@ -310,8 +318,8 @@ __device__ __forceinline__ void pgateup_chunk(const PrefillArgs& p, const PItem&
     wait_vm();
     __syncthreads();  // block b + 1 staged; bs0 read by all (block b)
     bdma_issue(dma, p.xb, bs0, b2);
-    gn = q4k_lane_load(gbase + (roff + b2 * kQ4KBlock), j);
-    un = q4k_lane_load(ubase + (roff + b2 * kQ4KBlock), j);
+    gn = q4k_lane_load<false>(gbase, arow, b2, j);
+    un = q4k_lane_load<false>(ubase, arow, b2, j);
     pgateup_block<NB, PAIR>(bs1, gl, ul, ag, au, c16, j);
   }
   wait_vm();  // the re-staged copy has landed before the buffers are reused
@@ -393,7 +401,7 @@ __device__ __forceinline__ void pdown_chunk(const PrefillArgs& p, const PItem& i
   constexpr int NH = PAIR ? 2 : 1, HT = kPDnTok<PAIR>;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int j = lane >> 4, c16 = lane & 15;
-  const uint32_t roff = (uint32_t)(blockIdx.x * kPM + wave * 16 + c16) * kQ4KRowFfn;
+  const int arow = blockIdx.x * kPM + wave * 16 + c16;
   const uint8_t* dbase = it.blob + 2 * (size_t)kGateBytes;
   const BDma<NB, NH, HT> dma =
       bdma_init<NB, NH, HT>(trow, n_tok, kFfn * 2, PAIR ? (uint32_t)(p.act_rows * kFfn * 2) : 0u);
@@ -402,20 +410,20 @@ __device__ __forceinline__ void pdown_chunk(const PrefillArgs& p, const PItem& i
   for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   __syncthreads();
   bdma_issue(dma, p.actb, bs0, 0);
-  Q4KLane dn = q4k_lane_load(dbase + roff, j);
+  Q4KLane dn = q4k_lane_load<true>(dbase, arow, 0, j);
   for (int b = 0; b < kBlocks; b += 2) {
     Q4KLane dl = dn;
     wait_vm();
     __syncthreads();
     bdma_issue(dma, p.actb, bs1, b + 1);
-    dn = q4k_lane_load(dbase + (roff + (b + 1) * kQ4KBlock), j);
+    dn = q4k_lane_load<true>(dbase, arow, b + 1, j);
     pdown_block<NB, PAIR>(bs0, dl, acc, c16, j);
     dl = dn;
     const int b2 = min(b + 2, kBlocks - 1);
     wait_vm();
     __syncthreads();
     bdma_issue(dma, p.actb, bs0, b2);
-    dn = q4k_lane_load(dbase + (roff + b2 * kQ4KBlock), j);
+    dn = q4k_lane_load<true>(dbase, arow, b2, j);
     pdown_block<NB, PAIR>(bs1, dl, acc, c16, j);
   }
   wait_vm();

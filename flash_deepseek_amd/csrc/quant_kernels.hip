@@ -78,6 +78,59 @@ __global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__
   }
 }
 
+// ---- packed blobs -> the resident expert layout (REL) ----------------------------------
+// One thread per Q4_K block of a blob's gate, up or Q4_K down matrix: the
+// block's header dwords and its 8 half-groups go to their REL pieces (see
+// rel_step / rel_piece).  Blob b of n: src + b * src_stride ->
+// dst + b * expert_size.  A Q6_K down matrix is copied by the caller.
+__global__ __launch_bounds__(256) void k_rel_pack(const uint8_t* __restrict__ src, size_t src_stride,
+                                                  uint8_t* __restrict__ dst, size_t expert_size,
+                                                  int n_blobs, int with_down) {
+  constexpr int kGuBlocks = kFfn * (kHidden / kQK);  // 57,344 per gate / up matrix
+  constexpr int kDnBlocks = kHidden * (kFfn / kQK);  // 57,344 per down matrix
+  const int per_blob = 2 * kGuBlocks + (with_down ? kDnBlocks : 0);
+  const size_t total = (size_t)n_blobs * per_blob;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int b = (int)(i / per_blob);
+    int k = (int)(i % per_blob);
+    const uint8_t* sb = src + (size_t)b * src_stride;
+    uint8_t* db = dst + (size_t)b * expert_size;
+    const u32x4* blk;
+    uint8_t* step;
+    int L, N;
+    if (k < 2 * kGuBlocks) {
+      const int m = k / kGuBlocks;  // 0 gate, 1 up
+      k %= kGuBlocks;
+      const int row = k / (kHidden / kQK), block = k % (kHidden / kQK);
+      const size_t mo = (size_t)m * kGateBytes;
+      blk = reinterpret_cast<const u32x4*>(sb + mo + (size_t)row * kQ4KRowHidden + block * kQ4KBlock);
+      step = const_cast<uint8_t*>(rel_step<false>(db + mo, row, block));
+      L = rel_piece<false>(row, block, 0);
+      N = kRelGuPieces;
+    } else {
+      k -= 2 * kGuBlocks;
+      const int row = k / (kFfn / kQK), block = k % (kFfn / kQK);
+      const size_t mo = 2 * (size_t)kGateBytes;
+      blk = reinterpret_cast<const u32x4*>(sb + mo + (size_t)row * kQ4KRowFfn + block * kQ4KBlock);
+      step = const_cast<uint8_t*>(rel_step<true>(db + mo, row, block));
+      L = rel_piece<true>(row, block, 0);
+      N = kRelDnPieces;
+    }
+    u32x4 v[9];
+#pragma unroll
+    for (int j = 0; j < 9; ++j) v[j] = blk[j];
+    // header dwords g = 0..3 (pieces L + g are consecutive)
+    *reinterpret_cast<u32x4*>(step + 32 * N + 4 * L) = v[0];
+    // qs of group g: bytes 32 g .. 32 g + 31 of the block's qs = v[1 + 2 g], v[2 + 2 g]
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      *reinterpret_cast<u32x4*>(step + 16 * (L + g)) = v[1 + 2 * g];
+      *reinterpret_cast<u32x4*>(step + 16 * N + 16 * (L + g)) = v[2 + 2 * g];
+    }
+  }
+}
+
 static unsigned grid_for_waves(size_t waves) {
   size_t wg = (waves + 3) / 4;
   const size_t cap = (size_t)(g_num_cus > 0 ? g_num_cus : 256) * 16;
@@ -103,6 +156,22 @@ hipError_t launch_dequant_q6k(const uint8_t* src, float* dst, size_t n_blocks, h
   hipLaunchKernelGGL(k_dequant_q6k, dim3(grid_for_waves(n_blocks)), dim3(256), 0, s, src, dst,
                      n_blocks);
   return hipGetLastError();
+}
+
+hipError_t launch_rel_pack(const uint8_t* src, size_t src_stride, uint8_t* dst, size_t expert_size,
+                           int n_blobs, bool down_q6, hipStream_t s) {
+  const size_t blocks = (size_t)n_blobs * (down_q6 ? 2 : 3) * 57344;
+  size_t wg = (blocks + 255) / 256;
+  const size_t cap = (size_t)(g_num_cus > 0 ? g_num_cus : 256) * 32;
+  if (wg > cap) wg = cap;
+  hipLaunchKernelGGL(k_rel_pack, dim3((unsigned)(wg ? wg : 1)), dim3(256), 0, s, src, src_stride, dst,
+                     expert_size, n_blobs, down_q6 ? 0 : 1);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (!down_q6) return hipSuccess;
+  // a Q6_K down keeps the packed layout: one strided copy of every blob's down part
+  const size_t off = 2 * (size_t)kGateBytes;
+  return hipMemcpy2DAsync(dst + off, expert_size, src + off, src_stride, expert_size - off, (size_t)n_blobs,
+                          hipMemcpyDeviceToDevice, s);
 }
 
 }  // namespace fdm

@@ -117,8 +117,13 @@ int fdm_route(const float *d_logits, const float *d_bias, int T, int K, int *d_i
  * (infer.m:1794-1823) and the per-token pread of the selected experts
  * (infer.m:1577-1602): all experts of a layer stay resident in HBM.
  * expert_size must be FDM_EXPERT_Q4K_BYTES or FDM_EXPERT_Q6K_BYTES.
- * attach: the caller keeps ownership of the device buffers.
- * upload: the library allocates and copies from host memory.
+ * The experts (and the shared expert) are copied into library-owned device
+ * memory in the resident expert layout, a permutation of the packed blobs'
+ * bytes that lets every load of the expert kernels read whole contiguous
+ * lines (values unchanged); both calls are synchronous.
+ * attach: from device buffers, which the caller may free after the call;
+ *   d_Wg and d_bias stay the caller's and must live while the layer does.
+ * upload: from host memory; the library owns every buffer.
  * d_shared / h_shared: the shared expert as one more packed blob (may be
  * NULL: no shared expert). */
 int fdm_layer_attach(int L, const void *d_experts, size_t expert_size, int n_experts,
@@ -231,17 +236,6 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
  * FDM_E_STATE. */
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
-
-/* Kernel behind fdm_moe_layer (no counterpart in the reference, which has
- * one Metal path; a tuning and test switch): FDM_LAYER_ITEMS runs the
- * ordered work list, FDM_LAYER_STREAM streams the layer through 256
- * resident workgroups (fails with FDM_E_INVAL on a device with fewer than
- * 256 CUs) and FDM_LAYER_AUTO picks the faster one, currently ITEMS.
- * Stores the previous mode in *prev when prev is not NULL. */
-#define FDM_LAYER_AUTO 0
-#define FDM_LAYER_ITEMS 1
-#define FDM_LAYER_STREAM 2
-int fdm_set_layer_kernel(int mode, int *prev);
 
 /* ---- batched decode: T tokens through the MoE branch of layer L in one
  * step, with token -> expert dispatch so that each selected expert's weights

@@ -27,16 +27,6 @@ def layer(request, fdm):
     fdm.release_layer(L)
 
 
-@pytest.fixture(params=["items", "stream"])
-def layer_kernel(request, fdm):
-    """Runs the test under each kernel behind fdm_moe_layer: the ordered work
-    list and the streamed 256-workgroup kernel."""
-    mode = fdm.LAYER_ITEMS if request.param == "items" else fdm.LAYER_STREAM
-    prev = fdm.set_layer_kernel(mode)
-    yield request.param
-    fdm.set_layer_kernel(prev)
-
-
 def oracle_layer(oracle, lay, h, h_in, K, Wg=None, bias=None):
     Wg = to_host(lay.Wg if Wg is None else Wg)
     bias = to_host(lay.bias if bias is None else bias)
@@ -63,7 +53,7 @@ def run_layer(fdm, oracle, L, lay, K, tok, Wg=None, bias=None):
 
 
 @pytest.mark.parametrize("K,tok", [(8, 0), (8, 1), (1, 2), (4, 3), (16, 4)])
-def test_moe_layer(fdm, oracle, layer, layer_kernel, K, tok):
+def test_moe_layer(fdm, oracle, layer, K, tok):
     L, lay = layer
     h_in, got, gi, gw, ri, rw, moe, sd, want = run_layer(fdm, oracle, L, lay, K, tok)
     assert np.array_equal(gi, ri)
@@ -75,7 +65,7 @@ def test_moe_layer(fdm, oracle, layer, layer_kernel, K, tok):
 
 
 @pytest.mark.parametrize("K", [5, 7])
-def test_moe_layer_tied_set(fdm, oracle, layer, layer_kernel, K):
+def test_moe_layer_tied_set(fdm, oracle, layer, K):
     """Every router row and bias duplicated in adjacent experts (same group):
     each choice occurs twice, so with K odd the K-th largest is tied with an
     expert left out and the set itself depends on route()'s scan order."""
