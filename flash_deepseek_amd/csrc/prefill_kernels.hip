@@ -35,16 +35,15 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kPTokens = 64;                       // tokens per shared-expert item and per down chunk
 
-// One lane's share of one Q4_K block for the MFMA A operand: the header and
-// the 8 qs bytes of each 64-element group that hold the lane's elements
-// (k = 32 s + 8 j .. +8 of sub-block s, j = lane / 16: bytes 32 (s/2) + 8 j,
-// low nibbles for even s, high for odd s), read from a matrix in the
-// resident expert layout (rel_step / rel_piece: the header dwords of a block
-// are consecutive pieces, qs bytes 32 g .. 32 g + 15 sit in the first half
-// of the step, 32 g + 16 .. 32 g + 31 in the second).
+// One lane's share of one Q4_K block for the MFMA A operand.  Lane (c16, j)
+// of a wave holds row c16 and the 32 qs bytes 32 j .. 32 j + 31, i.e. all of
+// sub-blocks 2 j (low nibbles) and 2 j + 1 (high nibbles), as two whole
+// 16-byte pieces of the resident expert layout (q0: bytes 32 j .. +15, q1:
+// 32 j + 16 .. +31; rel_step / rel_piece), plus the block header.  The four
+// lanes of a row then read one contiguous 64-byte run per instruction.
 struct Q4KLane {
   u32x4 hdr;
-  uint2 qs[4];
+  u32x4 q0, q1;
 };
 
 template <bool DOWN>
@@ -52,39 +51,40 @@ __device__ __forceinline__ Q4KLane q4k_lane_load(const uint8_t* mat, int row, in
   constexpr int N = DOWN ? kRelDnPieces : kRelGuPieces;
   const uint8_t* st = rel_step<DOWN>(mat, row, block);
   const int L = rel_piece<DOWN>(row, block, 0);
-  const uint8_t* q = st + (j < 2 ? 0 : 16 * N) + 8 * (j & 1);
   Q4KLane r;
   r.hdr = *reinterpret_cast<const u32x4*>(st + 32 * N + 4 * L);
-#pragma unroll
-  for (int g = 0; g < 4; ++g) r.qs[g] = *reinterpret_cast<const uint2*>(q + 16 * (L + g));
+  r.q0 = *reinterpret_cast<const u32x4*>(st + 16 * (L + j));
+  r.q1 = *reinterpret_cast<const u32x4*>(st + 16 * N + 16 * (L + j));
   return r;
 }
 
-// The lane's 8 weights of sub-block S (d*sc*q - dmin*m in fp32 after the
-// dequant of quant.c:49-57) as bf16: hi = bf16(w) and, with PAIR, the
-// remainder lo = bf16(w - hi).
+// The lane's 8 weights of MFMA step M (0..7) of a block: sub-block
+// s = 2 j + (M >> 2), elements 8 (M & 3) .. 8 (M & 3) + 7 of it, i.e. block
+// elements 64 j + 32 (M >> 2) + 8 (M & 3) + 0..7 (k-piece 8 j + M of the
+// block; the B operand reads the same piece), as d*sc*q - dmin*m in fp32
+// after the dequant of quant.c:49-57, then bf16: hi = bf16(w) and, with PAIR,
+// the remainder lo = bf16(w - hi).
 struct W8 {
   bf16x8 hi, lo;
 };
 
-template <int S, bool PAIR>
-__device__ __forceinline__ W8 q4k_lane_w(const Q4KLane& r) {
-  const uint32_t s0 = r.hdr.y, s1 = r.hdr.z, s2 = r.hdr.w;
-  // get_scale_min_k4(S) (quant.c:26-34) on the 12 scale bytes s0|s1|s2
-  int sc, m;
-  if constexpr (S < 4) {
-    sc = (int)((s0 >> (8 * S)) & 63u);
-    m = (int)((s1 >> (8 * S)) & 63u);
-  } else {
-    const uint32_t b = (s2 >> (8 * (S - 4))) & 0xFFu;
-    sc = (int)((b & 0xFu) | (((s0 >> (8 * (S - 4))) >> 6 & 3u) << 4));
-    m = (int)((b >> 4) | (((s1 >> (8 * (S - 4))) >> 6 & 3u) << 4));
-  }
+template <int M, bool PAIR>
+__device__ __forceinline__ W8 q4k_lane_w(const Q4KLane& r, int j) {
+  constexpr int H = M >> 2, R = M & 3;
+  // get_scale_min_k4(s) (quant.c:26-34) on the 12 scale bytes hdr.y|z|w for
+  // the lane's s = 2 j + H: byte s & 3 of each word; s >= 4 when j >= 2
+  const uint32_t sh = 8u * (uint32_t)((2 * j + H) & 3);
+  const uint32_t b0 = (r.hdr.y >> sh) & 0xFFu, b1 = (r.hdr.z >> sh) & 0xFFu, b2 = (r.hdr.w >> sh) & 0xFFu;
+  // branch-free select (a conditional here becomes divergent branches)
+  const uint32_t up = 0u - (uint32_t)(j >> 1);
+  const int sc = (int)((((b2 & 0xFu) | ((b0 >> 6) << 4)) & up) | ((b0 & 63u) & ~up));
+  const int m = (int)((((b2 >> 4) | ((b1 >> 6) << 4)) & up) | ((b1 & 63u) & ~up));
   const float d1 = half_to_float(r.hdr.x) * (float)sc;
   const float m1 = half_to_float(r.hdr.x >> 16) * (float)m;
-  const uint2 w = r.qs[S >> 1];
-  uint32_t lo = (S & 1) ? (w.x >> 4) & 0x0F0F0F0Fu : w.x & 0x0F0F0F0Fu;
-  uint32_t hi = (S & 1) ? (w.y >> 4) & 0x0F0F0F0Fu : w.y & 0x0F0F0F0Fu;
+  const u32x4& q = R < 2 ? r.q0 : r.q1;
+  const uint32_t w0 = q[2 * (R & 1)], w1 = q[2 * (R & 1) + 1];
+  uint32_t lo = H ? (w0 >> 4) & 0x0F0F0F0Fu : w0 & 0x0F0F0F0Fu;
+  uint32_t hi = H ? (w1 >> 4) & 0x0F0F0F0Fu : w1 & 0x0F0F0F0Fu;
   // Opaque to the optimiser: otherwise it folds the mask into one bit-field
   // extract per nibble instead of converting bytes 1..3 in place.
   asm("" : "+v"(lo), "+v"(hi));
@@ -240,13 +240,14 @@ __device__ __forceinline__ void bdma_issue(const BDma<NB, NH, HT>& d, const __bf
 // The wave's direct LDS loads (and every other global load) have landed.
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// B operand of an MFMA from the LDS tile: token row tok = 16 nb + c16 of half
-// h, k-piece 4 S + j of the current block.
+// B operand of MFMA step M from the LDS tile: token row tok = 16 nb + c16 of
+// half h, k-piece 8 j + M of the current block (the pieces q4k_lane_w<M>
+// dequantises for lane j).
 template <int HT>
-__device__ __forceinline__ bf16x8 lds_b(const __bf16* bs, int h, int nb, int c16, int S, int j) {
+__device__ __forceinline__ bf16x8 lds_b(const __bf16* bs, int h, int nb, int c16, int M, int j) {
   const int t = 16 * nb + c16;
   return *reinterpret_cast<const bf16x8*>(reinterpret_cast<const uint8_t*>(bs) + (h * HT + t) * kPRowB +
-                                           16 * ((4 * S + j) ^ c16));
+                                           16 * ((8 * j + M) ^ c16));
 }
 
 // ---- grouped gate/up GEMM + SwiGLU --------------------------------------------------------
@@ -263,7 +264,7 @@ __device__ __forceinline__ void pgateup_block(const __bf16* cur, const Q4KLane& 
                                               f32x4 (&ag)[NB], f32x4 (&au)[NB], int c16, int j) {
 #define FDM_PGU_STEP(S)                                                  \
   {                                                                      \
-    const W8 ga = q4k_lane_w<S, PAIR>(gl), ua = q4k_lane_w<S, PAIR>(ul); \
+    const W8 ga = q4k_lane_w<S, PAIR>(gl, j), ua = q4k_lane_w<S, PAIR>(ul, j); \
     _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                  \
       const bf16x8 bh = lds_b<kPGuTokens>(cur, 0, nb, c16, S, j);        \
       const bf16x8 bl = lds_b<kPGuTokens>(cur, 1, nb, c16, S, j);        \
@@ -378,7 +379,7 @@ __device__ __forceinline__ void pdown_block(const __bf16* cur, const Q4KLane& dl
   constexpr int HT = kPDnTok<PAIR>;
 #define FDM_PDN_STEP(S)                                                                  \
   {                                                                                      \
-    const W8 da = q4k_lane_w<S, PAIR>(dl);                                               \
+    const W8 da = q4k_lane_w<S, PAIR>(dl, j);                                            \
     _Pragma("unroll") for (int nb = 0; nb < NB; ++nb) {                                  \
       const bf16x8 bh = lds_b<HT>(cur, 0, nb, c16, S, j);                                \
       acc[nb] = mfma16(da.hi, bh, acc[nb]);                                              \
