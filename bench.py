@@ -147,6 +147,45 @@ def bench_prefill(F, torch, layers, args, stream, K, n_layers=4, iters=5):
             "mfma_util_est": round(flops / dt / 2.5e15, 4)}
 
 
+def bench_dense(F, torch, args, stream, steps=60, warmup=6):
+    """Dense FFN layers 0..n-1 (R1: 3 layers, F16 weights, inter 18432):
+    hidden = h_in + W_down (silu(W_gate h) * (W_up h)) per call, the next
+    layer each call (each layer's 792 MB exceeds the 256 MB MALL)."""
+    from flash_deepseek_amd.synthetic import make_tokens
+    inter = F.DENSE_FFN
+    g = torch.Generator(device="cuda").manual_seed(4242)
+    for l in range(args.dense):
+        mats = [(torch.randn((inter, HIDDEN), generator=g, device="cuda") * HIDDEN ** -0.5).half(),
+                (torch.randn((inter, HIDDEN), generator=g, device="cuda") * HIDDEN ** -0.5).half(),
+                (torch.randn((HIDDEN, inter), generator=g, device="cuda") * inter ** -0.5).half()]
+        F.attach_dense(l, *mats, inter)  # the library keeps its own copy
+        del mats
+    torch.cuda.empty_cache()
+    X = make_tokens(steps + warmup, 9300)
+    Hin = make_tokens(steps + warmup, 9400)
+    Y = torch.empty((steps + warmup, HIDDEN), dtype=torch.float32, device="cuda")
+    for i in range(warmup):
+        F.dense_ffn(i % args.dense, X[i], Hin[i], Y[i], stream=stream)
+    torch.cuda.synchronize()
+    F.prof_enable(True)
+    F.prof_reset()
+    t0 = time.perf_counter()
+    for i in range(warmup, steps + warmup):
+        F.dense_ffn(i % args.dense, X[i], Hin[i], Y[i], stream=stream)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    n, tot, mn, mx = F.prof_read("dense")
+    F.prof_enable(False)
+    for l in range(args.dense):
+        F.release_dense(l)
+    layer_bytes = 3 * inter * HIDDEN * 2 + HIDDEN * 4 * 3
+    kern = tot / n * 1e-3 if n else dt
+    return {"layers": args.dense, "inter": inter, "us_per_layer": round(dt * 1e6, 2),
+            "kernel_avg_us": round(kern * 1e6, 2), "bytes_per_layer": layer_bytes,
+            "gbps": round(layer_bytes / kern / 1e9, 1),
+            "frac": round(layer_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +200,8 @@ def main():
                     help="also time batched decode at these token counts ('' to skip)")
     ap.add_argument("--prefill", type=int, default=512,
                     help="also time prefill of this many tokens through 4 resident layers (0 to skip)")
+    ap.add_argument("--dense", type=int, default=3,
+                    help="also time the dense FFN over this many F16 dense layers (0 to skip)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter-collection run: a few layer steps, then plain 256 MiB "
                          "copies (read + write of known size) that calibrate the counters")
@@ -277,6 +318,8 @@ def main():
         result["batched"] = bench_batched(F, torch, layers, args, stream, K)
     if args.prefill:
         result["prefill"] = bench_prefill(F, torch, layers, args, stream, K)
+    if args.dense:
+        result["dense"] = bench_dense(F, torch, args, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.down, args.cpu_seconds, K)
         cb = result["cpu_baseline"]["value"]

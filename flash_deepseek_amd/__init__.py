@@ -14,6 +14,8 @@ for this path, over the C ABI of libfdm.so (include/fdm.h):
   load_layer_weights (MoE part) :1794      attach_layer / upload_layer
   metal_moe_forward             :1604      moe_forward / moe_forward_host
   layer_forward MoE branch      :1878-1922 moe_layer
+  layer_forward dense branch    :1852-1868 dense_ffn (weights: upload_dense /
+                                           attach_dense / load_dense_gguf)
 
 Tensors are torch tensors on the GPU (torch provides device memory and the
 current stream; all compute is the library's own HIP kernels).  Every call
@@ -22,14 +24,15 @@ is asynchronous on torch's current stream unless noted.
 import ctypes
 
 from . import _lib
-from ._lib import (EXPERT_Q4K_BYTES, EXPERT_Q6K_BYTES, HIDDEN, MAX_K, MAX_LAYERS, MAX_TOKENS,
+from ._lib import (DENSE_FFN, EXPERT_Q4K_BYTES, EXPERT_Q6K_BYTES, HIDDEN, MAX_K, MAX_LAYERS, MAX_TOKENS,
                    MOE_FFN, N_EXPERTS, Q4K_BLOCK_SIZE, Q6K_BLOCK_SIZE, QK_K, FdmError)
 
 __all__ = [
     "init", "shutdown", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
     "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
-    "moe_forward_host", "moe_layer", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "moe_forward_host", "moe_layer", "f32_to_f16", "upload_dense", "attach_dense", "load_dense_gguf",
+    "release_dense", "dense_info", "dense_ffn", "DENSE_FFN", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -190,10 +193,52 @@ def moe_prefill(layers, H, T, K, norm_w, idx=None, stream=None):
          ctypes.cast(nw, ctypes.c_void_p) if nw is not None else None, _p(idx), _stream(stream))
 
 
+# ---- dense FFN layers (layer_forward's branch for L < 3) ------------------------------
+def f32_to_f16(src, dst, n=None, stream=None):
+    """(__fp16) cast of f32_to_f16_alloc on the device: fp32 -> F16 bits."""
+    n = src.numel() if n is None else n
+    call("fdm_f32_to_f16", _p(src), _p(dst), n, _stream(stream))
+
+
+def upload_dense(L, gate, up, down):
+    """Copy F16 weights (numpy uint16 or float16 arrays on the host; gate and
+    up [inter][7168], down [7168][inter]) to HBM as dense layer L."""
+    inter = gate.shape[0]
+    call("fdm_dense_upload", L, gate.ctypes.data, up.ctypes.data, down.ctypes.data, inter)
+
+
+def attach_dense(L, gate, up, down, inter):
+    """Copy F16 weights from device memory (the library keeps its own copy)."""
+    call("fdm_dense_attach", L, _p(gate), _p(up), _p(down), inter)
+
+
+def load_dense_gguf(L, gguf):
+    """blk.L.ffn_{gate,up,down}.weight of an open GGUF (see gguf.GGUF),
+    converted to F16 as dequant_tensor_f16.  Returns the intermediate size."""
+    inter = ctypes.c_int()
+    call("fdm_dense_load_gguf", L, gguf.handle, ctypes.byref(inter))
+    return inter.value
+
+
+def release_dense(L):
+    call("fdm_dense_release", L)
+
+
+def dense_info(L):
+    inter = ctypes.c_int()
+    call("fdm_dense_query", L, ctypes.byref(inter))
+    return inter.value
+
+
+def dense_ffn(L, h_post, h_in, hidden, stream=None):
+    """hidden = h_in + W_down . (silu(W_gate . h_post) * (W_up . h_post))."""
+    call("fdm_dense_ffn", L, _p(h_post), _p(h_in), _p(hidden), _stream(stream))
+
+
 # ---- per-kernel GPU timing (HIP events; the moe_prof_t counterpart) --------------------
 PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
           "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER,
-          "batch": _lib.PROF_BATCH, "prefill": _lib.PROF_PREFILL}
+          "batch": _lib.PROF_BATCH, "prefill": _lib.PROF_PREFILL, "dense": _lib.PROF_DENSE}
 
 
 def prof_enable(on=True):

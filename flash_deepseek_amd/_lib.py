@@ -20,7 +20,7 @@ FDM_E_IO = -7
 FDM_E_FORMAT = -8
 
 (PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER, PROF_BATCH,
- PROF_PREFILL) = range(8)
+ PROF_PREFILL, PROF_DENSE) = range(9)
 
 QK_K = 256
 Q4K_BLOCK_SIZE = 144
@@ -31,6 +31,7 @@ N_EXPERTS = 256
 MAX_K = 16
 MAX_LAYERS = 61
 MAX_TOKENS = 512
+DENSE_FFN = 18432
 EXPERT_Q4K_BYTES = 24772608
 EXPERT_Q6K_BYTES = 28557312
 
@@ -56,6 +57,13 @@ SIGNATURES = {
     "fdm_memcpy_d2h": [_vp, _vp, _sz, _vp],
     "fdm_stream_sync": [_vp],
     "fdm_fp16_to_fp32": [_vp, _vp, _sz, _vp],
+    "fdm_f32_to_f16": [_vp, _vp, _sz, _vp],
+    "fdm_dense_upload": [_i, _vp, _vp, _vp, _i],
+    "fdm_dense_attach": [_i, _vp, _vp, _vp, _i],
+    "fdm_dense_load_gguf": [_i, _vp, ctypes.POINTER(_i)],
+    "fdm_dense_release": [_i],
+    "fdm_dense_query": [_i, ctypes.POINTER(_i)],
+    "fdm_dense_ffn": [_i, _vp, _vp, _vp, _vp],
     "fdm_dequant_q4k": [_vp, _vp, _sz, _vp],
     "fdm_dequant_q6k": [_vp, _vp, _sz, _vp],
     "fdm_matvec_q4k": [_vp, _vp, _vp, _u32, _u32, _vp],

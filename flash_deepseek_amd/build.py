@@ -27,6 +27,7 @@ SOURCES = [
     "batched_kernels.hip",
     "prefill_kernels.hip",
     "synth_kernels.hip",
+    "dense_kernels.hip",
     "gguf_host.hip",
     "capi.hip",
 ]

@@ -76,6 +76,7 @@ struct Workspace {
   float* stage_y = nullptr;   //                   moe_out
   int* stage_idx = nullptr;   //                   exp_idx
   float* stage_w = nullptr;   //                   exp_w
+  float* dense_act = nullptr; // dense FFN activations [kDenseMaxFfn]
 };
 
 struct Layer {
@@ -89,6 +90,13 @@ struct Layer {
   const float* Wg = nullptr;
   const float* bias = nullptr;
   const uint8_t* shared = nullptr;
+};
+
+// A dense FFN layer: library-owned F16 weights (gate, up [inter][7168],
+// down [7168][inter]), as dequant_tensor_f16 leaves them.
+struct DenseLayer {
+  uint16_t *gate = nullptr, *up = nullptr, *down = nullptr;
+  int inter = 0;  // 0: not resident
 };
 
 // Event pairs recorded around kernel launches when profiling is on.
@@ -109,6 +117,7 @@ struct State {
   int device = -1;
   Workspace ws;
   Layer layers[FDM_MAX_LAYERS];
+  DenseLayer dense[FDM_MAX_LAYERS];
 };
 
 State g;
@@ -143,7 +152,7 @@ void free_workspace() {
                   w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w,
                   w.layer_cnt, w.layer_flags, w.layer_tagged, w.b_seg, w.b_pair_tok,
                   w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act, w.b_act_xd, w.b_eo,
-                  w.p_hpost, w.p_xb, w.p_actb};
+                  w.p_hpost, w.p_xb, w.p_actb, w.dense_act};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -177,6 +186,44 @@ int alloc_workspace() {
   FDM_HIP(hipMalloc(&w.stage_y, FDM_HIDDEN * sizeof(float)));
   FDM_HIP(hipMalloc(&w.stage_idx, FDM_MAX_K * sizeof(int)));
   FDM_HIP(hipMalloc(&w.stage_w, FDM_MAX_K * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.dense_act, kDenseMaxFfn * sizeof(float)));
+  return FDM_OK;
+}
+
+void release_dense(DenseLayer& d) {
+  for (uint16_t* p : {d.gate, d.up, d.down})
+    if (p) (void)hipFree(p);
+  d = DenseLayer();
+}
+
+// Buffers of a dense layer under construction; freed unless committed.
+struct DenseBuffers {
+  uint16_t* m[3] = {};  // gate, up, down
+  ~DenseBuffers() {
+    for (uint16_t* p : m)
+      if (p) (void)hipFree(p);
+  }
+  int alloc(int inter, int L) {
+    const size_t n = (size_t)inter * FDM_HIDDEN * sizeof(uint16_t);
+    for (uint16_t*& p : m)
+      if (hipMalloc(&p, n) != hipSuccess) return fail(FDM_E_NOMEM, "cannot allocate 3 x %zu bytes for dense layer %d", n, L);
+    return FDM_OK;
+  }
+  void commit(int L, int inter) {
+    release_dense(g.dense[L]);
+    g.dense[L].gate = m[0];
+    g.dense[L].up = m[1];
+    g.dense[L].down = m[2];
+    g.dense[L].inter = inter;
+    m[0] = m[1] = m[2] = nullptr;
+  }
+};
+
+int check_dense(int L, int inter) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (inter < 512 || inter > kDenseMaxFfn || inter % 512)
+    return fail(FDM_E_INVAL, "dense inter dim %d: must be a multiple of 512 in [512, %d]", inter, kDenseMaxFfn);
   return FDM_OK;
 }
 
@@ -540,6 +587,7 @@ int fdm_shutdown(void) {
   if (!g.ready) return FDM_OK;
   (void)hipDeviceSynchronize();
   for (auto& L : g.layers) release_layer(L);
+  for (auto& d : g.dense) release_dense(d);
   free_workspace();
   for (int i = 0; i < g.prof.created; ++i) {
     (void)hipEventDestroy(g.prof.start[i]);
@@ -1283,6 +1331,142 @@ int fdm_prof_read(int phase, int* count, double* total_ms, double* min_ms, doubl
 }
 
 // ---- synthetic data ------------------------------------------------------------------
+// ---- dense FFN layers ---------------------------------------------------------------
+int fdm_f32_to_f16(const float* d_src, uint16_t* d_dst, size_t n, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (!d_src || !d_dst) return fail(FDM_E_INVAL, "null pointer");
+  if (n == 0) return FDM_OK;
+  FDM_HIP(launch_to_f16(d_src, kGgmlF32, d_dst, n, static_cast<hipStream_t>(stream)));
+  return FDM_OK;
+}
+
+static int dense_copy_in(int L, const uint16_t* gate, const uint16_t* up, const uint16_t* down, int inter,
+                         hipMemcpyKind kind) {
+  if (int rc = check_dense(L, inter)) return rc;
+  if (!gate || !up || !down) return fail(FDM_E_INVAL, "null weight pointer");
+  DenseBuffers b;
+  if (int rc = b.alloc(inter, L)) return rc;
+  const size_t n = (size_t)inter * FDM_HIDDEN * sizeof(uint16_t);
+  const uint16_t* src[3] = {gate, up, down};
+  for (int i = 0; i < 3; ++i) FDM_HIP(hipMemcpy(b.m[i], src[i], n, kind));
+  FDM_HIP(hipDeviceSynchronize());
+  b.commit(L, inter);
+  return FDM_OK;
+}
+
+int fdm_dense_upload(int L, const uint16_t* h_gate, const uint16_t* h_up, const uint16_t* h_down, int inter) {
+  return dense_copy_in(L, h_gate, h_up, h_down, inter, hipMemcpyHostToDevice);
+}
+
+int fdm_dense_attach(int L, const uint16_t* d_gate, const uint16_t* d_up, const uint16_t* d_down, int inter) {
+  return dense_copy_in(L, d_gate, d_up, d_down, inter, hipMemcpyDeviceToDevice);
+}
+
+int fdm_dense_load_gguf(int L, const fdm_gguf* mh, int* inter_out) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  const GgufManifest* m = gguf_manifest(mh);
+  if (!m) return fail(FDM_E_INVAL, "null manifest");
+  char name[128];
+  snprintf(name, sizeof name, "blk.%d.ffn_gate.weight", L);
+  const GgufTensor* t0 = m->find(name);
+  if (!t0) return fail(FDM_E_FORMAT, "tensor %s not in the GGUF", name);
+  if (t0->n_dims != 2 || t0->dims[0] != FDM_HIDDEN)
+    return fail(FDM_E_FORMAT, "tensor %s: expected [%d, inter]", name, FDM_HIDDEN);
+  const int inter = (int)t0->dims[1];
+  if (int rc = check_dense(L, inter)) return rc;
+  const std::initializer_list<uint32_t> types = {FDM_GGML_F32, FDM_GGML_F16, FDM_GGML_BF16, FDM_GGML_Q4_K,
+                                                 FDM_GGML_Q6_K};
+  const char* which[3] = {"gate", "up", "down"};
+  const GgufTensor* t[3] = {};
+  for (int i = 0; i < 3; ++i) {
+    snprintf(name, sizeof name, "blk.%d.ffn_%s.weight", L, which[i]);
+    if (i < 2) {
+      if (int rc = expect_tensor(*m, name, &t[i], types, {FDM_HIDDEN, (uint64_t)inter})) return rc;
+    } else if (int rc = expect_tensor(*m, name, &t[i], types, {(uint64_t)inter, FDM_HIDDEN})) {
+      return rc;
+    }
+  }
+  DenseBuffers b;
+  if (int rc = b.alloc(inter, L)) return rc;
+  const size_t n = (size_t)inter * FDM_HIDDEN;
+  void *raw = nullptr, *wide = nullptr;  // the tensor's bytes; its fp32 values (Q4_K / Q6_K)
+  struct Free {
+    void** p[2];
+    ~Free() {
+      for (void** q : p)
+        if (*q) (void)hipFree(*q);
+    }
+  } free_{{&raw, &wide}};
+  Uploader up;
+  if (int rc = up.init()) return rc;
+  for (int i = 0; i < 3; ++i) {
+    const GgufTensor& ti = *t[i];
+    if (hipMalloc(&raw, ti.nbytes) != hipSuccess) return fail(FDM_E_NOMEM, "cannot stage %s", which[i]);
+    if (int rc = up.copy(raw, ti.nbytes, [&](void* dst, uint64_t k, uint64_t off) { return m->read(ti, dst, k, off); }))
+      return rc;
+    if (int rc = up.finish()) return rc;
+    // dequant_tensor_f16 (infer.m:530-538): the type's fp32 values, then (__fp16)
+    if (ti.type == FDM_GGML_Q4_K || ti.type == FDM_GGML_Q6_K) {
+      if (hipMalloc(&wide, n * sizeof(float)) != hipSuccess) return fail(FDM_E_NOMEM, "cannot widen %s", which[i]);
+      if (ti.type == FDM_GGML_Q4_K)
+        FDM_HIP(launch_dequant_q4k(static_cast<const uint8_t*>(raw), static_cast<float*>(wide), n / FDM_QK_K, 0));
+      else
+        FDM_HIP(launch_dequant_q6k(static_cast<const uint8_t*>(raw), static_cast<float*>(wide), n / FDM_QK_K, 0));
+      FDM_HIP(launch_to_f16(wide, kGgmlF32, b.m[i], n, 0));
+    } else {
+      FDM_HIP(launch_to_f16(raw, (int)ti.type, b.m[i], n, 0));
+    }
+    FDM_HIP(hipDeviceSynchronize());
+    FDM_HIP(hipFree(raw));
+    raw = nullptr;
+    if (wide) FDM_HIP(hipFree(wide));
+    wide = nullptr;
+  }
+  b.commit(L, inter);
+  if (inter_out) *inter_out = inter;
+  return FDM_OK;
+}
+
+int fdm_dense_release(int L) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  (void)hipDeviceSynchronize();
+  release_dense(g.dense[L]);
+  return FDM_OK;
+}
+
+int fdm_dense_query(int L, int* inter) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (!g.dense[L].inter) return fail(FDM_E_STATE, "dense layer %d not resident", L);
+  if (inter) *inter = g.dense[L].inter;
+  return FDM_OK;
+}
+
+int fdm_dense_ffn(int L, const float* d_h_post, const float* d_h_in, float* d_hidden, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  const DenseLayer& d = g.dense[L];
+  if (!d.inter) return fail(FDM_E_STATE, "dense layer %d not resident", L);
+  if (!d_h_post || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(d_h_post, 16)) return fail(FDM_E_INVAL, "h_post must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  ProfScope prof(FDM_PROF_DENSE, s);
+  DenseArgs a;
+  a.gate = d.gate;
+  a.up = d.up;
+  a.down = d.down;
+  a.x = d_h_post;
+  a.h_in = d_h_in;
+  a.act = g.ws.dense_act;
+  a.out = d_hidden;
+  a.inter = d.inter;
+  a.n_cus = g_num_cus;
+  FDM_HIP(launch_dense_ffn(a, s));
+  return FDM_OK;
+}
+
 int fdm_synth_q4k(void* d_dst, size_t n_blocks, uint64_t seed, void* stream) {
   if (int rc = check_ready()) return rc;
   if (!d_dst || !aligned(d_dst, 8)) return fail(FDM_E_INVAL, "destination must be 8-byte aligned");

@@ -171,6 +171,22 @@ hipError_t launch_prefill_experts(const PrefillArgs& p, bool pair, hipStream_t s
 // x [n] fp32 -> its bf16 pair: hi at xb[i], lo at xb[n + i]
 hipError_t launch_bf16_pair(const float* x, __bf16* xb, size_t n, hipStream_t s);
 
+// dense_kernels.hip: the dense FFN of the first layers (F16 weights)
+constexpr int kDenseMaxFfn = 18432;  // DENSE_INTERMEDIATE (infer.m:59): the down kernel's LDS bound
+constexpr int kGgmlF32 = 0, kGgmlF16 = 1, kGgmlBF16 = 30;  // ggml type ids of k_to_f16's inputs
+struct DenseArgs {
+  const uint16_t *gate, *up, *down;  // F16 row-major: [inter][7168] x 2, [7168][inter]
+  const float* x;                    // h_post [7168]
+  const float* h_in;                 // residual [7168] or null
+  float* act;                        // workspace [inter]
+  float* out;                        // [7168]
+  int inter;                         // multiple of 512, <= kDenseMaxFfn
+  int n_cus;
+};
+hipError_t launch_dense_ffn(const DenseArgs& a, hipStream_t s);
+// n elements of ggml type F32 / BF16 / F16 -> F16 bits (round to nearest even)
+hipError_t launch_to_f16(const void* src, int type, uint16_t* dst, size_t n, hipStream_t s);
+
 // synth_kernels.hip
 hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);
 hipError_t launch_synth_q6k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);

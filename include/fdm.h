@@ -83,6 +83,9 @@ int fdm_stream_sync(void *stream);
  * Bit-exact with quant.c read as C with FP_CONTRACT off: every product and
  * difference rounds separately.  n must be a multiple of 256. */
 int fdm_fp16_to_fp32(const uint16_t *d_src, float *d_dst, size_t n, void *stream);
+/* the reverse, for the dense weights: (__fp16)x as f32_to_f16_alloc
+ * (infer.m:521-528), round to nearest even, subnormals kept, NaN quieted. */
+int fdm_f32_to_f16(const float *d_src, uint16_t *d_dst, size_t n, void *stream);
 int fdm_dequant_q4k(const void *d_src, float *d_dst, size_t n, void *stream);
 int fdm_dequant_q6k(const void *d_src, float *d_dst, size_t n, void *stream);
 
@@ -280,6 +283,33 @@ int fdm_rms_norm(const float *d_x, const float *d_w, float *d_o, int T, int d, v
 int fdm_moe_prefill(const int *layers, int n_layers, float *d_H, int T, int K,
                     const float *const *d_norm_w, int *d_idx, void *stream);
 
+/* ---- dense FFN layers (the layers before the first MoE layer, L < 3 in
+ * R1): replaces the dense branch of layer_forward (infer.m:1852-1868),
+ *   hidden = h_in + W_down . (silu(W_gate . h_post) * (W_up . h_post)),
+ * with F16 weights and fp32 activations and accumulation as mv_f16
+ * (infer.m:459-513).  The weights are held as dequant_tensor_f16 leaves
+ * them (infer.m:530-538, 1786-1792): row-major F16, gate and up
+ * [inter][7168], down [7168][inter]; inter = DENSE_INTERMEDIATE (18432) in
+ * R1, any multiple of 512 up to it is accepted.  The library keeps its own
+ * copy of the weights (upload: from host, attach: from device; both
+ * synchronous, the caller's buffers may be freed afterwards).
+ * fdm_dense_load_gguf reads blk.L.ffn_{gate,up,down}.weight (F32, F16,
+ * BF16, Q4_K or Q6_K, as dequant_tensor_full, infer.m:314-355), widens to
+ * fp32 and rounds to F16 on the device, bit-exact with the reference's
+ * (__fp16) cast; *inter receives the intermediate size (may be NULL).
+ * fdm_dense_ffn: d_h_post 16-byte aligned, d_h_in may be NULL (no residual),
+ * d_hidden must not alias d_h_post; calls on one device must not overlap
+ * (they share the activation workspace). */
+#define FDM_DENSE_FFN 18432
+int fdm_dense_upload(int L, const uint16_t *h_gate, const uint16_t *h_up, const uint16_t *h_down,
+                     int inter);
+int fdm_dense_attach(int L, const uint16_t *d_gate, const uint16_t *d_up, const uint16_t *d_down,
+                     int inter);
+int fdm_dense_load_gguf(int L, const fdm_gguf *m, int *inter);
+int fdm_dense_release(int L);
+int fdm_dense_query(int L, int *inter);
+int fdm_dense_ffn(int L, const float *d_h_post, const float *d_h_in, float *d_hidden, void *stream);
+
 /* ---- per-kernel GPU timing: replaces the host-clock moe_prof_t ring
  * (infer.m:177-261) with HIP events recorded on the launch stream around
  * every kernel of the entry points above.  fdm_prof_read synchronises on
@@ -293,7 +323,8 @@ int fdm_moe_prefill(const int *layers, int n_layers, float *d_H, int T, int K,
 #define FDM_PROF_LAYER 5    /* fdm_moe_layer: the whole layer, 1 launch */
 #define FDM_PROF_BATCH 6    /* fdm_moe_forward_batched: the whole step  */
 #define FDM_PROF_PREFILL 7  /* fdm_moe_prefill: all layers              */
-#define FDM_PROF_PHASES 8
+#define FDM_PROF_DENSE 8    /* fdm_dense_ffn: both launches             */
+#define FDM_PROF_PHASES 9
 int fdm_prof_enable(int on);
 int fdm_prof_reset(void);
 int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);

@@ -160,6 +160,74 @@ void orc_expert_ffn(const void *blob, int down_is_q6, const float *x, float *out
     free(o);
 }
 
+/* (__fp16)x as f32_to_f16_alloc (infer.m:521-528) does it on the
+ * reference's AArch64 host (FCVT with the default FPCR): IEEE round to
+ * nearest even, subnormal halves kept, overflow to infinity, NaN quieted
+ * with the top 9 payload bits kept.  Computed in double: x is scaled by the
+ * half quantum of its binade (an exact power-of-two scaling), rounded to an
+ * integer by nearbyint in the default round-to-nearest-even mode, and the
+ * result encoded. */
+uint16_t orc_fp32_to_fp16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, 4);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    if (isnan(f)) return (uint16_t)(sign | 0x7E00u | ((bits >> 13) & 0x1FFu));
+    const double a = fabs((double)f);
+    if (a >= 65520.0) return (uint16_t)(sign | 0x7C00u); /* rounds to 2^16 or beyond */
+    if (a == 0.0) return sign;
+    int e;
+    (void)frexp(a, &e);                          /* a = m 2^e, m in [0.5, 1) */
+    const int qexp = (e - 11 > -24) ? e - 11 : -24; /* 11 significant bits, or subnormal */
+    const double n = nearbyint(ldexp(a, -qexp));  /* integer count of quanta */
+    const double v = ldexp(n, qexp);
+    if (v < ldexp(1.0, -14)) return (uint16_t)(sign | (uint16_t)n); /* subnormal (or 0) */
+    int e2;
+    const double m2 = frexp(v, &e2);              /* v = m2 2^e2 */
+    const unsigned mant = (unsigned)((m2 * 2.0 - 1.0) * 1024.0);
+    return (uint16_t)(sign | (uint16_t)((unsigned)(e2 - 1 + 15) << 10) | mant);
+}
+
+void orc_fp32_to_fp16_array(const float *src, uint16_t *dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_fp32_to_fp16(src[i]);
+}
+
+/* Double-precision matvec over F16 rows (internal). */
+static void matvec_f16_d(const uint16_t *W, const double *x, double *y, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *w = W + (size_t)r * cols;
+        double acc = 0.0;
+        for (int c = 0; c < cols; ++c) acc += (double)orc_fp16_to_fp32(w[c]) * x[c];
+        y[r] = acc;
+    }
+}
+
+/* infer.m:1852-1868 (the dense branch of layer_forward): g = W_gate.h_post,
+ * u = W_up.h_post (mv_f16, infer.m:459-513: F16 weights widened to fp32),
+ * act = silu(g) * u (infer.m:378-383), out = h_in + W_down.act.  Gate and up
+ * are [inter][7168], down [7168][inter], row-major F16.  Accumulated in
+ * double: the truth the kernels are held to.  h_in may be NULL (0). */
+void orc_dense_ffn(const uint16_t *gate, const uint16_t *up, const uint16_t *down, int inter,
+                   const float *h_post, const float *h_in, float *out, float *act_out) {
+    const int H = ORC_HIDDEN;
+    double *x = (double *)malloc(sizeof(double) * H);
+    double *g = (double *)malloc(sizeof(double) * inter);
+    double *u = (double *)malloc(sizeof(double) * inter);
+    double *o = (double *)malloc(sizeof(double) * H);
+    for (int i = 0; i < H; ++i) x[i] = h_post[i];
+    matvec_f16_d(gate, x, g, inter, H);
+    matvec_f16_d(up, x, u, inter, H);
+    for (int i = 0; i < inter; ++i) {
+        g[i] = g[i] / (1.0 + exp(-g[i])) * u[i];
+        if (act_out) act_out[i] = (float)g[i];
+    }
+    matvec_f16_d(down, g, o, H, inter);
+    for (int i = 0; i < H; ++i) out[i] = (float)((h_in ? (double)h_in[i] : 0.0) + o[i]);
+    free(x);
+    free(g);
+    free(u);
+    free(o);
+}
+
 /* ---------------------------------------------------------------------- */
 /* Router logits, canonical order.  For output row e, 256 partial sums are
  * formed: partial t accumulates, with one fmaf per element, the float4

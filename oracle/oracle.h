@@ -67,6 +67,12 @@ void orc_matvec_q6k_f32(const void *W, const float *x, float *y, int rows, int c
 /* One SwiGLU expert from a packed blob [gate Q4_K | up Q4_K | down Q4_K/Q6_K]
  * (infer.m:1069-1091).  Computed in double from the bit-exact dequantised
  * weights, rounded to float at the end.  gate_out/up_out/act_out may be NULL. */
+/* (__fp16)x of f32_to_f16_alloc (infer.m:521-528) and the dense FFN of
+ * layer_forward (infer.m:1852-1868), see moe_ref.c. */
+uint16_t orc_fp32_to_fp16(float f);
+void orc_fp32_to_fp16_array(const float *src, uint16_t *dst, size_t n);
+void orc_dense_ffn(const uint16_t *gate, const uint16_t *up, const uint16_t *down, int inter,
+                   const float *h_post, const float *h_in, float *out, float *act_out);
 void orc_expert_ffn(const void *blob, int down_is_q6, const float *x, float *out,
                     float *gate_out, float *up_out, float *act_out);
 

@@ -52,6 +52,9 @@ def _load():
         "orc_matvec_q4k_f32": (None, [_vp, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_matvec_q6k_f32": (None, [_vp, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_expert_ffn": (None, [_vp, ctypes.c_int, _f32p, _f32p, _vp, _vp, _vp]),
+        "orc_fp32_to_fp16": (ctypes.c_uint16, [ctypes.c_float]),
+        "orc_fp32_to_fp16_array": (None, [_f32p, _vp, ctypes.c_size_t]),
+        "orc_dense_ffn": (None, [_vp, _vp, _vp, ctypes.c_int, _f32p, _vp, _f32p, _vp]),
         "orc_router_logits": (None, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_route_ex": (None, [_f32p, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 ctypes.c_int, ctypes.c_float, _i32p, _f32p]),
@@ -153,6 +156,29 @@ def expert_ffn(blob, down_is_q6, x, with_intermediates=False):
         return out, g, u, a
     L.orc_expert_ffn(_ptr(blob), int(down_is_q6), x, out, None, None, None)
     return out
+
+
+def fp32_to_fp16(x):
+    """(__fp16)x elementwise (infer.m:521-528): uint16 bits."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    L.orc_fp32_to_fp16_array(x.ravel(), _ptr(out), x.size)
+    return out
+
+
+def dense_ffn(gate, up, down, h_post, h_in=None, with_act=False):
+    """Dense branch of layer_forward (infer.m:1852-1868) on F16 bit arrays:
+    gate, up [inter][7168], down [7168][inter]; float64 accumulation."""
+    gate, up, down = (np.ascontiguousarray(a).view(np.uint16) for a in (gate, up, down))
+    inter = gate.shape[0]
+    assert gate.shape == (inter, HIDDEN) and up.shape == gate.shape and down.shape == (HIDDEN, inter)
+    h_post = np.ascontiguousarray(h_post, dtype=np.float32)
+    hp = None if h_in is None else _ptr(np.ascontiguousarray(h_in, dtype=np.float32))
+    out = np.empty(HIDDEN, dtype=np.float32)
+    act = np.empty(inter, dtype=np.float32) if with_act else None
+    L.orc_dense_ffn(_ptr(gate), _ptr(up), _ptr(down), inter, h_post, hp, out,
+                    None if act is None else _ptr(act))
+    return (out, act) if with_act else out
 
 
 # ---- router -------------------------------------------------------------------
