@@ -140,22 +140,37 @@ __device__ __forceinline__ bool prefill_item(const PrefillArgs& p, int y, PItem&
 
 // ---- rms_norm: h_post = x * (1 / sqrt(sum x^2 / d + 1e-6)) * w ---------------------------
 // One workgroup per token.  The sum of squares is taken in index order by
-// one thread, as the reference's loop (infer.m:369-374), so h_post -- and
-// with it the routing -- is bit-exact; sqrt and division are IEEE.  Also
+// one thread with one fused multiply-add per element, as the reference's
+// loop compiles (infer.m:369-374: clang contracts `ss += x[i]*x[i]`), so
+// h_post -- and with it the routing -- is bit-exact; sqrt and division are
+// IEEE.  Also
 // writes the bf16 pair (hi, lo) of h_post for the expert GEMMs when xb is
 // not null (hi at xb, lo at xb + T*d).
 __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x,
                                                   const float* __restrict__ w, float* __restrict__ o,
                                                   __bf16* __restrict__ xb, int d, float eps) {
 #pragma clang fp contract(off)
-  __shared__ float row[kHidden];
+  __shared__ __attribute__((aligned(16))) float row[kHidden];
   __shared__ float inv_s;
   const float* xr = x + (size_t)blockIdx.x * d;
   for (int i = threadIdx.x; i < d; i += 256) row[i] = xr[i];
   __syncthreads();
   if (threadIdx.x == 0) {
+    // the reference's loop as compiled: ss = fma(x_i, x_i, ss) in index order
+    // (clang contracts `ss += x[i]*x[i]`); one dependent chain, fed 16
+    // values at a time from LDS so the reads run ahead of it
     float ss = 0.0f;
-    for (int i = 0; i < d; ++i) ss += row[i] * row[i];
+    int i = 0;
+#pragma unroll 2
+    for (; i + 16 <= d; i += 16) {
+      const f32x4* r4 = reinterpret_cast<const f32x4*>(row + i);
+      const f32x4 a = r4[0], b = r4[1], c = r4[2], e = r4[3];
+      ss = fmaf(a.x, a.x, ss); ss = fmaf(a.y, a.y, ss); ss = fmaf(a.z, a.z, ss); ss = fmaf(a.w, a.w, ss);
+      ss = fmaf(b.x, b.x, ss); ss = fmaf(b.y, b.y, ss); ss = fmaf(b.z, b.z, ss); ss = fmaf(b.w, b.w, ss);
+      ss = fmaf(c.x, c.x, ss); ss = fmaf(c.y, c.y, ss); ss = fmaf(c.z, c.z, ss); ss = fmaf(c.w, c.w, ss);
+      ss = fmaf(e.x, e.x, ss); ss = fmaf(e.y, e.y, ss); ss = fmaf(e.z, e.z, ss); ss = fmaf(e.w, e.w, ss);
+    }
+    for (; i < d; ++i) ss = fmaf(row[i], row[i], ss);
     inv_s = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)d) + eps));
   }
   __syncthreads();

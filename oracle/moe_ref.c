@@ -65,8 +65,12 @@ void orc_silu_mul(const float *g, const float *u, float *o, int d) {
 
 /* infer.m:369-374: inv = 1/sqrt(ss/d + eps); o = x * inv * w. */
 void orc_rms_norm(const float *x, const float *w, float *o, int d) {
+    /* `ss += x[i]*x[i]` is one statement: the reference's compiler (clang,
+     * -O3 without fast-math, Makefile:2) contracts it to a fused multiply-add
+     * (its default -ffp-contract=on), still in index order; the other
+     * expressions have no multiply feeding an add. */
     float ss = 0.0f;
-    for (int i = 0; i < d; ++i) ss += x[i] * x[i];
+    for (int i = 0; i < d; ++i) ss = fmaf(x[i], x[i], ss);
     const float inv = 1.0f / sqrtf(ss / (float)d + ORC_RMS_EPS);
     for (int i = 0; i < d; ++i) o[i] = w ? x[i] * inv * w[i] : x[i] * inv;
 }
