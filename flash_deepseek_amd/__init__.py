@@ -14,6 +14,7 @@ for this path, over the C ABI of libfdm.so (include/fdm.h):
   load_layer_weights (MoE part) :1794      attach_layer / upload_layer
   metal_moe_forward             :1604      moe_forward / moe_forward_host
   layer_forward MoE branch      :1878-1922 moe_layer
+  expert streaming (flash)      :1478-1602 stream_layer / moe_layer_streamed
   layer_forward dense branch    :1852-1868 dense_ffn (weights: upload_dense /
                                            attach_dense / load_dense_gguf)
 
@@ -32,7 +33,8 @@ __all__ = [
     "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
     "moe_forward_host", "moe_layer", "f32_to_f16", "upload_dense", "attach_dense", "load_dense_gguf",
-    "release_dense", "dense_info", "dense_ffn", "DENSE_FFN", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "release_dense", "dense_info", "dense_ffn", "DENSE_FFN", "stream_layer", "moe_layer_streamed",
+    "stream_stats", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -191,6 +193,28 @@ def moe_prefill(layers, H, T, K, norm_w, idx=None, stream=None):
     nw = (ctypes.c_void_p * n)(*[_p(w) for w in norm_w]) if norm_w is not None else None
     call("fdm_moe_prefill", ctypes.cast(lay, ctypes.c_void_p),  n, _p(H), T, K,
          ctypes.cast(nw, ctypes.c_void_p) if nw is not None else None, _p(idx), _stream(stream))
+
+
+# ---- streamed layers (experts read from the packed layer file on demand) --------------
+def stream_layer(L, layer_file, expert_size, Wg, bias, shared=None, n_cache=N_EXPERTS, n_threads=0,
+                 n_experts=N_EXPERTS):
+    """Open layer L as a streamed layer: routed experts stay in layer_file
+    (repack_experts.c layout) and are read into an HBM cache of n_cache
+    slots on demand; Wg / bias stay caller-owned device tensors."""
+    call("fdm_layer_stream_open", L, str(layer_file).encode(), expert_size, n_experts, _p(Wg), _p(bias),
+         _p(shared), n_cache, n_threads)
+
+
+def moe_layer_streamed(L, h_post, h_in, K, hidden, idx=None, w=None, stream=None):
+    """moe_layer for a streamed layer (reads the routed experts it lacks)."""
+    call("fdm_moe_layer_streamed", L, _p(h_post), _p(h_in), K, _p(hidden), _p(idx), _p(w), _stream(stream))
+
+
+def stream_stats(L):
+    """(hits, misses, bytes read) of a streamed layer since it was opened."""
+    h, m, b = ctypes.c_uint64(), ctypes.c_uint64(), ctypes.c_uint64()
+    call("fdm_stream_stats", L, ctypes.byref(h), ctypes.byref(m), ctypes.byref(b))
+    return h.value, m.value, b.value
 
 
 # ---- dense FFN layers (layer_forward's branch for L < 3) ------------------------------

@@ -64,6 +64,9 @@ SIGNATURES = {
     "fdm_dense_release": [_i],
     "fdm_dense_query": [_i, ctypes.POINTER(_i)],
     "fdm_dense_ffn": [_i, _vp, _vp, _vp, _vp],
+    "fdm_layer_stream_open": [_i, ctypes.c_char_p, _sz, _i, _vp, _vp, _vp, _i, _i],
+    "fdm_moe_layer_streamed": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
+    "fdm_stream_stats": [_i, ctypes.POINTER(_u64), ctypes.POINTER(_u64), ctypes.POINTER(_u64)],
     "fdm_dequant_q4k": [_vp, _vp, _sz, _vp],
     "fdm_dequant_q6k": [_vp, _vp, _sz, _vp],
     "fdm_matvec_q4k": [_vp, _vp, _vp, _u32, _u32, _vp],

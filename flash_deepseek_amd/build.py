@@ -28,6 +28,7 @@ SOURCES = [
     "prefill_kernels.hip",
     "synth_kernels.hip",
     "dense_kernels.hip",
+    "expert_stream.hip",
     "gguf_host.hip",
     "capi.hip",
 ]

@@ -10,6 +10,7 @@
 #include <unistd.h>
 
 #include <initializer_list>
+#include <memory>
 
 #include "../../include/fdm.h"
 #include "fdm_internal.h"
@@ -99,6 +100,21 @@ struct DenseLayer {
   int inter = 0;  // 0: not resident
 };
 
+// A streamed layer: router, bias (caller-owned) and shared expert (packed,
+// library-owned) resident; the routed experts read from the layer file into
+// an HBM cache on demand.
+struct StreamedLayer {
+  ExpertStream es;
+  const float* Wg = nullptr;
+  const float* bias = nullptr;
+  uint8_t* shared = nullptr;
+  size_t expert_size = 0;
+  bool q6 = false;
+  ~StreamedLayer() {
+    if (shared) (void)hipFree(shared);
+  }
+};
+
 // Event pairs recorded around kernel launches when profiling is on.
 struct Prof {
   static constexpr int kPool = 8192;
@@ -118,6 +134,9 @@ struct State {
   Workspace ws;
   Layer layers[FDM_MAX_LAYERS];
   DenseLayer dense[FDM_MAX_LAYERS];
+  std::unique_ptr<StreamedLayer> streamed[FDM_MAX_LAYERS];
+  int* stream_ids_h = nullptr;    // pinned host: the routed ids of a streamed call
+  int* stream_slots_h = nullptr;  // pinned host: their cache slots
 };
 
 State g;
@@ -531,6 +550,7 @@ int commit_layer(int L, LayerBuffers& b, size_t es, bool q6) {
                                      static_cast<const uint8_t*>(b.shared), es, q6, L, &rel, &rel_shared))
     return rc;
   release_layer(g.layers[L]);
+  g.streamed[L].reset();
   Layer& y = g.layers[L];
   y.resident = true;
   y.owned = true;
@@ -588,6 +608,11 @@ int fdm_shutdown(void) {
   (void)hipDeviceSynchronize();
   for (auto& L : g.layers) release_layer(L);
   for (auto& d : g.dense) release_dense(d);
+  for (auto& st : g.streamed) st.reset();
+  release_stream_pool();
+  for (int* p : {g.stream_ids_h, g.stream_slots_h})
+    if (p) (void)hipHostFree(p);
+  g.stream_ids_h = g.stream_slots_h = nullptr;
   free_workspace();
   for (int i = 0; i < g.prof.created; ++i) {
     (void)hipEventDestroy(g.prof.start[i]);
@@ -823,6 +848,7 @@ int fdm_layer_attach(int L, const void* d_experts, size_t expert_size, int n_exp
                                      &rel_shared))
     return rc;
   release_layer(g.layers[L]);
+  g.streamed[L].reset();
   Layer& y = g.layers[L];
   y.resident = true;
   y.owned = false;
@@ -878,6 +904,7 @@ int fdm_layer_upload(int L, const void* h_experts, size_t expert_size, int n_exp
   (void)hipFree(de);  // the packed staging copies
   if (ds) (void)hipFree(ds);
   release_layer(g.layers[L]);
+  g.streamed[L].reset();
   Layer& y = g.layers[L];
   y.resident = true;
   y.owned = true;
@@ -984,6 +1011,7 @@ int fdm_layer_release(int L) {
   if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
   (void)hipDeviceSynchronize();
   release_layer(g.layers[L]);
+  g.streamed[L].reset();
   return FDM_OK;
 }
 
@@ -1331,6 +1359,91 @@ int fdm_prof_read(int phase, int* count, double* total_ms, double* min_ms, doubl
 }
 
 // ---- synthetic data ------------------------------------------------------------------
+// ---- streamed layers (experts read from the layer file on demand) -------------------
+int fdm_layer_stream_open(int L, const char* layer_file, size_t expert_size, int n_experts,
+                          const float* d_Wg, const float* d_bias, const void* d_shared, int n_cache,
+                          int n_threads) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (!layer_file || !d_Wg) return fail(FDM_E_INVAL, "null layer file or router weights");
+  if (n_experts != FDM_N_EXPERTS)
+    return fail(FDM_E_INVAL, "n_experts=%d: the router is the R1 256-expert router", n_experts);
+  bool q6 = false;
+  if (int rc = down_type(expert_size, &q6)) return rc;
+  if (n_cache < 1 || n_cache > n_experts) return fail(FDM_E_INVAL, "n_cache=%d: 1 .. n_experts", n_cache);
+  if (n_threads < 0 || n_threads > 64) return fail(FDM_E_INVAL, "n_threads=%d: 0 (default 8) .. 64", n_threads);
+  if (!aligned(d_Wg, 16) || (d_shared && !aligned(d_shared, 16)))
+    return fail(FDM_E_INVAL, "router weights and shared expert must be 16-byte aligned");
+  if (!g.stream_ids_h) {
+    FDM_HIP(hipHostMalloc(reinterpret_cast<void**>(&g.stream_ids_h), FDM_MAX_K * sizeof(int), hipHostMallocDefault));
+    FDM_HIP(hipHostMalloc(reinterpret_cast<void**>(&g.stream_slots_h), FDM_MAX_K * sizeof(int), hipHostMallocDefault));
+  }
+  auto st = std::make_unique<StreamedLayer>();
+  std::string err;
+  if (int rc = st->es.open(layer_file, expert_size, n_experts, n_cache, n_threads ? n_threads : 8, g.device, &err))
+    return fail(rc, "layer %d: %s", L, err.c_str());
+  if (d_shared) {
+    if (hipMalloc(&st->shared, expert_size) != hipSuccess) return fail(FDM_E_NOMEM, "cannot allocate the shared expert");
+    FDM_HIP(hipMemcpy(st->shared, d_shared, expert_size, hipMemcpyDeviceToDevice));
+  }
+  st->Wg = d_Wg;
+  st->bias = d_bias;
+  st->expert_size = expert_size;
+  st->q6 = q6;
+  (void)hipDeviceSynchronize();
+  release_layer(g.layers[L]);
+  g.streamed[L] = std::move(st);
+  return FDM_OK;
+}
+
+int fdm_moe_layer_streamed(int L, const float* d_h_post, const float* d_h_in, int K, float* d_hidden,
+                           int* d_idx, float* d_w, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS || !g.streamed[L]) return fail(FDM_E_STATE, "layer %d is not streamed", L);
+  if (int rc = check_K(K)) return rc;
+  if (!d_h_post || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(d_h_post, 16)) return fail(FDM_E_INVAL, "h_post must be 16-byte aligned");
+  StreamedLayer& y = *g.streamed[L];
+  if (K > y.es.n_cache()) return fail(FDM_E_INVAL, "K=%d exceeds the layer's %d cache slots", K, y.es.n_cache());
+  hipStream_t s = as_stream(stream);
+  Workspace& w = g.ws;
+  // route on the device (infer.m:1881-1883), then the ids to the host
+  FDM_HIP(launch_router_logits(y.Wg, d_h_post, FDM_N_EXPERTS, FDM_HIDDEN, 1, w.logits, s));
+  FDM_HIP(launch_route(w.logits, y.bias, 1, K, w.idx, w.w, s));
+  FDM_HIP(hipMemcpyAsync(g.stream_ids_h, w.idx, K * sizeof(int), hipMemcpyDeviceToHost, s));
+  FDM_HIP(hipStreamSynchronize(s));
+  // the selected experts into the cache (parallel pread, infer.m:1577-1602)
+  std::string err;
+  if (int rc = y.es.fetch(g.stream_ids_h, K, g.stream_slots_h, &err)) return fail(rc, "layer %d: %s", L, err.c_str());
+  FDM_HIP(hipMemcpyAsync(w.stage_idx, g.stream_slots_h, K * sizeof(int), hipMemcpyHostToDevice, s));
+  SlotTable t;
+  t.experts = y.es.cache();
+  t.expert_size = y.expert_size;
+  t.n_experts = y.es.n_cache();
+  t.shared = y.shared;
+  t.idx = w.stage_idx;
+  t.w = w.w;
+  t.K = K;
+  t.n_slots = K + (y.shared ? 1 : 0);
+  t.rel = false;
+  FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, w.xd, s));
+  FDM_HIP(launch_gateup(t, w.xd, w.act, w.act_xd, w.gu_count, s));
+  FDM_HIP(launch_down_combine(t, y.q6, w.act_xd, d_h_in, d_hidden, nullptr, w.eo, w.dn_count, s));
+  if (d_idx) FDM_HIP(hipMemcpyAsync(d_idx, w.idx, K * sizeof(int), hipMemcpyDeviceToDevice, s));
+  if (d_w) FDM_HIP(hipMemcpyAsync(d_w, w.w, K * sizeof(float), hipMemcpyDeviceToDevice, s));
+  return FDM_OK;
+}
+
+int fdm_stream_stats(int L, uint64_t* hits, uint64_t* misses, uint64_t* bytes_read) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS || !g.streamed[L]) return fail(FDM_E_STATE, "layer %d is not streamed", L);
+  const ExpertStream& es = g.streamed[L]->es;
+  if (hits) *hits = es.hits();
+  if (misses) *misses = es.misses();
+  if (bytes_read) *bytes_read = es.bytes_read();
+  return FDM_OK;
+}
+
 // ---- dense FFN layers ---------------------------------------------------------------
 int fdm_f32_to_f16(const float* d_src, uint16_t* d_dst, size_t n, void* stream) {
   if (int rc = check_ready()) return rc;

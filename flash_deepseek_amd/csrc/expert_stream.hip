@@ -1,0 +1,217 @@
+// expert_stream.hip -- routed experts read from the packed layer file on
+// demand, for models whose experts exceed HBM (the reference's expert
+// streaming: parallel pread of the K selected experts per token,
+// infer.m:1478-1602, N_PREAD_CHUNKS at 1502; the layer files of
+// repack_experts.c, expert e at e * expert_size).
+//
+// Each streamed layer keeps an LRU cache of n_cache expert blobs in HBM.  A
+// fetch of the K routed experts of one token reads the misses with a pool of
+// host threads: every thread preads 4 MB chunks into its own two pinned
+// buffers and queues each chunk's host-to-device copy on its own stream, so
+// file reads overlap PCIe copies.  fetch() returns once every copy has
+// landed.  The blobs stay in the packed layout; the expert kernels read it
+// as they read caller blobs.
+#include <errno.h>
+#include <string.h>
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <atomic>
+#include <thread>
+
+#include "../../include/fdm.h"
+#include "fdm_internal.h"
+
+namespace fdm {
+
+namespace {
+
+constexpr size_t kStreamChunk = 4u << 20;
+
+// Pinned staging and copy streams shared by every streamed layer.
+struct ReadPool {
+  struct Worker {
+    hipStream_t s = nullptr;
+    void* buf[2] = {};
+    hipEvent_t ev[2] = {};
+  };
+  std::vector<Worker> w;
+  int device = -1;
+
+  hipError_t init(int n, int dev) {
+    if (!w.empty()) return hipSuccess;
+    device = dev;
+    w.resize(n);
+    for (Worker& k : w) {
+      if (hipError_t e = hipStreamCreateWithFlags(&k.s, hipStreamNonBlocking)) return e;
+      for (int b = 0; b < 2; ++b) {
+        if (hipError_t e = hipHostMalloc(&k.buf[b], kStreamChunk, hipHostMallocDefault)) return e;
+        if (hipError_t e = hipEventCreateWithFlags(&k.ev[b], hipEventDisableTiming)) return e;
+      }
+    }
+    return hipSuccess;
+  }
+  void release() {
+    for (Worker& k : w) {
+      if (k.s) (void)hipStreamSynchronize(k.s);
+      for (int b = 0; b < 2; ++b) {
+        if (k.ev[b]) (void)hipEventDestroy(k.ev[b]);
+        if (k.buf[b]) (void)hipHostFree(k.buf[b]);
+      }
+      if (k.s) (void)hipStreamDestroy(k.s);
+    }
+    w.clear();
+  }
+};
+
+ReadPool g_pool;
+
+}  // namespace
+
+ExpertStream::~ExpertStream() {
+  if (fd_ >= 0) close(fd_);
+  if (cache_) (void)hipFree(cache_);
+}
+
+int ExpertStream::open(const char* path, size_t expert_size, int n_experts, int n_cache, int n_threads,
+                       int device, std::string* err) {
+  es_ = expert_size;
+  n_experts_ = n_experts;
+  n_cache_ = n_cache;
+  n_threads_ = n_threads;
+  fd_ = ::open(path, O_RDONLY | O_CLOEXEC);
+  if (fd_ < 0) {
+    *err = std::string("cannot open ") + path + ": " + strerror(errno);
+    return FDM_E_IO;
+  }
+  struct stat st;
+  if (fstat(fd_, &st) != 0 || (uint64_t)st.st_size < (uint64_t)n_experts * es_) {
+    *err = std::string(path) + " is shorter than n_experts x expert_size";
+    return FDM_E_FORMAT;
+  }
+  if (hipMalloc(&cache_, (size_t)n_cache * es_) != hipSuccess) {
+    *err = "cannot allocate the expert cache";
+    return FDM_E_NOMEM;
+  }
+  if (g_pool.init(std::max(n_threads, 1), device) != hipSuccess) {
+    *err = "cannot allocate the pinned read buffers";
+    return FDM_E_NOMEM;
+  }
+  slot_of_.assign(n_experts, -1);
+  expert_in_.assign(n_cache, -1);
+  last_use_.assign(n_cache, 0);
+  return FDM_OK;
+}
+
+int ExpertStream::fetch(const int* ids, int K, int* slots, std::string* err) {
+  if (K > n_cache_) {
+    *err = "K exceeds the expert cache";
+    return FDM_E_INVAL;
+  }
+  ++tick_;
+  std::vector<char> held(n_cache_, 0);  // slots this token uses
+  std::vector<std::pair<int, int>> misses;  // (expert, slot)
+  for (int k = 0; k < K; ++k) {
+    const int e = ids[k];
+    if (e < 0 || e >= n_experts_) {
+      *err = "routed expert id out of range";
+      return FDM_E_INVAL;
+    }
+    if (slot_of_[e] >= 0) {
+      slots[k] = slot_of_[e];
+      if (!held[slots[k]]) ++hits_;
+      held[slots[k]] = 1;
+      last_use_[slots[k]] = tick_;
+    } else {
+      slots[k] = -1;
+    }
+  }
+  for (int k = 0; k < K; ++k) {
+    if (slots[k] >= 0) continue;
+    const int e = ids[k];
+    if (slot_of_[e] >= 0) {  // a repeated id of this token, placed just now
+      slots[k] = slot_of_[e];
+      continue;
+    }
+    int v = -1;  // least recently used slot that this token does not hold
+    for (int c = 0; c < n_cache_; ++c)
+      if (!held[c] && (v < 0 || last_use_[c] < last_use_[v])) v = c;
+    if (expert_in_[v] >= 0) slot_of_[expert_in_[v]] = -1;
+    expert_in_[v] = e;
+    slot_of_[e] = v;
+    last_use_[v] = tick_;
+    held[v] = 1;
+    slots[k] = v;
+    misses.emplace_back(e, v);
+    ++misses_;
+  }
+  if (misses.empty()) return FDM_OK;
+  const size_t per = (es_ + kStreamChunk - 1) / kStreamChunk;
+  const size_t n_jobs = misses.size() * per;
+  std::atomic<size_t> next{0};
+  std::atomic<int> rc{FDM_OK};
+  std::atomic<int> io_errno{0};
+  auto work = [&](int t) {
+    if (hipSetDevice(g_pool.device) != hipSuccess) {
+      rc = FDM_E_HIP;
+      return;
+    }
+    ReadPool::Worker& wk = g_pool.w[t];
+    bool used[2] = {false, false};
+    for (int j = 0;; ++j) {
+      const size_t i = next.fetch_add(1);
+      if (i >= n_jobs || rc.load() != FDM_OK) break;
+      const auto& m = misses[i / per];
+      const size_t off = (i % per) * kStreamChunk;
+      const size_t len = std::min(kStreamChunk, es_ - off);
+      const int b = j & 1;
+      if (used[b] && hipEventSynchronize(wk.ev[b]) != hipSuccess) {
+        rc = FDM_E_HIP;
+        break;
+      }
+      uint8_t* dst = static_cast<uint8_t*>(wk.buf[b]);
+      size_t got = 0;
+      const off_t at = (off_t)((uint64_t)m.first * es_ + off);
+      while (got < len) {
+        const ssize_t r = pread(fd_, dst + got, len - got, at + (off_t)got);
+        if (r <= 0) {
+          io_errno = r < 0 ? errno : EIO;
+          rc = FDM_E_IO;
+          break;
+        }
+        got += (size_t)r;
+      }
+      if (rc.load() != FDM_OK) break;
+      if (hipMemcpyAsync(cache_ + (size_t)m.second * es_ + off, dst, len, hipMemcpyHostToDevice, wk.s) !=
+              hipSuccess ||
+          hipEventRecord(wk.ev[b], wk.s) != hipSuccess) {
+        rc = FDM_E_HIP;
+        break;
+      }
+      used[b] = true;
+    }
+    if (hipStreamSynchronize(wk.s) != hipSuccess) rc = FDM_E_HIP;
+  };
+  const int n_thr = (int)std::min<size_t>(std::min<size_t>((size_t)std::max(n_threads_, 1), g_pool.w.size()), n_jobs);
+  std::vector<std::thread> th;
+  for (int t = 1; t < n_thr; ++t) th.emplace_back(work, t);
+  work(0);
+  for (auto& x : th) x.join();
+  if (rc.load() != FDM_OK) {
+    for (const auto& m : misses) {  // the failed blobs are not valid cache entries
+      slot_of_[m.first] = -1;
+      expert_in_[m.second] = -1;
+    }
+    *err = rc.load() == FDM_E_IO ? std::string("reading the layer file: ") + strerror(io_errno.load())
+                                 : std::string("copying experts to the device");
+    return rc.load();
+  }
+  bytes_ += (uint64_t)misses.size() * es_;
+  return FDM_OK;
+}
+
+void release_stream_pool() { g_pool.release(); }
+
+}  // namespace fdm

@@ -187,6 +187,34 @@ hipError_t launch_dense_ffn(const DenseArgs& a, hipStream_t s);
 // n elements of ggml type F32 / BF16 / F16 -> F16 bits (round to nearest even)
 hipError_t launch_to_f16(const void* src, int type, uint16_t* dst, size_t n, hipStream_t s);
 
+// expert_stream.hip: routed experts read from a packed layer file into an
+// LRU cache of expert blobs in HBM (host side).
+class ExpertStream {
+ public:
+  ~ExpertStream();
+  // FDM_OK or an FDM_E_* code with *err set
+  int open(const char* path, size_t expert_size, int n_experts, int n_cache, int n_threads, int device,
+           std::string* err);
+  // makes experts ids[0..K) resident; slots[k] = the cache slot of ids[k]
+  int fetch(const int* ids, int K, int* slots, std::string* err);
+  uint8_t* cache() const { return cache_; }
+  int n_cache() const { return n_cache_; }
+  uint64_t hits() const { return hits_; }
+  uint64_t misses() const { return misses_; }
+  uint64_t bytes_read() const { return bytes_; }
+
+ private:
+  int fd_ = -1;
+  size_t es_ = 0;
+  int n_experts_ = 0, n_cache_ = 0, n_threads_ = 0;
+  uint8_t* cache_ = nullptr;
+  std::vector<int> slot_of_, expert_in_;
+  std::vector<uint64_t> last_use_;
+  uint64_t tick_ = 0, hits_ = 0, misses_ = 0, bytes_ = 0;
+};
+// frees the pinned read buffers shared by all streamed layers
+void release_stream_pool();
+
 // synth_kernels.hip
 hipError_t launch_synth_q4k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);
 hipError_t launch_synth_q6k(uint8_t* dst, size_t n_blocks, uint64_t seed, hipStream_t s);

@@ -283,6 +283,31 @@ int fdm_rms_norm(const float *d_x, const float *d_w, float *d_o, int T, int d, v
 int fdm_moe_prefill(const int *layers, int n_layers, float *d_H, int T, int K,
                     const float *const *d_norm_w, int *d_idx, void *stream);
 
+/* ---- streamed layers: the reference's expert streaming (infer.m:1478-1602:
+ * route, then a parallel pread of the K selected experts from the packed
+ * layer file, N_PREAD_CHUNKS chunks each, then the experts) for models whose
+ * routed experts do not fit in HBM.  A streamed layer keeps the router
+ * weights and bias (caller-owned device memory, as fdm_layer_attach) and a
+ * library copy of the shared expert (packed blob, may be NULL) resident; its
+ * routed experts stay in layer_file (repack_experts.c layout: expert e at
+ * e * expert_size, n_experts = 256) and are read into an LRU cache of
+ * n_cache expert slots in HBM (K <= n_cache <= 256; n_cache = 256 keeps
+ * every expert once read).  n_threads host threads read (0: 8).
+ * fdm_moe_layer_streamed computes the same layer as fdm_moe_layer: it
+ * routes on the device (bit-exact), synchronises the stream to read the
+ * routed ids, reads the missing experts, then runs the experts, the combine
+ * and the residual on `stream`; it returns after queuing them.  Calls on one
+ * device must not overlap.  Opening a layer streamed releases it as a
+ * resident layer and the other way round; fdm_layer_release releases both.
+ * fdm_stream_stats: cumulative cache hits and misses (routed experts) and
+ * bytes read from the file. */
+int fdm_layer_stream_open(int L, const char *layer_file, size_t expert_size, int n_experts,
+                          const float *d_Wg, const float *d_bias, const void *d_shared, int n_cache,
+                          int n_threads);
+int fdm_moe_layer_streamed(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
+                           int *d_idx, float *d_w, void *stream);
+int fdm_stream_stats(int L, uint64_t *hits, uint64_t *misses, uint64_t *bytes_read);
+
 /* ---- dense FFN layers (the layers before the first MoE layer, L < 3 in
  * R1): replaces the dense branch of layer_forward (infer.m:1852-1868),
  *   hidden = h_in + W_down . (silu(W_gate . h_post) * (W_up . h_post)),
