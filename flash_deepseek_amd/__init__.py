@@ -15,6 +15,7 @@ for this path, over the C ABI of libfdm.so (include/fdm.h):
   metal_moe_forward             :1604      moe_forward / moe_forward_host
   layer_forward MoE branch      :1878-1922 moe_layer
   expert streaming (flash)      :1478-1602 stream_layer / moe_layer_streamed
+  mla_forward                   :766-903   attn_upload / attn_forward
   layer_forward dense branch    :1852-1868 dense_ffn (weights: upload_dense /
                                            attach_dense / load_dense_gguf)
 
@@ -34,7 +35,7 @@ __all__ = [
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
     "moe_forward_host", "moe_layer", "f32_to_f16", "upload_dense", "attach_dense", "load_dense_gguf",
     "release_dense", "dense_info", "dense_ffn", "DENSE_FFN", "stream_layer", "moe_layer_streamed",
-    "stream_stats", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "stream_stats", "attn_upload", "attn_forward", "attn_reset", "attn_len", "attn_release", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -217,6 +218,37 @@ def stream_stats(L):
     return h.value, m.value, b.value
 
 
+# ---- MLA attention (mla_forward) ------------------------------------------------------
+ATTN_FIELDS = ("attn_norm", "q_a", "q_a_norm", "q_b", "kv_a", "kv_a_norm", "k_b", "v_b", "o_proj")
+
+
+def attn_upload(L, weights, max_seq=_lib.ATTN_MAX_SEQ):
+    """Copy one layer's attention weights to HBM: weights maps the
+    fdm_attn_weights field names to contiguous host arrays (norms float32,
+    matrices F16 as uint16 or float16) in LayerAttnDense's layout."""
+    w = _lib.AttnWeights(*[weights[n].ctypes.data for n in ATTN_FIELDS])
+    call("fdm_attn_upload", L, ctypes.byref(w), max_seq)
+
+
+def attn_forward(L, hidden, pos, stream=None):
+    """hidden += W_o . MLA(rms_norm(hidden), pos), appending to the layer's KV cache."""
+    call("fdm_attn_forward", L, _p(hidden), pos, _stream(stream))
+
+
+def attn_reset(L):
+    call("fdm_attn_reset", L)
+
+
+def attn_len(L):
+    n = ctypes.c_int()
+    call("fdm_attn_len", L, ctypes.byref(n))
+    return n.value
+
+
+def attn_release(L):
+    call("fdm_attn_release", L)
+
+
 # ---- dense FFN layers (layer_forward's branch for L < 3) ------------------------------
 def f32_to_f16(src, dst, n=None, stream=None):
     """(__fp16) cast of f32_to_f16_alloc on the device: fp32 -> F16 bits."""
@@ -262,7 +294,8 @@ def dense_ffn(L, h_post, h_in, hidden, stream=None):
 # ---- per-kernel GPU timing (HIP events; the moe_prof_t counterpart) --------------------
 PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
           "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER,
-          "batch": _lib.PROF_BATCH, "prefill": _lib.PROF_PREFILL, "dense": _lib.PROF_DENSE}
+          "batch": _lib.PROF_BATCH, "prefill": _lib.PROF_PREFILL, "dense": _lib.PROF_DENSE,
+          "attn": _lib.PROF_ATTN}
 
 
 def prof_enable(on=True):

@@ -20,7 +20,7 @@ FDM_E_IO = -7
 FDM_E_FORMAT = -8
 
 (PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER, PROF_BATCH,
- PROF_PREFILL, PROF_DENSE) = range(9)
+ PROF_PREFILL, PROF_DENSE, PROF_ATTN) = range(10)
 
 QK_K = 256
 Q4K_BLOCK_SIZE = 144
@@ -32,6 +32,13 @@ MAX_K = 16
 MAX_LAYERS = 61
 MAX_TOKENS = 512
 DENSE_FFN = 18432
+ATTN_MAX_SEQ = 16384
+
+
+class AttnWeights(ctypes.Structure):
+    """struct fdm_attn_weights (host pointers)."""
+    _fields_ = [(n, ctypes.c_void_p) for n in
+                ("attn_norm", "q_a", "q_a_norm", "q_b", "kv_a", "kv_a_norm", "k_b", "v_b", "o_proj")]
 EXPERT_Q4K_BYTES = 24772608
 EXPERT_Q6K_BYTES = 28557312
 
@@ -67,6 +74,11 @@ SIGNATURES = {
     "fdm_layer_stream_open": [_i, ctypes.c_char_p, _sz, _i, _vp, _vp, _vp, _i, _i],
     "fdm_moe_layer_streamed": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
     "fdm_stream_stats": [_i, ctypes.POINTER(_u64), ctypes.POINTER(_u64), ctypes.POINTER(_u64)],
+    "fdm_attn_upload": [_i, ctypes.POINTER(AttnWeights), _i],
+    "fdm_attn_forward": [_i, _vp, _i, _vp],
+    "fdm_attn_reset": [_i],
+    "fdm_attn_len": [_i, ctypes.POINTER(_i)],
+    "fdm_attn_release": [_i],
     "fdm_dequant_q4k": [_vp, _vp, _sz, _vp],
     "fdm_dequant_q6k": [_vp, _vp, _sz, _vp],
     "fdm_matvec_q4k": [_vp, _vp, _vp, _u32, _u32, _vp],

@@ -29,6 +29,7 @@ SOURCES = [
     "synth_kernels.hip",
     "dense_kernels.hip",
     "expert_stream.hip",
+    "attn_kernels.hip",
     "gguf_host.hip",
     "capi.hip",
 ]

@@ -10,6 +10,7 @@
 #include <unistd.h>
 
 #include <initializer_list>
+#include <math.h>
 #include <memory>
 
 #include "../../include/fdm.h"
@@ -115,6 +116,33 @@ struct StreamedLayer {
   }
 };
 
+// An MLA attention layer: library-owned weights (F16 matrices, fp32 norm
+// vectors) in the reference's in-memory layout, its latent KV cache and the
+// YaRN frequency table.
+struct AttnLayer {
+  float *attn_norm = nullptr, *q_a_norm = nullptr, *kv_a_norm = nullptr, *freq = nullptr;
+  uint16_t *q_a = nullptr, *q_b = nullptr, *kv_a = nullptr, *k_b = nullptr, *v_b = nullptr, *o_proj = nullptr;
+  float *cache_c = nullptr, *cache_k = nullptr;
+  int max_seq = 0, len = 0;
+  ~AttnLayer() {
+    for (void* p : {(void*)attn_norm, (void*)q_a_norm, (void*)kv_a_norm, (void*)freq, (void*)q_a, (void*)q_b,
+                    (void*)kv_a, (void*)k_b, (void*)v_b, (void*)o_proj, (void*)cache_c, (void*)cache_k})
+      if (p) (void)hipFree(p);
+  }
+};
+
+// Per-token scratch of the attention (grown to the largest max_seq).
+struct AttnScratch {
+  float *normed = nullptr, *q_a = nullptr, *q_a_n = nullptr, *q = nullptr, *kv_a = nullptr, *c_kv_n = nullptr;
+  float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr;
+  int seq = 0;
+  void release() {
+    for (float* p : {normed, q_a, q_a_n, q, kv_a, c_kv_n, q_abs, scores, wc, attn})
+      if (p) (void)hipFree(p);
+    *this = AttnScratch();
+  }
+};
+
 // Event pairs recorded around kernel launches when profiling is on.
 struct Prof {
   static constexpr int kPool = 8192;
@@ -135,6 +163,8 @@ struct State {
   Layer layers[FDM_MAX_LAYERS];
   DenseLayer dense[FDM_MAX_LAYERS];
   std::unique_ptr<StreamedLayer> streamed[FDM_MAX_LAYERS];
+  std::unique_ptr<AttnLayer> attn[FDM_MAX_LAYERS];
+  AttnScratch attn_ws;
   int* stream_ids_h = nullptr;    // pinned host: the routed ids of a streamed call
   int* stream_slots_h = nullptr;  // pinned host: their cache slots
 };
@@ -609,6 +639,8 @@ int fdm_shutdown(void) {
   for (auto& L : g.layers) release_layer(L);
   for (auto& d : g.dense) release_dense(d);
   for (auto& st : g.streamed) st.reset();
+  for (auto& a : g.attn) a.reset();
+  g.attn_ws.release();
   release_stream_pool();
   for (int* p : {g.stream_ids_h, g.stream_slots_h})
     if (p) (void)hipHostFree(p);
@@ -1441,6 +1473,140 @@ int fdm_stream_stats(int L, uint64_t* hits, uint64_t* misses, uint64_t* bytes_re
   if (hits) *hits = es.hits();
   if (misses) *misses = es.misses();
   if (bytes_read) *bytes_read = es.bytes_read();
+  return FDM_OK;
+}
+
+// ---- MLA attention layers ---------------------------------------------------------------
+// yarn_freq(i) of infer.m:586-624 (YaRN correction range of the 64 rope
+// dims, base 10000, original context 4096, factor 40), in float as there.
+static void yarn_table(float* f) {
+  const int dim = 64;
+  const float base = 10000.0f, orig = 4096.0f, twopi = 2.0f * (float)M_PI;
+  const float lo_f = ((float)dim * logf(orig / (32.0f * twopi))) / (2.0f * logf(base));
+  const float hi_f = ((float)dim * logf(orig / (1.0f * twopi))) / (2.0f * logf(base));
+  int lo = (int)floorf(lo_f), hi = (int)ceilf(hi_f);
+  if (lo < 0) lo = 0;
+  if (hi > dim / 2 - 1) hi = dim / 2 - 1;
+  if (hi <= lo) hi = lo + 1;
+  for (int i = 0; i < dim / 2; ++i) {
+    const float freq_extra = 1.0f / powf(base, (float)(2 * i) / (float)dim);
+    const float freq_inter = freq_extra / 40.0f;
+    float denom = (float)(hi - lo);
+    if (denom < 1e-3f) denom = 1e-3f;
+    float ramp = ((float)i - (float)lo) / denom;
+    if (ramp < 0.0f) ramp = 0.0f;
+    if (ramp > 1.0f) ramp = 1.0f;
+    const float mask = 1.0f - ramp;
+    f[i] = freq_inter * (1.0f - mask) + freq_extra * mask;
+  }
+}
+
+int fdm_attn_upload(int L, const fdm_attn_weights* w, int max_seq) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  if (!w || !w->attn_norm || !w->q_a || !w->q_a_norm || !w->q_b || !w->kv_a || !w->kv_a_norm || !w->k_b ||
+      !w->v_b || !w->o_proj)
+    return fail(FDM_E_INVAL, "null attention weight");
+  if (max_seq < 1 || max_seq > FDM_ATTN_MAX_SEQ) return fail(FDM_E_INVAL, "max_seq %d: 1 .. %d", max_seq, FDM_ATTN_MAX_SEQ);
+  auto a = std::make_unique<AttnLayer>();
+  const size_t H = FDM_HIDDEN, QA = 1536, QB = 128 * 192, KVA = 576, KB = 128 * 512 * 128, O = 128 * 128;
+  struct M {
+    void** dst;
+    const void* src;
+    size_t bytes;
+  } m[] = {{(void**)&a->attn_norm, w->attn_norm, H * 4}, {(void**)&a->q_a_norm, w->q_a_norm, QA * 4},
+           {(void**)&a->kv_a_norm, w->kv_a_norm, 512 * 4}, {(void**)&a->q_a, w->q_a, QA * H * 2},
+           {(void**)&a->q_b, w->q_b, QB * QA * 2}, {(void**)&a->kv_a, w->kv_a, KVA * H * 2},
+           {(void**)&a->k_b, w->k_b, KB * 2}, {(void**)&a->v_b, w->v_b, KB * 2}, {(void**)&a->o_proj, w->o_proj, H * O * 2}};
+  for (const M& x : m) {
+    if (hipMalloc(x.dst, x.bytes) != hipSuccess) return fail(FDM_E_NOMEM, "cannot allocate attention layer %d", L);
+    FDM_HIP(hipMemcpy(*x.dst, x.src, x.bytes, hipMemcpyHostToDevice));
+  }
+  float freq[32];
+  yarn_table(freq);
+  if (hipMalloc(&a->freq, sizeof freq) != hipSuccess ||
+      hipMalloc(&a->cache_c, (size_t)max_seq * 512 * 4) != hipSuccess ||
+      hipMalloc(&a->cache_k, (size_t)max_seq * 64 * 4) != hipSuccess)
+    return fail(FDM_E_NOMEM, "cannot allocate the KV cache of layer %d", L);
+  FDM_HIP(hipMemcpy(a->freq, freq, sizeof freq, hipMemcpyHostToDevice));
+  a->max_seq = max_seq;
+  AttnScratch& ws = g.attn_ws;
+  if (ws.seq < max_seq) {
+    (void)hipDeviceSynchronize();
+    ws.release();
+    const size_t n[] = {H, QA, QA, QB, KVA, 512, 128 * 512, (size_t)128 * max_seq, 128 * 512, O};
+    float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.kv_a, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn};
+    for (int i = 0; i < 10; ++i)
+      if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
+        ws.release();
+        return fail(FDM_E_NOMEM, "cannot allocate the attention scratch");
+      }
+    ws.seq = max_seq;
+  }
+  (void)hipDeviceSynchronize();
+  g.attn[L] = std::move(a);
+  return FDM_OK;
+}
+
+int fdm_attn_reset(int L) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS || !g.attn[L]) return fail(FDM_E_STATE, "attention layer %d not resident", L);
+  g.attn[L]->len = 0;
+  return FDM_OK;
+}
+
+int fdm_attn_len(int L, int* len) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS || !g.attn[L]) return fail(FDM_E_STATE, "attention layer %d not resident", L);
+  if (len) *len = g.attn[L]->len;
+  return FDM_OK;
+}
+
+int fdm_attn_release(int L) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  (void)hipDeviceSynchronize();
+  g.attn[L].reset();
+  return FDM_OK;
+}
+
+int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS || !g.attn[L]) return fail(FDM_E_STATE, "attention layer %d not resident", L);
+  if (!d_hidden || !aligned(d_hidden, 16)) return fail(FDM_E_INVAL, "hidden must be a 16-byte aligned pointer");
+  if (pos < 0) return fail(FDM_E_INVAL, "pos %d", pos);
+  AttnLayer& a = *g.attn[L];
+  if (a.len >= a.max_seq) return fail(FDM_E_INVAL, "KV cache of layer %d is full (%d)", L, a.max_seq);
+  AttnScratch& ws = g.attn_ws;
+  hipStream_t s = as_stream(stream);
+  ProfScope prof(FDM_PROF_ATTN, s);
+  FDM_HIP(launch_rms_norm(d_hidden, a.attn_norm, ws.normed, nullptr, 1, FDM_HIDDEN, s));
+  FDM_HIP(launch_mv_f16(a.q_a, ws.normed, nullptr, ws.q_a, 1536, FDM_HIDDEN, s));
+  FDM_HIP(launch_rms_norm(ws.q_a, a.q_a_norm, ws.q_a_n, nullptr, 1, 1536, s));
+  FDM_HIP(launch_mv_f16(a.q_b, ws.q_a_n, nullptr, ws.q, 128 * 192, 1536, s));
+  FDM_HIP(launch_mv_f16(a.kv_a, ws.normed, nullptr, ws.kv_a, 576, FDM_HIDDEN, s));
+  FDM_HIP(launch_rms_norm(ws.kv_a, a.kv_a_norm, ws.c_kv_n, nullptr, 1, 512, s));
+  // softmax scale with the YaRN mscale (infer.m:802-815), in float as there
+  const float mscale = 0.1f * logf(40.0f) + 1.0f;
+  MlaArgs m;
+  m.q = ws.q;
+  m.kv_a = ws.kv_a;
+  m.c_kv_n = ws.c_kv_n;
+  m.freq = a.freq;
+  m.pos = pos;
+  m.len = a.len;
+  m.cache_c = a.cache_c;
+  m.cache_k = a.cache_k;
+  m.k_b = a.k_b;
+  m.v_b = a.v_b;
+  m.q_abs = ws.q_abs;
+  m.scores = ws.scores;
+  m.wc = ws.wc;
+  m.attn = ws.attn;
+  m.scale = (mscale * mscale) / sqrtf(192.0f);
+  FDM_HIP(launch_mla_attend(m, s));
+  FDM_HIP(launch_mv_f16(a.o_proj, ws.attn, d_hidden, d_hidden, FDM_HIDDEN, 128 * 128, s));
+  ++a.len;
   return FDM_OK;
 }
 

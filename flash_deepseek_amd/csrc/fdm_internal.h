@@ -187,6 +187,27 @@ hipError_t launch_dense_ffn(const DenseArgs& a, hipStream_t s);
 // n elements of ggml type F32 / BF16 / F16 -> F16 bits (round to nearest even)
 hipError_t launch_to_f16(const void* src, int type, uint16_t* dst, size_t n, hipStream_t s);
 
+// attn_kernels.hip: MLA attention of one decode token
+struct MlaArgs {
+  float* q;              // [128][192] (q_b output; the rope part rotated in place)
+  const float* kv_a;     // [576]: latent (512) + k_rope (64), before RoPE
+  const float* c_kv_n;   // [512]: rms_norm of the latent
+  const float* freq;     // [32]: yarn_freq(i)
+  int pos, len;          // RoPE position; cache rows before this token
+  float *cache_c, *cache_k;  // [max_seq][512], [max_seq][64]
+  const uint16_t *k_b, *v_b;  // F16 [128][512][128], [128][128][512]
+  float *q_abs, *scores, *wc, *attn;  // [128][512], [128][S], [128][512], [128][128]
+  float scale;
+};
+// y[r] = (res ? res[r] : 0) + W[r] . x; cols % 512 == 0, cols <= 16384
+hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, float* y, int rows, int cols,
+                         hipStream_t s);
+// y[h][r] = W[h][r] . x[h * x_stride ..]; cols 128 or 512
+hipError_t launch_mv_f16_heads(const uint16_t* W, const float* x, int x_stride, float* y, int heads, int rows_h,
+                               int cols, hipStream_t s);
+// RoPE + cache append, Q_abs, scores, softmax, weighted latent sum, v_b
+hipError_t launch_mla_attend(const MlaArgs& a, hipStream_t s);
+
 // expert_stream.hip: routed experts read from a packed layer file into an
 // LRU cache of expert blobs in HBM (host side).
 class ExpertStream {

@@ -308,6 +308,37 @@ int fdm_moe_layer_streamed(int L, const float *d_h_post, const float *d_h_in, in
                            int *d_idx, float *d_w, void *stream);
 int fdm_stream_stats(int L, uint64_t *hits, uint64_t *misses, uint64_t *bytes_read);
 
+/* ---- MLA attention (mla_forward, infer.m:766-903) of one decode token:
+ *   hidden <- hidden + W_o . MLA(rms_norm(hidden, attn_norm), pos)
+ * with the latent KV cache (c_kv 512 + k_rope 64 per position, fp32) on the
+ * device: q = W_qb . rms_norm(W_qa . x, q_a_norm) [128 heads][128 nope | 64
+ * rope], kv = W_kva . x (rms_norm on the 512 latent dims), YaRN RoPE of the
+ * rope parts at position pos (interleaved pairs, infer.m:586-655), the
+ * absorbed scores scale (k_b[h] . q_nope[h]) . c_kv + scale q_rope . k_rope
+ * with scale = mscale^2 / sqrt(192), mscale = 0.1 ln 40 + 1, softmax over
+ * the cache, the latent weighted sum, v_b per head and o_proj.  Weights in
+ * the layout LayerAttnDense holds them (infer.m:687-706), row-major; the
+ * library keeps its own copy (synchronous upload).  Each fdm_attn_forward
+ * appends the token at the cache's next row (fdm_attn_reset empties it);
+ * max_seq <= FDM_ATTN_MAX_SEQ.  Calls on one device must not overlap. */
+#define FDM_ATTN_MAX_SEQ 16384 /* MAX_SEQ, infer.m:67 */
+typedef struct fdm_attn_weights {
+  const float *attn_norm;  /* [7168]                                 */
+  const uint16_t *q_a;     /* F16 [1536][7168]                       */
+  const float *q_a_norm;   /* [1536]                                 */
+  const uint16_t *q_b;     /* F16 [128 * 192][1536]                  */
+  const uint16_t *kv_a;    /* F16 [576][7168]                        */
+  const float *kv_a_norm;  /* [512]                                  */
+  const uint16_t *k_b;     /* F16 [128][512][128]: per head (KV_LORA, NOPE) */
+  const uint16_t *v_b;     /* F16 [128][128][512]: per head (V_HEAD, KV_LORA) */
+  const uint16_t *o_proj;  /* F16 [7168][128 * 128]                  */
+} fdm_attn_weights;
+int fdm_attn_upload(int L, const fdm_attn_weights *host_weights, int max_seq);
+int fdm_attn_forward(int L, float *d_hidden, int pos, void *stream);
+int fdm_attn_reset(int L);
+int fdm_attn_len(int L, int *len);
+int fdm_attn_release(int L);
+
 /* ---- dense FFN layers (the layers before the first MoE layer, L < 3 in
  * R1): replaces the dense branch of layer_forward (infer.m:1852-1868),
  *   hidden = h_in + W_down . (silu(W_gate . h_post) * (W_up . h_post)),
@@ -349,7 +380,8 @@ int fdm_dense_ffn(int L, const float *d_h_post, const float *d_h_in, float *d_hi
 #define FDM_PROF_BATCH 6    /* fdm_moe_forward_batched: the whole step  */
 #define FDM_PROF_PREFILL 7  /* fdm_moe_prefill: all layers              */
 #define FDM_PROF_DENSE 8    /* fdm_dense_ffn: both launches             */
-#define FDM_PROF_PHASES 9
+#define FDM_PROF_ATTN 9     /* fdm_attn_forward: the whole token        */
+#define FDM_PROF_PHASES 10
 int fdm_prof_enable(int on);
 int fdm_prof_reset(void);
 int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);

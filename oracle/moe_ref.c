@@ -232,6 +232,132 @@ void orc_dense_ffn(const uint16_t *gate, const uint16_t *up, const uint16_t *dow
     free(o);
 }
 
+/* yarn_freq(i), i < 32 (infer.m:586-624): YaRN correction range of the 64
+ * rope dims (base 10000, original context 4096, beta 32 / 1), factor 40,
+ * evaluated in float as the reference does. */
+void orc_yarn_freq(float *freq) {
+    const int dim = 64;
+    const float base = 10000.0f, orig = 4096.0f, twopi = 2.0f * (float)M_PI;
+    const float lo_f = ((float)dim * logf(orig / (32.0f * twopi))) / (2.0f * logf(base));
+    const float hi_f = ((float)dim * logf(orig / (1.0f * twopi))) / (2.0f * logf(base));
+    int lo = (int)floorf(lo_f), hi = (int)ceilf(hi_f);
+    if (lo < 0) lo = 0;
+    if (hi > dim / 2 - 1) hi = dim / 2 - 1;
+    if (hi <= lo) hi = lo + 1;
+    for (int i = 0; i < dim / 2; ++i) {
+        const float extra = 1.0f / powf(base, (float)(2 * i) / (float)dim);
+        const float inter = extra / 40.0f;
+        float denom = (float)(hi - lo);
+        if (denom < 1e-3f) denom = 1e-3f;
+        float ramp = ((float)i - (float)lo) / denom;
+        if (ramp < 0.0f) ramp = 0.0f;
+        if (ramp > 1.0f) ramp = 1.0f;
+        const float mask = 1.0f - ramp;
+        freq[i] = inter * (1.0f - mask) + extra * mask;
+    }
+}
+
+/* The softmax scale of mla_forward (infer.m:802-815), in float. */
+float orc_mla_scale(void) {
+    const float m = 0.1f * logf(40.0f) + 1.0f;
+    return (m * m) / sqrtf(192.0f);
+}
+
+static void mv_f16_rows_d(const uint16_t *W, const double *x, double *y, int rows, int cols) {
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t *w = W + (size_t)r * cols;
+        double acc = 0.0;
+        for (int c = 0; c < cols; ++c) acc += (double)orc_fp16_to_fp32(w[c]) * x[c];
+        y[r] = acc;
+    }
+}
+
+/* mla_forward (infer.m:766-903) of one token at position pos; the cache holds
+ * len rows before it and receives row len.  Dot products, softmax and the
+ * latent sums in double (the truth); the three rms_norms are the reference's
+ * float function on the float-rounded inputs; the YaRN table, the rope angle
+ * (float)pos * freq and the softmax scale in float as the reference computes
+ * them.  Weights as LayerAttnDense holds them (see fdm_attn_weights). */
+void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q_a_norm, const uint16_t *q_b,
+                     const uint16_t *kv_a, const float *kv_a_norm, const uint16_t *k_b, const uint16_t *v_b,
+                     const uint16_t *o_proj, float *hidden, float *cache_c, float *cache_k, int len, int pos) {
+    const int H = ORC_HIDDEN, NH = 128, QA = 1536, KVL = 512, NOPE = 128, ROPE = 64, QK = 192, VH = 128;
+    const int S = len + 1;
+    float *normed = (float *)malloc(sizeof(float) * H);
+    double *xd = (double *)malloc(sizeof(double) * (H > NH * VH ? H : NH * VH));
+    double *qa = (double *)malloc(sizeof(double) * QA);
+    float *qaf = (float *)malloc(sizeof(float) * QA);
+    double *q = (double *)malloc(sizeof(double) * NH * QK);
+    double *kva = (double *)malloc(sizeof(double) * 576);
+    float *kvf = (float *)malloc(sizeof(float) * KVL);
+    float *ckv = (float *)malloc(sizeof(float) * KVL);
+    double *qabs = (double *)malloc(sizeof(double) * NH * KVL);
+    double *p = (double *)malloc(sizeof(double) * S);
+    double *wc = (double *)malloc(sizeof(double) * KVL);
+    double *attn = (double *)malloc(sizeof(double) * NH * VH);
+    double *o = (double *)malloc(sizeof(double) * H);
+    float freq[32];
+    orc_yarn_freq(freq);
+
+    orc_rms_norm(hidden, attn_norm, normed, H);
+    for (int i = 0; i < H; ++i) xd[i] = normed[i];
+    mv_f16_rows_d(q_a, xd, qa, QA, H);
+    for (int i = 0; i < QA; ++i) qaf[i] = (float)qa[i];
+    orc_rms_norm(qaf, q_a_norm, qaf, QA);
+    for (int i = 0; i < QA; ++i) qa[i] = qaf[i];
+    mv_f16_rows_d(q_b, qa, q, NH * QK, QA);
+    mv_f16_rows_d(kv_a, xd, kva, 576, H);
+    for (int i = 0; i < KVL; ++i) kvf[i] = (float)kva[i];
+    orc_rms_norm(kvf, kv_a_norm, ckv, KVL);
+    /* interleaved-pair YaRN rotation (infer.m:626-655) */
+    double krot[64];
+    for (int i = 0; i < ROPE / 2; ++i) {
+        const float ang = (float)pos * freq[i];
+        const double c = cos((double)ang), sn = sin((double)ang);
+        for (int h = 0; h < NH; ++h) {
+            double *qr = q + (size_t)h * QK + NOPE;
+            const double a = qr[2 * i], b = qr[2 * i + 1];
+            qr[2 * i] = a * c - b * sn;
+            qr[2 * i + 1] = a * sn + b * c;
+        }
+        const double a = kva[KVL + 2 * i], b = kva[KVL + 2 * i + 1];
+        krot[2 * i] = a * c - b * sn;
+        krot[2 * i + 1] = a * sn + b * c;
+    }
+    for (int i = 0; i < KVL; ++i) cache_c[(size_t)len * KVL + i] = ckv[i];
+    for (int i = 0; i < ROPE; ++i) cache_k[(size_t)len * ROPE + i] = (float)krot[i];
+    const double scale = orc_mla_scale();
+    for (int h = 0; h < NH; ++h) {
+        /* Q_abs[h] = k_b[h] (KV_LORA x NOPE) . q_nope[h] (infer.m:722-731) */
+        mv_f16_rows_d(k_b + (size_t)h * KVL * NOPE, q + (size_t)h * QK, qabs + (size_t)h * KVL, KVL, NOPE);
+    }
+    for (int h = 0; h < NH; ++h) {
+        const double *qb = qabs + (size_t)h * KVL, *qr = q + (size_t)h * QK + NOPE;
+        double m = -INFINITY;
+        for (int t = 0; t < S; ++t) {
+            double a = 0.0, b = 0.0;
+            for (int i = 0; i < KVL; ++i) a += qb[i] * cache_c[(size_t)t * KVL + i];
+            for (int i = 0; i < ROPE; ++i) b += qr[i] * cache_k[(size_t)t * ROPE + i];
+            p[t] = scale * a + scale * b;
+            if (p[t] > m) m = p[t];
+        }
+        double sum = 0.0;
+        for (int t = 0; t < S; ++t) {
+            p[t] = exp(p[t] - m);
+            sum += p[t];
+        }
+        for (int i = 0; i < KVL; ++i) wc[i] = 0.0;
+        for (int t = 0; t < S; ++t)
+            for (int i = 0; i < KVL; ++i) wc[i] += p[t] / sum * cache_c[(size_t)t * KVL + i];
+        /* attn[h] = v_b[h] (V_HEAD x KV_LORA) . wc (infer.m:740-749) */
+        mv_f16_rows_d(v_b + (size_t)h * VH * KVL, wc, attn + (size_t)h * VH, VH, KVL);
+    }
+    mv_f16_rows_d(o_proj, attn, o, H, NH * VH);
+    for (int i = 0; i < H; ++i) hidden[i] = (float)((double)hidden[i] + o[i]);
+    free(normed); free(xd); free(qa); free(qaf); free(q); free(kva); free(kvf); free(ckv);
+    free(qabs); free(p); free(wc); free(attn); free(o);
+}
+
 /* ---------------------------------------------------------------------- */
 /* Router logits, canonical order.  For output row e, 256 partial sums are
  * formed: partial t accumulates, with one fmaf per element, the float4

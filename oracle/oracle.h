@@ -73,6 +73,12 @@ uint16_t orc_fp32_to_fp16(float f);
 void orc_fp32_to_fp16_array(const float *src, uint16_t *dst, size_t n);
 void orc_dense_ffn(const uint16_t *gate, const uint16_t *up, const uint16_t *down, int inter,
                    const float *h_post, const float *h_in, float *out, float *act_out);
+/* MLA attention of one decode token (infer.m:586-655, 766-903), see moe_ref.c. */
+void orc_yarn_freq(float *freq);
+float orc_mla_scale(void);
+void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q_a_norm, const uint16_t *q_b,
+                     const uint16_t *kv_a, const float *kv_a_norm, const uint16_t *k_b, const uint16_t *v_b,
+                     const uint16_t *o_proj, float *hidden, float *cache_c, float *cache_k, int len, int pos);
 void orc_expert_ffn(const void *blob, int down_is_q6, const float *x, float *out,
                     float *gate_out, float *up_out, float *act_out);
 

@@ -55,6 +55,9 @@ def _load():
         "orc_fp32_to_fp16": (ctypes.c_uint16, [ctypes.c_float]),
         "orc_fp32_to_fp16_array": (None, [_f32p, _vp, ctypes.c_size_t]),
         "orc_dense_ffn": (None, [_vp, _vp, _vp, ctypes.c_int, _f32p, _vp, _f32p, _vp]),
+        "orc_yarn_freq": (None, [_f32p]),
+        "orc_mla_scale": (ctypes.c_float, []),
+        "orc_mla_forward": (None, [_vp] * 9 + [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_router_logits": (None, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_route_ex": (None, [_f32p, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 ctypes.c_int, ctypes.c_float, _i32p, _f32p]),
@@ -179,6 +182,38 @@ def dense_ffn(gate, up, down, h_post, h_in=None, with_act=False):
     L.orc_dense_ffn(_ptr(gate), _ptr(up), _ptr(down), inter, h_post, hp, out,
                     None if act is None else _ptr(act))
     return (out, act) if with_act else out
+
+
+ATTN_FIELDS = ("attn_norm", "q_a", "q_a_norm", "q_b", "kv_a", "kv_a_norm", "k_b", "v_b", "o_proj")
+
+
+def yarn_freq():
+    f = np.empty(32, dtype=np.float32)
+    L.orc_yarn_freq(f)
+    return f
+
+
+def mla_scale():
+    return L.orc_mla_scale()
+
+
+class MlaCache:
+    """The latent KV cache of one layer (c_kv [n][512], k_rope [n][64], fp32)."""
+
+    def __init__(self, max_seq):
+        self.c = np.zeros((max_seq, 512), np.float32)
+        self.k = np.zeros((max_seq, 64), np.float32)
+        self.len = 0
+
+
+def mla_forward(w, hidden, cache, pos):
+    """mla_forward (infer.m:766-903): returns the new hidden; appends to cache.
+    w maps ATTN_FIELDS to arrays (norms float32, matrices F16 bits)."""
+    h = np.ascontiguousarray(hidden, dtype=np.float32).copy()
+    args = [_ptr(np.ascontiguousarray(w[n])) for n in ATTN_FIELDS]
+    L.orc_mla_forward(*args, h, cache.c, cache.k, cache.len, pos)
+    cache.len += 1
+    return h
 
 
 # ---- router -------------------------------------------------------------------
