@@ -186,6 +186,46 @@ def bench_dense(F, torch, args, stream, steps=60, warmup=6):
             "frac": round(layer_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def bench_attn(F, torch, args, stream, steps=50):
+    """MLA attention of decode tokens (one layer, R1 shapes, F16 weights) at
+    a cache of args.attn positions: the cache is filled first, then `steps`
+    tokens are timed (positions args.attn .. args.attn + steps - 1)."""
+    g = torch.Generator(device="cuda").manual_seed(766)
+
+    def f16(rows, cols, *lead):
+        t = torch.randn((*lead, rows, cols), generator=g, device="cuda") * cols ** -0.5
+        return t.half().cpu().numpy().view(np.uint16)
+
+    def norm(n):
+        return (1.0 + 0.1 * torch.randn(n, generator=g, device="cuda")).cpu().numpy()
+
+    w = {"attn_norm": norm(HIDDEN), "q_a": f16(1536, HIDDEN), "q_a_norm": norm(1536),
+         "q_b": f16(128 * 192, 1536), "kv_a": f16(576, HIDDEN), "kv_a_norm": norm(512),
+         "k_b": f16(512, 128, 128), "v_b": f16(128, 512, 128), "o_proj": f16(HIDDEN, 128 * 128)}
+    S = args.attn
+    F.attn_upload(0, w, max_seq=S + steps)
+    wbytes = sum(a.nbytes for a in w.values())
+    X = torch.randn((S + steps, HIDDEN), generator=g, device="cuda")
+    for pos in range(S):
+        F.attn_forward(0, X[pos], pos, stream=stream)
+    torch.cuda.synchronize()
+    F.prof_enable(True)
+    F.prof_reset()
+    t0 = time.perf_counter()
+    for pos in range(S, S + steps):
+        F.attn_forward(0, X[pos], pos, stream=stream)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    n, tot, mn, mx = F.prof_read("attn")
+    F.prof_enable(False)
+    F.attn_release(0)
+    kern = tot / n * 1e-3 if n else dt
+    step_bytes = wbytes + (S + steps // 2) * 576 * 4 * 3
+    return {"cache_len": S, "us_per_token": round(dt * 1e6, 2), "kernels_us": round(kern * 1e6, 2),
+            "weight_bytes": wbytes, "gbps": round(step_bytes / kern / 1e9, 1),
+            "frac": round(step_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,6 +240,8 @@ def main():
                     help="also time batched decode at these token counts ('' to skip)")
     ap.add_argument("--prefill", type=int, default=512,
                     help="also time prefill of this many tokens through 4 resident layers (0 to skip)")
+    ap.add_argument("--attn", type=int, default=1024,
+                    help="also time MLA attention of decode tokens at this KV cache length (0 to skip)")
     ap.add_argument("--dense", type=int, default=3,
                     help="also time the dense FFN over this many F16 dense layers (0 to skip)")
     ap.add_argument("--pmc-workload", action="store_true",
@@ -320,6 +362,8 @@ def main():
         result["prefill"] = bench_prefill(F, torch, layers, args, stream, K)
     if args.dense:
         result["dense"] = bench_dense(F, torch, args, stream)
+    if args.attn:
+        result["attn"] = bench_attn(F, torch, args, stream)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args.down, args.cpu_seconds, K)
         cb = result["cpu_baseline"]["value"]

@@ -136,72 +136,97 @@ __global__ __launch_bounds__(256) void k_mla_rope_append(float* __restrict__ q, 
 }
 
 // scores[h][s] = scale * (Q_abs[h] . c_kv[s]) + scale * (q_rope[h] . k_rope[s])
-// for s < S (the reference's two sgemm calls, infer.m:829-838).  One
-// workgroup per 16 positions: their cache rows in LDS, wave w handles heads
-// w, w + 4, ...
+// for s < S (the reference's two sgemm calls, infer.m:829-838), as a tiled
+// product: workgroup (position block of 64, head block of 16); the 576 dims
+// go through LDS in 9 tiles of 64 (8 latent, 1 rope), the cache tile
+// transposed so the 64 lanes of a wave read 64 consecutive positions.
+// Thread (wave w, lane p): position p of the block, heads 4 w .. 4 w + 3.
 __global__ __launch_bounds__(256) void k_mla_scores(const float* __restrict__ q_abs, const float* __restrict__ q,
                                                     const float* __restrict__ cache_c,
                                                     const float* __restrict__ cache_k, int S, float scale,
                                                     float* __restrict__ scores) {
-  __shared__ float cs[16][512];
-  __shared__ float ks[16][64];
-  const int s0 = blockIdx.x * 16, ns = min(16, S - s0);
-  for (int i = threadIdx.x; i < 16 * 512; i += 256) cs[i / 512][i % 512] = (i / 512 < ns) ? cache_c[(size_t)s0 * 512 + i] : 0.0f;
-  for (int i = threadIdx.x; i < 16 * 64; i += 256) ks[i / 64][i % 64] = (i / 64 < ns) ? cache_k[(size_t)s0 * 64 + i] : 0.0f;
-  __syncthreads();
+  __shared__ float ct[64][65];  // [dim][position], padded
+  __shared__ float qt[16][64];  // [head][dim]
+  const int s0 = blockIdx.x * 64, h0 = blockIdx.y * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int h = wave; h < 128; h += 4) {
-    float qa[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qa[j] = q_abs[(size_t)h * 512 + 64 * j + lane];
-    const float qr = q[(size_t)h * 192 + 128 + lane];
-    for (int s = 0; s < ns; ++s) {
-      float a = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) a = fmaf(qa[j], cs[s][64 * j + lane], a);
-      const float b = qr * ks[s][lane];
-      a = lane_sum(a, 64);
-      const float bb = lane_sum(b, 64);
-      if (lane == 0) scores[(size_t)h * S + s0 + s] = scale * a + scale * bb;
+  float a[4] = {}, b[4] = {};
+  for (int tile = 0; tile < 9; ++tile) {
+    const bool rope = tile == 8;
+    __syncthreads();
+    // cache tile: positions s0 .. s0 + 63, dims 64 tile .. + 63 (coalesced rows)
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+      const int sp = i >> 6, d = i & 63, s = s0 + sp;
+      float v = 0.0f;
+      if (s < S) v = rope ? cache_k[(size_t)s * 64 + d] : cache_c[(size_t)s * 512 + 64 * tile + d];
+      ct[d][sp] = v;
     }
+    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
+      const int h = h0 + (i >> 6), d = i & 63;
+      qt[i >> 6][d] = rope ? q[(size_t)h * 192 + 128 + d] : q_abs[(size_t)h * 512 + 64 * tile + d];
+    }
+    __syncthreads();
+#pragma unroll 8
+    for (int d = 0; d < 64; ++d) {
+      const float c = ct[d][lane];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (rope)
+          b[j] = fmaf(qt[4 * wave + j][d], c, b[j]);
+        else
+          a[j] = fmaf(qt[4 * wave + j][d], c, a[j]);
+      }
+    }
+  }
+  const int s = s0 + lane;
+  if (s < S) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) scores[(size_t)(h0 + 4 * wave + j) * S + s] = scale * a[j] + scale * b[j];
   }
 }
 
-// Per head (one workgroup each): p = softmax(scores[h][0..S)) (infer.m:385-389),
-// then wc[h][d] = sum_s p[s] c_kv[s][d] (infer.m:862-867).
-__global__ __launch_bounds__(256) void k_mla_softmax_wsum(const float* __restrict__ scores, int S,
+// Per head (one workgroup of 512 threads each): p = softmax(scores[h][0..S))
+// (infer.m:385-389) into LDS once, then thread d: wc[h][d] = sum_s p[s] c_kv[s][d]
+// (infer.m:862-867).
+__global__ __launch_bounds__(512) void k_mla_softmax_wsum(const float* __restrict__ scores, int S,
                                                           const float* __restrict__ cache_c,
                                                           float* __restrict__ wc) {
-  __shared__ float red[4];
+  __shared__ float ps[kMvMaxCols];  // S <= 16384
+  __shared__ float red[8];
   __shared__ float stat;
   const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const float* sc = scores + (size_t)h * S;
   float m = -__builtin_inff();
-  for (int s = threadIdx.x; s < S; s += 256) m = fmaxf(m, sc[s]);
+  for (int s = threadIdx.x; s < S; s += 512) m = fmaxf(m, sc[s]);
   for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   if (lane == 0) red[wave] = m;
   __syncthreads();
-  if (threadIdx.x == 0) stat = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  if (threadIdx.x == 0) {
+    float v = red[0];
+    for (int i = 1; i < 8; ++i) v = fmaxf(v, red[i]);
+    stat = v;
+  }
   __syncthreads();
   m = stat;
   float sum = 0.0f;
-  for (int s = threadIdx.x; s < S; s += 256) sum += expf(sc[s] - m);
+  for (int s = threadIdx.x; s < S; s += 512) {
+    const float e = expf(sc[s] - m);
+    ps[s] = e;
+    sum += e;
+  }
   sum = lane_sum(sum, 64);
   __syncthreads();
   if (lane == 0) red[wave] = sum;
   __syncthreads();
-  if (threadIdx.x == 0) stat = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+  if (threadIdx.x == 0) {
+    float v = 0.0f;
+    for (int i = 0; i < 8; ++i) v += red[i];
+    stat = 1.0f / v;
+  }
   __syncthreads();
   const float inv = stat;
-  // thread t: dims t and t + 256
-  float a0 = 0.0f, a1 = 0.0f;
-  for (int s = 0; s < S; ++s) {
-    const float p = expf(sc[s] - m) * inv;
-    a0 = fmaf(p, cache_c[(size_t)s * 512 + threadIdx.x], a0);
-    a1 = fmaf(p, cache_c[(size_t)s * 512 + 256 + threadIdx.x], a1);
-  }
-  wc[(size_t)h * 512 + threadIdx.x] = a0;
-  wc[(size_t)h * 512 + 256 + threadIdx.x] = a1;
+  float acc = 0.0f;
+  for (int s = 0; s < S; ++s) acc = fmaf(ps[s] * inv, cache_c[(size_t)s * 512 + threadIdx.x], acc);
+  wc[(size_t)h * 512 + threadIdx.x] = acc;
 }
 
 hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, float* y, int rows, int cols,
@@ -227,9 +252,10 @@ hipError_t launch_mla_attend(const MlaArgs& a, hipStream_t s) {
   // Q_abs[h] = k_b[h] (512 x 128) . q_nope[h]
   if (hipError_t e = launch_mv_f16_heads(a.k_b, a.q, 192, a.q_abs, 128, 512, 128, s)) return e;
   const int S = a.len + 1;
-  k_mla_scores<<<(S + 15) / 16, 256, 0, s>>>(a.q_abs, a.q, a.cache_c, a.cache_k, S, a.scale, a.scores);
+  k_mla_scores<<<dim3((S + 63) / 64, 128 / 16), 256, 0, s>>>(a.q_abs, a.q, a.cache_c, a.cache_k, S, a.scale,
+                                                              a.scores);
   if (hipError_t e = hipGetLastError()) return e;
-  k_mla_softmax_wsum<<<128, 256, 0, s>>>(a.scores, S, a.cache_c, a.wc);
+  k_mla_softmax_wsum<<<128, 512, 0, s>>>(a.scores, S, a.cache_c, a.wc);
   if (hipError_t e = hipGetLastError()) return e;
   // attn[h] = v_b[h] (128 x 512) . wc[h]
   return launch_mv_f16_heads(a.v_b, a.wc, 512, a.attn, 128, 128, 512, s);
