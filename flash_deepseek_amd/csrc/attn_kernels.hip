@@ -153,16 +153,28 @@ __global__ __launch_bounds__(256) void k_mla_scores(const float* __restrict__ q_
   for (int tile = 0; tile < 9; ++tile) {
     const bool rope = tile == 8;
     __syncthreads();
-    // cache tile: positions s0 .. s0 + 63, dims 64 tile .. + 63 (coalesced rows)
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-      const int sp = i >> 6, d = i & 63, s = s0 + sp;
-      float v = 0.0f;
-      if (s < S) v = rope ? cache_k[(size_t)s * 64 + d] : cache_c[(size_t)s * 512 + 64 * tile + d];
-      ct[d][sp] = v;
+    // cache tile: positions s0 .. s0 + 63, dims 64 tile .. + 63 (coalesced
+    // rows); every load of the tile is issued before the first LDS store
+    float cv[16], qv[4];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int i = threadIdx.x + 256 * k, sp = i >> 6, d = i & 63, s = s0 + sp;
+      cv[k] = s < S ? (rope ? cache_k[(size_t)s * 64 + d] : cache_c[(size_t)s * 512 + 64 * tile + d]) : 0.0f;
     }
-    for (int i = threadIdx.x; i < 16 * 64; i += 256) {
-      const int h = h0 + (i >> 6), d = i & 63;
-      qt[i >> 6][d] = rope ? q[(size_t)h * 192 + 128 + d] : q_abs[(size_t)h * 512 + 64 * tile + d];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = threadIdx.x + 256 * k, h = h0 + (i >> 6), d = i & 63;
+      qv[k] = rope ? q[(size_t)h * 192 + 128 + d] : q_abs[(size_t)h * 512 + 64 * tile + d];
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      ct[i & 63][i >> 6] = cv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      qt[i >> 6][i & 63] = qv[k];
     }
     __syncthreads();
 #pragma unroll 8
