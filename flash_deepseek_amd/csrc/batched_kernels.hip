@@ -28,10 +28,11 @@ constexpr int kBGuRows = 8;                   // gate (and up) rows per tile
 constexpr int kBGuTiles = kFfn / kBGuRows;    // 256
 constexpr int kBDnRows = 16;                  // down rows per tile
 constexpr int kBDnTiles = kHidden / kBDnRows; // 448
+constexpr int kBShChunk = 16;                 // shared-expert tokens per work item
 
 // Token t's row list of one work item: a distinct routed expert (its
-// (token, slot) pairs, rows = pair positions) or the shared expert (every
-// token, rows = P + t).
+// (token, slot) pairs, rows = pair positions) or one chunk of kBShChunk
+// tokens of the shared expert (rows = P + t).
 struct ItemRows {
   int first, count;  // pair positions [first, first + count) or tokens [0, count)
   bool shared;
@@ -47,19 +48,41 @@ __device__ __forceinline__ ItemRows item_rows(const BatchArgs& b, int d, int D, 
     r.shared = false;
   } else {
     *expert = -1;
-    r.first = 0;
-    r.count = b.T;
+    r.first = (d - D) * kBShChunk;
+    r.count = min(kBShChunk, b.T - r.first);
     r.shared = true;
   }
   return r;
 }
 
-__device__ __forceinline__ void stage_records(XGroup* __restrict__ dst,
-                                              const XGroup* __restrict__ src, int n) {
-  const u32x4* s = reinterpret_cast<const u32x4*>(src);
-  u32x4* d = reinterpret_cast<u32x4*>(dst);
-  for (int i = threadIdx.x; i < n * 9; i += 256) d[i] = s[i];
+__device__ __forceinline__ int n_items_of(const BatchArgs& b, int D) {
+  return D + (b.shared ? (b.T + kBShChunk - 1) / kBShChunk : 0);
 }
+
+// One token's digit records (N records of 9 x 16 bytes) held in registers,
+// 16 bytes per thread per step: loaded while the previous token is being
+// contracted, stored to LDS after it.
+template <int N>
+struct Records {
+  static constexpr int kSteps = (N * 9 + 255) / 256;
+  u32x4 v[kSteps];
+  __device__ __forceinline__ void load(const XGroup* __restrict__ src) {
+    const u32x4* s = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < N * 9) v[k] = s[i];
+    }
+  }
+  __device__ __forceinline__ void store(XGroup* __restrict__ dst) const {
+    u32x4* d = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < N * 9) d[i] = v[k];
+    }
+  }
+};
 
 }  // namespace
 
@@ -112,10 +135,10 @@ __global__ __launch_bounds__(256) void k_dispatch(BatchArgs b) {
 // in gate (lanes 0-31) and up (lanes 32-63), 16 lanes per row; the tile's
 // weights are loaded once and every token of the item is applied to them.
 __global__ __launch_bounds__(256) void k_bgateup(BatchArgs b) {
-  __shared__ XGroup xs[kHidden / 64];
+  __shared__ XGroup xs[2][kHidden / 64];
   const int tile = blockIdx.x;
   const int D = *b.n_distinct;
-  const int n_items = D + (b.shared ? 1 : 0);
+  const int n_items = n_items_of(b, D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
   const int row = tile * kBGuRows + 2 * wave + (q & 1);
@@ -129,12 +152,16 @@ __global__ __launch_bounds__(256) void k_bgateup(BatchArgs b) {
     const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
 #pragma unroll
     for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
+    auto tok_of = [&](int i) { return r.shared ? r.first + i : b.pair_tok[r.first + i]; };
+    Records<kHidden / 64> rec;
+    rec.load(b.xd + (size_t)tok_of(0) * (kHidden / 64));
+    __syncthreads();  // the previous item's last records are no longer read
+    rec.store(xs[0]);
+    __syncthreads();
     for (int i = 0; i < r.count; ++i) {
-      const int tok = r.shared ? i : b.pair_tok[r.first + i];
-      const int out_row = r.shared ? P + i : r.first + i;
-      __syncthreads();  // the previous token's records are no longer read
-      stage_records(xs, b.xd + (size_t)tok * (kHidden / 64), kHidden / 64);
-      __syncthreads();
+      const int out_row = r.shared ? P + r.first + i : r.first + i;
+      const XGroup* cur = xs[i & 1];
+      if (i + 1 < r.count) rec.load(b.xd + (size_t)tok_of(i + 1) * (kHidden / 64));
       float acc = 0.0f;
 #pragma unroll
       for (int k = 0; k < 7; ++k) {
@@ -142,12 +169,15 @@ __global__ __launch_bounds__(256) void k_bgateup(BatchArgs b) {
         // unpacking stays inside this loop instead of being hoisted out of
         // it (seven unpacked groups would take 112 more registers)
         __asm__ volatile("" : "+v"(ld[k].q0), "+v"(ld[k].q1), "+v"(ld[k].hdr_part));
-        acc += q4k_group_dot_ld(ld[k], sel, &xs[16 * k + l16]);
+        acc += q4k_group_dot_ld(ld[k], sel, &cur[16 * k + l16]);
         __builtin_amdgcn_sched_barrier(0);
       }
       acc = sum16(acc);
       const float up = __shfl(acc, (lane + 32) & 63);
       if (lane == 0 || lane == 16) b.act[(size_t)out_row * kFfn + row] = silu_mul(acc, up);
+      // the other buffer was last read before the barrier that ended token i - 1
+      if (i + 1 < r.count) rec.store(xs[(i + 1) & 1]);
+      __syncthreads();
     }
   }
 }
@@ -158,10 +188,10 @@ __global__ __launch_bounds__(256) void k_bgateup(BatchArgs b) {
 // row of the item.
 template <bool Q6>
 __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
-  __shared__ XGroup xs[kFfn / 64];
+  __shared__ XGroup xs[2][kFfn / 64];
   const int tile = blockIdx.x;
   const int D = *b.n_distinct;
-  const int n_items = D + (b.shared ? 1 : 0);
+  const int n_items = n_items_of(b, D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
   const int row = tile * kBDnRows + wave * 4 + (lane >> 4);
@@ -179,21 +209,28 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
     } else {
       l6 = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (l16 >> 1) * kQ6KBlock, l16 & 1);
     }
+    auto row_of = [&](int i) { return r.shared ? P + r.first + i : r.first + i; };
+    Records<kFfn / 64> rec;
+    rec.load(b.act_xd + (size_t)row_of(0) * (kFfn / 64));
+    __syncthreads();
+    rec.store(xs[0]);
+    __syncthreads();
     for (int i = 0; i < r.count; ++i) {
-      const int arow = r.shared ? P + i : r.first + i;
-      __syncthreads();
-      stage_records(xs, b.act_xd + (size_t)arow * (kFfn / 64), kFfn / 64);
-      __syncthreads();
+      const int arow = row_of(i);
+      const XGroup* cur = xs[i & 1];
+      if (i + 1 < r.count) rec.load(b.act_xd + (size_t)row_of(i + 1) * (kFfn / 64));
       float acc = 0.0f;
       if (!Q6) {
         const Q4KScaleSel sel = q4k_scale_sel(l16 & 3);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) acc += q4k_group_dot_ld(ld[k], sel, &xs[16 * k + l16]);
+        for (int k = 0; k < 2; ++k) acc += q4k_group_dot_ld(ld[k], sel, &cur[16 * k + l16]);
       } else {
-        acc = q6k_half_dot_ld(l6, &xs[2 * l16]);
+        acc = q6k_half_dot_ld(l6, &cur[2 * l16]);
       }
       acc = sum16(acc);
       if (l16 == 0) b.eo[(size_t)arow * kHidden + row] = acc;
+      if (i + 1 < r.count) rec.store(xs[(i + 1) & 1]);
+      __syncthreads();
     }
   }
 }
@@ -231,7 +268,7 @@ hipError_t launch_combine(const BatchArgs& b, hipStream_t s) {
 hipError_t launch_batched_down(const BatchArgs& b, bool down_q6, hipStream_t s) {
   const int P = b.T * b.K;
   const int rows = P + (b.shared ? b.T : 0);
-  const int max_items = (P < kExperts ? P : kExperts) + (b.shared ? 1 : 0);
+  const int max_items = (P < kExperts ? P : kExperts) + (b.shared ? (b.T + kBShChunk - 1) / kBShChunk : 0);
   const int gy = max_items < 16 ? max_items : 16;
   if (hipError_t e = launch_xdigits(b.act, (size_t)rows * (kFfn / 64), b.act_xd, s)) return e;
   if (down_q6)
@@ -244,7 +281,7 @@ hipError_t launch_batched_down(const BatchArgs& b, bool down_q6, hipStream_t s) 
 hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s) {
   const int P = b.T * b.K;
   const int rows = P + (b.shared ? b.T : 0);
-  const int max_items = (P < kExperts ? P : kExperts) + (b.shared ? 1 : 0);
+  const int max_items = (P < kExperts ? P : kExperts) + (b.shared ? (b.T + kBShChunk - 1) / kBShChunk : 0);
   // workgroups per tile: enough items in flight to fill the chip
   const int gy = max_items < 16 ? max_items : 16;
   hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(256), 0, s, b);
