@@ -35,7 +35,7 @@ __all__ = [
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
     "moe_forward_host", "moe_layer", "f32_to_f16", "upload_dense", "attach_dense", "load_dense_gguf",
     "release_dense", "dense_info", "dense_ffn", "DENSE_FFN", "stream_layer", "moe_layer_streamed",
-    "stream_stats", "attn_upload", "attn_forward", "attn_reset", "attn_len", "attn_release", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
+    "stream_stats", "attn_upload", "attn_load_gguf", "attn_forward", "attn_reset", "attn_len", "attn_release", "set_batch_kernel", "BATCH_AUTO", "BATCH_DOT4", "BATCH_MFMA", "prof_enable", "prof_reset", "prof_read", "synth_q4k", "synth_q6k", "synth_normal", "FdmError",
     "QK_K", "Q4K_BLOCK_SIZE", "Q6K_BLOCK_SIZE", "HIDDEN", "MOE_FFN", "N_EXPERTS", "MAX_K",
     "MAX_LAYERS", "MAX_TOKENS", "EXPERT_Q4K_BYTES", "EXPERT_Q6K_BYTES",
 ]
@@ -228,6 +228,12 @@ def attn_upload(L, weights, max_seq=_lib.ATTN_MAX_SEQ):
     matrices F16 as uint16 or float16) in LayerAttnDense's layout."""
     w = _lib.AttnWeights(*[weights[n].ctypes.data for n in ATTN_FIELDS])
     call("fdm_attn_upload", L, ctypes.byref(w), max_seq)
+
+
+def attn_load_gguf(L, gguf, max_seq=_lib.ATTN_MAX_SEQ):
+    """One layer's attention weights from an open GGUF (see gguf.GGUF),
+    converted as load_layer_weights does."""
+    call("fdm_attn_load_gguf", L, gguf.handle, max_seq)
 
 
 def attn_forward(L, hidden, pos, stream=None):

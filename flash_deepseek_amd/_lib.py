@@ -76,6 +76,7 @@ SIGNATURES = {
     "fdm_stream_stats": [_i, ctypes.POINTER(_u64), ctypes.POINTER(_u64), ctypes.POINTER(_u64)],
     "fdm_attn_upload": [_i, ctypes.POINTER(AttnWeights), _i],
     "fdm_attn_forward": [_i, _vp, _i, _vp],
+    "fdm_attn_load_gguf": [_i, _vp, _i],
     "fdm_attn_reset": [_i],
     "fdm_attn_len": [_i, ctypes.POINTER(_i)],
     "fdm_attn_release": [_i],

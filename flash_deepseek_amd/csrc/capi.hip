@@ -1476,6 +1476,8 @@ int fdm_stream_stats(int L, uint64_t* hits, uint64_t* misses, uint64_t* bytes_re
   return FDM_OK;
 }
 
+static int tensor_to_f16(const GgufManifest& m, const GgufTensor& t, Uploader& up, uint16_t* dst, size_t n);
+
 // ---- MLA attention layers ---------------------------------------------------------------
 // yarn_freq(i) of infer.m:586-624 (YaRN correction range of the 64 rope
 // dims, base 10000, original context 4096, factor 40), in float as there.
@@ -1546,6 +1548,79 @@ int fdm_attn_upload(int L, const fdm_attn_weights* w, int max_seq) {
   (void)hipDeviceSynchronize();
   g.attn[L] = std::move(a);
   return FDM_OK;
+}
+
+int fdm_attn_load_gguf(int L, const fdm_gguf* mh, int max_seq) {
+  if (int rc = check_ready()) return rc;
+  if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
+  const GgufManifest* m = gguf_manifest(mh);
+  if (!m) return fail(FDM_E_INVAL, "null manifest");
+  const std::initializer_list<uint32_t> fp = {FDM_GGML_F32, FDM_GGML_F16, FDM_GGML_BF16};
+  const std::initializer_list<uint32_t> any = {FDM_GGML_F32, FDM_GGML_F16, FDM_GGML_BF16, FDM_GGML_Q4_K,
+                                               FDM_GGML_Q6_K};
+  char name[128];
+  auto find = [&](const char* what, const GgufTensor** out, std::initializer_list<uint32_t> types,
+                  std::initializer_list<uint64_t> dims) {
+    snprintf(name, sizeof name, "blk.%d.%s.weight", L, what);
+    return expect_tensor(*m, name, out, types, dims);
+  };
+  const GgufTensor *tn, *tqan, *tkvn, *tqa, *tqb, *tkva, *to, *tkb = nullptr, *tvb = nullptr, *tkvb = nullptr;
+  if (int rc = find("attn_norm", &tn, fp, {FDM_HIDDEN})) return rc;
+  if (int rc = find("attn_q_a_norm", &tqan, fp, {1536})) return rc;
+  if (int rc = find("attn_kv_a_norm", &tkvn, fp, {512})) return rc;
+  if (int rc = find("attn_q_a", &tqa, any, {FDM_HIDDEN, 1536})) return rc;
+  if (int rc = find("attn_q_b", &tqb, any, {1536, 128 * 192})) return rc;
+  if (int rc = find("attn_kv_a_mqa", &tkva, any, {FDM_HIDDEN, 576})) return rc;
+  if (int rc = find("attn_output", &to, any, {128 * 128, FDM_HIDDEN})) return rc;
+  // per head k_b [NOPE][KV_LORA] and v_b [V_HEAD][KV_LORA], or kv_b [NOPE + V_HEAD][KV_LORA]
+  // (infer.m:1746-1778); the element count is what the reference relies on
+  snprintf(name, sizeof name, "blk.%d.attn_k_b.weight", L);
+  const bool split = m->find(name) != nullptr;
+  if (split) {
+    if (int rc = find("attn_k_b", &tkb, any, {512, 128, 128})) return rc;
+    if (int rc = find("attn_v_b", &tvb, any, {512, 128, 128})) return rc;
+  } else if (int rc = find("attn_kv_b", &tkvb, any, {512, 256 * 128})) {
+    return rc;
+  }
+  std::vector<float> an, qan, kvn;
+  if (int rc = read_f32(*m, *tn, an)) return rc;
+  if (int rc = read_f32(*m, *tqan, qan)) return rc;
+  if (int rc = read_f32(*m, *tkvn, kvn)) return rc;
+  // the matrices, converted on the device into host arrays for fdm_attn_upload's copy
+  const size_t KB = (size_t)128 * 512 * 128;
+  std::vector<uint16_t> hqa((size_t)1536 * FDM_HIDDEN), hqb((size_t)128 * 192 * 1536), hkva((size_t)576 * FDM_HIDDEN),
+      hkb(KB), hvb(KB), ho((size_t)FDM_HIDDEN * 128 * 128);
+  uint16_t* dev = nullptr;
+  const size_t max_n = std::max(ho.size(), (size_t)2 * KB);
+  if (hipMalloc(&dev, 2 * max_n * sizeof(uint16_t)) != hipSuccess) return fail(FDM_E_NOMEM, "cannot stage attention weights");
+  std::unique_ptr<uint16_t, void (*)(uint16_t*)> keep(dev, [](uint16_t* p) { (void)hipFree(p); });
+  uint16_t* tmp = dev + max_n;
+  Uploader up;
+  if (int rc = up.init()) return rc;
+  auto plain = [&](const GgufTensor* t, std::vector<uint16_t>& h) {
+    if (int rc = tensor_to_f16(*m, *t, up, dev, h.size())) return rc;
+    FDM_HIP(hipMemcpy(h.data(), dev, h.size() * 2, hipMemcpyDeviceToHost));
+    return FDM_OK;
+  };
+  if (int rc = plain(tqa, hqa)) return rc;
+  if (int rc = plain(tqb, hqb)) return rc;
+  if (int rc = plain(tkva, hkva)) return rc;
+  if (int rc = plain(to, ho)) return rc;
+  if (split) {
+    if (int rc = tensor_to_f16(*m, *tkb, up, tmp, KB)) return rc;
+    FDM_HIP(launch_transpose_heads(tmp, (size_t)128 * 512, dev, 128, 128, 512, 0));
+    FDM_HIP(hipMemcpy(hkb.data(), dev, KB * 2, hipMemcpyDeviceToHost));
+    if (int rc = plain(tvb, hvb)) return rc;
+  } else {
+    if (int rc = tensor_to_f16(*m, *tkvb, up, tmp, 2 * KB)) return rc;
+    FDM_HIP(launch_transpose_heads(tmp, (size_t)256 * 512, dev, 128, 128, 512, 0));
+    FDM_HIP(hipMemcpy(hkb.data(), dev, KB * 2, hipMemcpyDeviceToHost));
+    FDM_HIP(hipMemcpy2D(hvb.data(), (size_t)128 * 512 * 2, tmp + (size_t)128 * 512, (size_t)256 * 512 * 2,
+                        (size_t)128 * 512 * 2, 128, hipMemcpyDeviceToHost));
+  }
+  fdm_attn_weights w = {an.data(), hqa.data(), qan.data(), hqb.data(), hkva.data(), kvn.data(),
+                        hkb.data(), hvb.data(), ho.data()};
+  return fdm_attn_upload(L, &w, max_seq);
 }
 
 int fdm_attn_reset(int L) {
@@ -1641,6 +1716,36 @@ int fdm_dense_attach(int L, const uint16_t* d_gate, const uint16_t* d_up, const 
   return dense_copy_in(L, d_gate, d_up, d_down, inter, hipMemcpyDeviceToDevice);
 }
 
+// One GGUF tensor (F32, F16, BF16, Q4_K or Q6_K) -> n F16 values at dst, as
+// dequant_tensor_f16 makes them (infer.m:530-538): the type's fp32 values
+// (the bit-exact dequant kernels for Q4_K / Q6_K), then (__fp16).
+// Synchronous; temporary device buffers are freed before it returns.
+static int tensor_to_f16(const GgufManifest& m, const GgufTensor& t, Uploader& up, uint16_t* dst, size_t n) {
+  struct Bufs {
+    void *raw = nullptr, *wide = nullptr;
+    ~Bufs() {
+      if (raw) (void)hipFree(raw);
+      if (wide) (void)hipFree(wide);
+    }
+  } b;
+  if (hipMalloc(&b.raw, t.nbytes) != hipSuccess) return fail(FDM_E_NOMEM, "cannot stage %s", t.name.c_str());
+  if (int rc = up.copy(b.raw, t.nbytes, [&](void* d, uint64_t k, uint64_t off) { return m.read(t, d, k, off); }))
+    return rc;
+  if (int rc = up.finish()) return rc;
+  if (t.type == FDM_GGML_Q4_K || t.type == FDM_GGML_Q6_K) {
+    if (hipMalloc(&b.wide, n * sizeof(float)) != hipSuccess) return fail(FDM_E_NOMEM, "cannot widen %s", t.name.c_str());
+    if (t.type == FDM_GGML_Q4_K)
+      FDM_HIP(launch_dequant_q4k(static_cast<const uint8_t*>(b.raw), static_cast<float*>(b.wide), n / FDM_QK_K, 0));
+    else
+      FDM_HIP(launch_dequant_q6k(static_cast<const uint8_t*>(b.raw), static_cast<float*>(b.wide), n / FDM_QK_K, 0));
+    FDM_HIP(launch_to_f16(b.wide, kGgmlF32, dst, n, 0));
+  } else {
+    FDM_HIP(launch_to_f16(b.raw, (int)t.type, dst, n, 0));
+  }
+  FDM_HIP(hipDeviceSynchronize());
+  return FDM_OK;
+}
+
 int fdm_dense_load_gguf(int L, const fdm_gguf* mh, int* inter_out) {
   if (int rc = check_ready()) return rc;
   if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
@@ -1669,39 +1774,10 @@ int fdm_dense_load_gguf(int L, const fdm_gguf* mh, int* inter_out) {
   DenseBuffers b;
   if (int rc = b.alloc(inter, L)) return rc;
   const size_t n = (size_t)inter * FDM_HIDDEN;
-  void *raw = nullptr, *wide = nullptr;  // the tensor's bytes; its fp32 values (Q4_K / Q6_K)
-  struct Free {
-    void** p[2];
-    ~Free() {
-      for (void** q : p)
-        if (*q) (void)hipFree(*q);
-    }
-  } free_{{&raw, &wide}};
   Uploader up;
   if (int rc = up.init()) return rc;
-  for (int i = 0; i < 3; ++i) {
-    const GgufTensor& ti = *t[i];
-    if (hipMalloc(&raw, ti.nbytes) != hipSuccess) return fail(FDM_E_NOMEM, "cannot stage %s", which[i]);
-    if (int rc = up.copy(raw, ti.nbytes, [&](void* dst, uint64_t k, uint64_t off) { return m->read(ti, dst, k, off); }))
-      return rc;
-    if (int rc = up.finish()) return rc;
-    // dequant_tensor_f16 (infer.m:530-538): the type's fp32 values, then (__fp16)
-    if (ti.type == FDM_GGML_Q4_K || ti.type == FDM_GGML_Q6_K) {
-      if (hipMalloc(&wide, n * sizeof(float)) != hipSuccess) return fail(FDM_E_NOMEM, "cannot widen %s", which[i]);
-      if (ti.type == FDM_GGML_Q4_K)
-        FDM_HIP(launch_dequant_q4k(static_cast<const uint8_t*>(raw), static_cast<float*>(wide), n / FDM_QK_K, 0));
-      else
-        FDM_HIP(launch_dequant_q6k(static_cast<const uint8_t*>(raw), static_cast<float*>(wide), n / FDM_QK_K, 0));
-      FDM_HIP(launch_to_f16(wide, kGgmlF32, b.m[i], n, 0));
-    } else {
-      FDM_HIP(launch_to_f16(raw, (int)ti.type, b.m[i], n, 0));
-    }
-    FDM_HIP(hipDeviceSynchronize());
-    FDM_HIP(hipFree(raw));
-    raw = nullptr;
-    if (wide) FDM_HIP(hipFree(wide));
-    wide = nullptr;
-  }
+  for (int i = 0; i < 3; ++i)
+    if (int rc = tensor_to_f16(*m, *t[i], up, b.m[i], n)) return rc;
   b.commit(L, inter);
   if (inter_out) *inter_out = inter;
   return FDM_OK;

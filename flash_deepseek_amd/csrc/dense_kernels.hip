@@ -164,6 +164,25 @@ __global__ __launch_bounds__(kDnWaves * 64) void k_dense_down(const uint16_t* __
   }
 }
 
+// dst[h][c][r] = src[h * head_stride + r * cols + c] for r < rows, c < cols
+// (the per-head transpose of k_b at load, infer.m:1707-1721).
+__global__ __launch_bounds__(256) void k_transpose_heads(const uint16_t* __restrict__ src, size_t head_stride,
+                                                         uint16_t* __restrict__ dst, int heads, int rows, int cols) {
+  const size_t n = (size_t)heads * rows * cols, stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const int r = (int)(i % rows);
+    const size_t hc = i / rows;
+    const int c = (int)(hc % cols), h = (int)(hc / cols);
+    dst[i] = src[(size_t)h * head_stride + (size_t)r * cols + c];
+  }
+}
+
+hipError_t launch_transpose_heads(const uint16_t* src, size_t head_stride, uint16_t* dst, int heads, int rows,
+                                  int cols, hipStream_t s) {
+  k_transpose_heads<<<4096, 256, 0, s>>>(src, head_stride, dst, heads, rows, cols);
+  return hipGetLastError();
+}
+
 hipError_t launch_to_f16(const void* src, int type, uint16_t* dst, size_t n, hipStream_t s) {
   const size_t blocks = (n + 255) / 256;
   k_to_f16<<<(unsigned)(blocks < 16384 ? (blocks ? blocks : 1) : 16384), 256, 0, s>>>(src, type, dst, n);

@@ -186,6 +186,9 @@ struct DenseArgs {
 hipError_t launch_dense_ffn(const DenseArgs& a, hipStream_t s);
 // n elements of ggml type F32 / BF16 / F16 -> F16 bits (round to nearest even)
 hipError_t launch_to_f16(const void* src, int type, uint16_t* dst, size_t n, hipStream_t s);
+// dst[h][c][r] = src[h * head_stride + r * cols + c] (F16 bits)
+hipError_t launch_transpose_heads(const uint16_t* src, size_t head_stride, uint16_t* dst, int heads, int rows,
+                                  int cols, hipStream_t s);
 
 // attn_kernels.hip: MLA attention of one decode token
 struct MlaArgs {

@@ -334,6 +334,11 @@ typedef struct fdm_attn_weights {
   const uint16_t *o_proj;  /* F16 [7168][128 * 128]                  */
 } fdm_attn_weights;
 int fdm_attn_upload(int L, const fdm_attn_weights *host_weights, int max_seq);
+/* From the model file: blk.L.attn_{norm,q_a,q_a_norm,q_b,kv_a_mqa,kv_a_norm,
+ * output}.weight and attn_k_b / attn_v_b (or attn_kv_b), converted as
+ * load_layer_weights does (infer.m:1736-1778: norms widened to fp32,
+ * matrices through dequant_tensor_f16, k_b transposed per head). */
+int fdm_attn_load_gguf(int L, const fdm_gguf *m, int max_seq);
 int fdm_attn_forward(int L, float *d_hidden, int pos, void *stream);
 int fdm_attn_reset(int L);
 int fdm_attn_len(int L, int *len);
