@@ -127,6 +127,8 @@ struct LayerSmem {
     float part[kLayerMaxSlots][kParts][kCombRows];  // combine: per-part down outputs
   };
   float red[4];
+  float cw[kLayerMaxSlots];   // combine: route() weights in slot order
+  int cperm[kLayerMaxSlots];  // combine: the expert-set slot of each
   int eid;                  // expert of the item's slot
 };
 
@@ -472,6 +474,8 @@ __device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile, Layer
   const int rr = threadIdx.x & (kCombRows - 1), p = threadIdx.x / kCombRows;
   const int r = tile * kCombRows + rr;
   const bool mine = p < kParts;
+  // the residual is read before the waits, so its load is not queued behind them
+  const float hin = (threadIdx.x < kCombRows && a.h_in) ? a.h_in[r] : 0.0f;
   float v[kLayerMaxSlots];
   poll_all(a, [&] {
     if (!mine) return true;
@@ -486,12 +490,19 @@ __device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile, Layer
     }
     return ok;
   });
-  // the exact route is finished long before the last expert output
+  // the exact route is finished long before the last expert output; its
+  // weights and slot permutation go to LDS from the loads that checked them
+  uint64_t tw = 0, tp = 0;
   poll_all(a, [&] {
     if (threadIdx.x >= a.K) return true;
-    return tag_is(get_tagged(a.route_w + threadIdx.x), a.epoch) &&
-           tag_is(get_tagged(a.route_perm + threadIdx.x), a.epoch);
+    tw = get_tagged(a.route_w + threadIdx.x);
+    tp = get_tagged(a.route_perm + threadIdx.x);
+    return tag_is(tw, a.epoch) && tag_is(tp, a.epoch);
   });
+  if (threadIdx.x < a.K) {
+    sm.cw[threadIdx.x] = tagged_f(tw);
+    sm.cperm[threadIdx.x] = tagged_i(tp);
+  }
   if (mine) {
 #pragma unroll
     for (int s = 0; s < kLayerMaxSlots; ++s)
@@ -506,12 +517,8 @@ __device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile, Layer
     return e;
   };
   float moe = 0.0f;
-  for (int k = 0; k < a.K; ++k) {
-    const int sl = tagged_i(get_tagged(a.route_perm + k));
-    moe = fmaf(tagged_f(get_tagged(a.route_w + k)), expert_out(sl), moe);
-  }
+  for (int k = 0; k < a.K; ++k) moe = fmaf(sm.cw[k], expert_out(sm.cperm[k]), moe);
   const float sd = a.n_slots > a.K ? expert_out(a.K) : 0.0f;
-  const float hin = a.h_in ? a.h_in[r] : 0.0f;
   a.out[r] = (hin + moe) + sd;
   if (a.moe_out) a.moe_out[r] = moe;
 }
