@@ -160,17 +160,32 @@ __global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x,
     // (clang contracts `ss += x[i]*x[i]`); one dependent chain, fed 16
     // values at a time from LDS so the reads run ahead of it
     float ss = 0.0f;
-    int i = 0;
-#pragma unroll 2
-    for (; i + 16 <= d; i += 16) {
-      const f32x4* r4 = reinterpret_cast<const f32x4*>(row + i);
-      const f32x4 a = r4[0], b = r4[1], c = r4[2], e = r4[3];
-      ss = fmaf(a.x, a.x, ss); ss = fmaf(a.y, a.y, ss); ss = fmaf(a.z, a.z, ss); ss = fmaf(a.w, a.w, ss);
-      ss = fmaf(b.x, b.x, ss); ss = fmaf(b.y, b.y, ss); ss = fmaf(b.z, b.z, ss); ss = fmaf(b.w, b.w, ss);
-      ss = fmaf(c.x, c.x, ss); ss = fmaf(c.y, c.y, ss); ss = fmaf(c.z, c.z, ss); ss = fmaf(c.w, c.w, ss);
-      ss = fmaf(e.x, e.x, ss); ss = fmaf(e.y, e.y, ss); ss = fmaf(e.z, e.z, ss); ss = fmaf(e.w, e.w, ss);
+    const int n64 = d / 64;
+    const f32x4* r4 = reinterpret_cast<const f32x4*>(row);
+    f32x4 buf[2][16];  // 64 values per chunk, the next chunk's reads in flight
+    if (n64 > 0) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) buf[0][k] = r4[k];
     }
-    for (; i < d; ++i) ss = fmaf(row[i], row[i], ss);
+    for (int c = 0; c < n64; c += 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        if (c + h >= n64) break;
+        if (c + h + 1 < n64) {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) buf[h ^ 1][k] = r4[16 * (c + h + 1) + k];
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const f32x4 v = buf[h][k];
+          ss = fmaf(v.x, v.x, ss);
+          ss = fmaf(v.y, v.y, ss);
+          ss = fmaf(v.z, v.z, ss);
+          ss = fmaf(v.w, v.w, ss);
+        }
+      }
+    }
+    for (int i = 64 * n64; i < d; ++i) ss = fmaf(row[i], row[i], ss);
     inv_s = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)d) + eps));
   }
   __syncthreads();
