@@ -12,7 +12,8 @@
 //   YaRN RoPE of q_rope and k_rope at pos, cache append k_mla_rope_append
 //   Q_abs[h] = k_b[h] . q_nope[h]  [128][512]           k_mv_f16_heads
 //   scores[h][s] = scale (Q_abs[h].c_kv[s] + q_rope[h].k_rope[s])   k_mla_scores
-//   p = softmax(scores[h]); wc[h] = sum_s p[h][s] c_kv[s]           k_mla_softmax_wsum
+//   p = softmax(scores[h]) in place                                  k_mla_softmax
+//   wc[h] = sum_s p[h][s] c_kv[s] (per 64-position chunk, then summed) k_mla_wsum_part/_reduce
 //   attn[h] = v_b[h] . wc[h]  [128][128]                k_mv_f16_heads
 //   hidden = residual + W_o . attn                      k_mv_f16 (+ residual)
 // The matvecs stream F16 weights (375 MB per R1 layer) once and bound the
@@ -137,32 +138,32 @@ __global__ __launch_bounds__(256) void k_mla_rope_append(float* __restrict__ q, 
 
 // scores[h][s] = scale * (Q_abs[h] . c_kv[s]) + scale * (q_rope[h] . k_rope[s])
 // for s < S (the reference's two sgemm calls, infer.m:829-838), as a tiled
-// product: workgroup (position block of 64, head block of 16); the 576 dims
+// product: workgroup (position block of 64, head block of 8); the 576 dims
 // go through LDS in 9 tiles of 64 (8 latent, 1 rope), the cache tile
 // transposed so the 64 lanes of a wave read 64 consecutive positions.
-// Thread (wave w, lane p): position p of the block, heads 4 w .. 4 w + 3.
+// Thread (wave w, lane p): position p of the block, heads 2 w, 2 w + 1.
 __global__ __launch_bounds__(256) void k_mla_scores(const float* __restrict__ q_abs, const float* __restrict__ q,
                                                     const float* __restrict__ cache_c,
                                                     const float* __restrict__ cache_k, int S, float scale,
                                                     float* __restrict__ scores) {
   __shared__ float ct[64][65];  // [dim][position], padded
-  __shared__ float qt[16][64];  // [head][dim]
-  const int s0 = blockIdx.x * 64, h0 = blockIdx.y * 16;
+  __shared__ float qt[8][64];  // [head][dim]
+  const int s0 = blockIdx.x * 64, h0 = blockIdx.y * 8;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float a[4] = {}, b[4] = {};
+  float a[2] = {}, b[2] = {};
   for (int tile = 0; tile < 9; ++tile) {
     const bool rope = tile == 8;
     __syncthreads();
     // cache tile: positions s0 .. s0 + 63, dims 64 tile .. + 63 (coalesced
     // rows); every load of the tile is issued before the first LDS store
-    float cv[16], qv[4];
+    float cv[16], qv[2];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int i = threadIdx.x + 256 * k, sp = i >> 6, d = i & 63, s = s0 + sp;
       cv[k] = s < S ? (rope ? cache_k[(size_t)s * 64 + d] : cache_c[(size_t)s * 512 + 64 * tile + d]) : 0.0f;
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 2; ++k) {
       const int i = threadIdx.x + 256 * k, h = h0 + (i >> 6), d = i & 63;
       qv[k] = rope ? q[(size_t)h * 192 + 128 + d] : q_abs[(size_t)h * 512 + 64 * tile + d];
     }
@@ -172,7 +173,7 @@ __global__ __launch_bounds__(256) void k_mla_scores(const float* __restrict__ q_
       ct[i & 63][i >> 6] = cv[k];
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < 2; ++k) {
       const int i = threadIdx.x + 256 * k;
       qt[i >> 6][i & 63] = qv[k];
     }
@@ -181,64 +182,103 @@ __global__ __launch_bounds__(256) void k_mla_scores(const float* __restrict__ q_
     for (int d = 0; d < 64; ++d) {
       const float c = ct[d][lane];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < 2; ++j) {
         if (rope)
-          b[j] = fmaf(qt[4 * wave + j][d], c, b[j]);
+          b[j] = fmaf(qt[2 * wave + j][d], c, b[j]);
         else
-          a[j] = fmaf(qt[4 * wave + j][d], c, a[j]);
+          a[j] = fmaf(qt[2 * wave + j][d], c, a[j]);
       }
     }
   }
   const int s = s0 + lane;
   if (s < S) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) scores[(size_t)(h0 + 4 * wave + j) * S + s] = scale * a[j] + scale * b[j];
+    for (int j = 0; j < 2; ++j) scores[(size_t)(h0 + 2 * wave + j) * S + s] = scale * a[j] + scale * b[j];
   }
 }
 
-// Per head (one workgroup of 512 threads each): p = softmax(scores[h][0..S))
-// (infer.m:385-389) into LDS once, then thread d: wc[h][d] = sum_s p[s] c_kv[s][d]
-// (infer.m:862-867).
-__global__ __launch_bounds__(512) void k_mla_softmax_wsum(const float* __restrict__ scores, int S,
-                                                          const float* __restrict__ cache_c,
-                                                          float* __restrict__ wc) {
-  __shared__ float ps[kMvMaxCols];  // S <= 16384
-  __shared__ float red[8];
+// Per head (one workgroup each): scores[h][0..S) <- softmax (infer.m:385-389),
+// in place.
+__global__ __launch_bounds__(256) void k_mla_softmax(float* __restrict__ scores, int S) {
+  __shared__ float red[4];
   __shared__ float stat;
   const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const float* sc = scores + (size_t)h * S;
+  float* sc = scores + (size_t)h * S;
   float m = -__builtin_inff();
-  for (int s = threadIdx.x; s < S; s += 512) m = fmaxf(m, sc[s]);
+  for (int s = threadIdx.x; s < S; s += 256) m = fmaxf(m, sc[s]);
   for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   if (lane == 0) red[wave] = m;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float v = red[0];
-    for (int i = 1; i < 8; ++i) v = fmaxf(v, red[i]);
-    stat = v;
-  }
+  if (threadIdx.x == 0) stat = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
   m = stat;
   float sum = 0.0f;
-  for (int s = threadIdx.x; s < S; s += 512) {
+  for (int s = threadIdx.x; s < S; s += 256) {
     const float e = expf(sc[s] - m);
-    ps[s] = e;
+    sc[s] = e;
     sum += e;
   }
   sum = lane_sum(sum, 64);
   __syncthreads();
   if (lane == 0) red[wave] = sum;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float v = 0.0f;
-    for (int i = 0; i < 8; ++i) v += red[i];
-    stat = 1.0f / v;
-  }
+  if (threadIdx.x == 0) stat = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
   __syncthreads();
   const float inv = stat;
-  float acc = 0.0f;
-  for (int s = 0; s < S; ++s) acc = fmaf(ps[s] * inv, cache_c[(size_t)s * 512 + threadIdx.x], acc);
-  wc[(size_t)h * 512 + threadIdx.x] = acc;
+  for (int s = threadIdx.x; s < S; s += 256) sc[s] *= inv;
+}
+
+// Partial latent sums (infer.m:862-867 as a tiled product): workgroup
+// (chunk c of 64 positions, block of 64 latent dims) reads its cache tile
+// and the 128 heads' probabilities once; thread t: dim 64 b + (t & 63),
+// heads (t >> 6) + 4 j, j < 32.  part[c][h][d] = sum over the chunk.
+__global__ __launch_bounds__(256) void k_mla_wsum_part(const float* __restrict__ p, int S,
+                                                       const float* __restrict__ cache_c,
+                                                       float* __restrict__ part) {
+  __shared__ float ct[64][64];    // [position][dim]
+  __shared__ float pt[128][65];   // [head][position], padded
+  const int c = blockIdx.x, d0 = blockIdx.y * 64, s0 = c * 64, ns = min(64, S - s0);
+  const int lane = threadIdx.x & 63, hq = threadIdx.x >> 6;
+  float cv[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int i = threadIdx.x + 256 * k, sp = i >> 6;
+    cv[k] = sp < ns ? cache_c[(size_t)(s0 + sp) * 512 + d0 + (i & 63)] : 0.0f;
+  }
+  float pv[32];
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const int i = threadIdx.x + 256 * k, h = i >> 6, sp = i & 63;
+    pv[k] = sp < ns ? p[(size_t)h * S + s0 + sp] : 0.0f;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    ct[i >> 6][i & 63] = cv[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    pt[i >> 6][i & 63] = pv[k];
+  }
+  __syncthreads();
+  float acc[32] = {};
+  for (int sp = 0; sp < 64; ++sp) {
+    const float cval = ct[sp][lane];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) acc[j] = fmaf(pt[hq + 4 * j][sp], cval, acc[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 32; ++j) part[((size_t)c * 128 + hq + 4 * j) * 512 + d0 + lane] = acc[j];
+}
+
+// wc[h][d] = sum over chunks c = 0, 1, ... of part[c][h][d] (fixed order).
+__global__ __launch_bounds__(256) void k_mla_wsum_reduce(const float* __restrict__ part, int n_chunks,
+                                                         float* __restrict__ wc) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // < 128 * 512
+  float a = 0.0f;
+  for (int c = 0; c < n_chunks; ++c) a += part[(size_t)c * 128 * 512 + i];
+  wc[i] = a;
 }
 
 hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, float* y, int rows, int cols,
@@ -264,10 +304,15 @@ hipError_t launch_mla_attend(const MlaArgs& a, hipStream_t s) {
   // Q_abs[h] = k_b[h] (512 x 128) . q_nope[h]
   if (hipError_t e = launch_mv_f16_heads(a.k_b, a.q, 192, a.q_abs, 128, 512, 128, s)) return e;
   const int S = a.len + 1;
-  k_mla_scores<<<dim3((S + 63) / 64, 128 / 16), 256, 0, s>>>(a.q_abs, a.q, a.cache_c, a.cache_k, S, a.scale,
-                                                              a.scores);
+  k_mla_scores<<<dim3((S + 63) / 64, 128 / 8), 256, 0, s>>>(a.q_abs, a.q, a.cache_c, a.cache_k, S, a.scale,
+                                                             a.scores);
   if (hipError_t e = hipGetLastError()) return e;
-  k_mla_softmax_wsum<<<128, 512, 0, s>>>(a.scores, S, a.cache_c, a.wc);
+  k_mla_softmax<<<128, 256, 0, s>>>(a.scores, S);
+  if (hipError_t e = hipGetLastError()) return e;
+  const int n_chunks = (S + 63) / 64;
+  k_mla_wsum_part<<<dim3(n_chunks, 512 / 64), 256, 0, s>>>(a.scores, S, a.cache_c, a.part);
+  if (hipError_t e = hipGetLastError()) return e;
+  k_mla_wsum_reduce<<<128 * 512 / 256, 256, 0, s>>>(a.part, n_chunks, a.wc);
   if (hipError_t e = hipGetLastError()) return e;
   // attn[h] = v_b[h] (128 x 512) . wc[h]
   return launch_mv_f16_heads(a.v_b, a.wc, 512, a.attn, 128, 128, 512, s);

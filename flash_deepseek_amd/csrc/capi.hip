@@ -134,10 +134,10 @@ struct AttnLayer {
 // Per-token scratch of the attention (grown to the largest max_seq).
 struct AttnScratch {
   float *normed = nullptr, *q_a = nullptr, *q_a_n = nullptr, *q = nullptr, *kv_a = nullptr, *c_kv_n = nullptr;
-  float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr;
+  float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr;
   int seq = 0;
   void release() {
-    for (float* p : {normed, q_a, q_a_n, q, kv_a, c_kv_n, q_abs, scores, wc, attn})
+    for (float* p : {normed, q_a, q_a_n, q, kv_a, c_kv_n, q_abs, scores, wc, attn, part})
       if (p) (void)hipFree(p);
     *this = AttnScratch();
   }
@@ -1536,9 +1536,11 @@ int fdm_attn_upload(int L, const fdm_attn_weights* w, int max_seq) {
   if (ws.seq < max_seq) {
     (void)hipDeviceSynchronize();
     ws.release();
-    const size_t n[] = {H, QA, QA, QB, KVA, 512, 128 * 512, (size_t)128 * max_seq, 128 * 512, O};
-    float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.kv_a, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn};
-    for (int i = 0; i < 10; ++i)
+    const size_t n[] = {H, QA, QA, QB, KVA, 512, 128 * 512, (size_t)128 * max_seq, 128 * 512, O,
+                        (size_t)((max_seq + 63) / 64) * 128 * 512};
+    float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.kv_a, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn,
+                   &ws.part};
+    for (int i = 0; i < 11; ++i)
       if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
         ws.release();
         return fail(FDM_E_NOMEM, "cannot allocate the attention scratch");
@@ -1678,6 +1680,7 @@ int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
   m.scores = ws.scores;
   m.wc = ws.wc;
   m.attn = ws.attn;
+  m.part = ws.part;
   m.scale = (mscale * mscale) / sqrtf(192.0f);
   FDM_HIP(launch_mla_attend(m, s));
   FDM_HIP(launch_mv_f16(a.o_proj, ws.attn, d_hidden, d_hidden, FDM_HIDDEN, 128 * 128, s));

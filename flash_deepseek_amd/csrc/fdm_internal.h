@@ -200,6 +200,7 @@ struct MlaArgs {
   float *cache_c, *cache_k;  // [max_seq][512], [max_seq][64]
   const uint16_t *k_b, *v_b;  // F16 [128][512][128], [128][128][512]
   float *q_abs, *scores, *wc, *attn;  // [128][512], [128][S], [128][512], [128][128]
+  float* part;                        // [ceil(S / 64)][128][512] partial latent sums
   float scale;
 };
 // y[r] = (res ? res[r] : 0) + W[r] . x; cols % 512 == 0, cols <= 16384
