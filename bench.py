@@ -299,6 +299,7 @@ def main():
         step(i)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    F.sync(stream)  # raises if a wait inside a layer kernel gave up
     us_per_token = elapsed / args.steps * 1e6
 
     # per-kernel durations from HIP events on the launch stream
@@ -307,6 +308,7 @@ def main():
     for i in range(args.warmup, args.warmup + args.prof_steps):
         step(i)
     torch.cuda.synchronize()
+    F.sync(stream)
     phases = {}
     for name in ("layer",):
         n, tot, mn, mx = F.prof_read(name)
@@ -329,7 +331,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4k x int8-digit dot4 -> fp32",
+        "dtype": "q4k weights x fp32 activations as three int8 digits (fp32 grade), dot4 -> fp32",
         "data": "synthetic (seeded, device-generated; no real weights)",
         "config": {
             "workload": ("DeepSeek-R1 MoE layer, batch-1 decode: fp32 router 256x7168 + "

@@ -30,7 +30,7 @@ from ._lib import (DENSE_FFN, EXPERT_Q4K_BYTES, EXPERT_Q6K_BYTES, HIDDEN, MAX_K,
                    MOE_FFN, N_EXPERTS, Q4K_BLOCK_SIZE, Q6K_BLOCK_SIZE, QK_K, FdmError)
 
 __all__ = [
-    "init", "shutdown", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
+    "init", "shutdown", "sync", "set_layer_spin_limit", "available", "dequantize_row_q4_K", "dequantize_row_q6_K",
     "fp16_to_fp32", "matvec_q4k", "matvec_q6k", "expert_ffn", "router_logits", "route",
     "attach_layer", "upload_layer", "release_layer", "layer_info", "moe_forward",
     "moe_forward_host", "moe_layer", "f32_to_f16", "upload_dense", "attach_dense", "load_dense_gguf",
@@ -69,6 +69,21 @@ def init(device=0):
 
 def shutdown():
     call("fdm_shutdown")
+
+
+def sync(stream=None):
+    """Wait for the stream's work and report what the kernels could only
+    record: raises FdmError (FDM_E_STATE) when a wait inside an earlier
+    moe_layer launch gave up, i.e. that call's result is not valid."""
+    call("fdm_stream_sync", _stream(stream))
+
+
+def set_layer_spin_limit(polls):
+    """Polls one wait inside moe_layer's kernel makes before giving up (0:
+    the default).  Returns the previous limit."""
+    prev = ctypes.c_uint32(0)
+    call("fdm_set_layer_spin_limit", polls, ctypes.byref(prev))
+    return prev.value
 
 
 def available():

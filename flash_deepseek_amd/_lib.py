@@ -58,6 +58,7 @@ SIGNATURES = {
     "fdm_last_error": [],
     "fdm_device_cus": [],
     "fdm_set_batch_kernel": [_i, ctypes.POINTER(ctypes.c_int)],
+    "fdm_set_layer_spin_limit": [_u32, ctypes.POINTER(_u32)],
     "fdm_malloc": [ctypes.POINTER(_vp), _sz],
     "fdm_free": [_vp],
     "fdm_memcpy_h2d": [_vp, _vp, _sz, _vp],

@@ -59,19 +59,19 @@ __device__ __forceinline__ int n_items_of(const BatchArgs& b, int D) {
   return D + (b.shared ? (b.T + kBShChunk - 1) / kBShChunk : 0);
 }
 
-// One token's digit records (N records of 9 x 16 bytes) held in registers,
+// One token's digit records (N records of 13 x 16 bytes) held in registers,
 // 16 bytes per thread per step: loaded while the previous token is being
 // contracted, stored to LDS after it.
 template <int N>
 struct Records {
-  static constexpr int kSteps = (N * 9 + 255) / 256;
+  static constexpr int kSteps = (N * kXGroupVec + 255) / 256;
   u32x4 v[kSteps];
   __device__ __forceinline__ void load(const XGroup* __restrict__ src) {
     const u32x4* s = reinterpret_cast<const u32x4*>(src);
 #pragma unroll
     for (int k = 0; k < kSteps; ++k) {
       const int i = threadIdx.x + 256 * k;
-      if (i < N * 9) v[k] = s[i];
+      if (i < N * kXGroupVec) v[k] = s[i];
     }
   }
   __device__ __forceinline__ void store(XGroup* __restrict__ dst) const {
@@ -79,7 +79,7 @@ struct Records {
 #pragma unroll
     for (int k = 0; k < kSteps; ++k) {
       const int i = threadIdx.x + 256 * k;
-      if (i < N * 9) d[i] = v[k];
+      if (i < N * kXGroupVec) d[i] = v[k];
     }
   }
 };

@@ -14,12 +14,14 @@
 #include <memory>
 
 #include "../../include/fdm.h"
+#include "epoch_book.h"
 #include "fdm_internal.h"
 
 namespace fdm {
 
 int g_num_cus = 0;
 int g_batch_mode = FDM_BATCH_AUTO;
+unsigned g_layer_spin_limit = kLayerSpinLimit;
 
 namespace {
 
@@ -50,8 +52,7 @@ struct Workspace {
   int* layer_cnt = nullptr;   // layer kernel arrival counters (kLayerCounters x stride)
   uint64_t* layer_tagged = nullptr;  // layer kernel tagged words (kLayerTagged)
   unsigned* layer_flags = nullptr;  // layer kernel epoch flags (kLayerFlags x stride)
-  unsigned epoch = 0;         // last epoch handed to the layer kernel
-  unsigned err_reported = 0;  // last error epoch reported by fdm_stream_sync
+  EpochBook epochs;           // layer kernel call epochs and reported timeouts
   // batched decode (fdm_moe_forward_batched); per-row buffers grow on demand
   int* b_seg = nullptr;       // [257]
   int* b_pair_tok = nullptr;  // [FDM_MAX_TOKENS * FDM_MAX_K]
@@ -708,15 +709,13 @@ int fdm_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stream) {
 int fdm_stream_sync(void* stream) {
   if (int rc = check_ready()) return rc;
   FDM_HIP(hipStreamSynchronize(as_stream(stream)));
-  if (g.ws.epoch != 0) {
+  if (g.ws.epochs.epoch != 0) {
     // the layer kernel records the epoch of a call whose waits timed out
     unsigned err = 0;
     FDM_HIP(hipMemcpy(&err, g.ws.layer_flags + kLayerFlagErr * kLayerStride, sizeof(err),
                       hipMemcpyDeviceToHost));
-    if (err != 0 && err != g.ws.err_reported) {
-      g.ws.err_reported = err;
+    if (g.ws.epochs.new_error(err))
       return fail(FDM_E_STATE, "fdm_moe_layer call %u timed out inside the kernel", err);
-    }
   }
   return FDM_OK;
 }
@@ -1131,8 +1130,8 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
   a.counters = g.ws.layer_cnt;
   a.flags = g.ws.layer_flags;
-  if (++g.ws.epoch == 0) ++g.ws.epoch;  // flags start at 0: skip epoch 0 on wrap
-  a.epoch = g.ws.epoch;
+  a.epoch = g.ws.epochs.next();
+  a.spin_limit = g_layer_spin_limit;
   {
     ProfScope p(FDM_PROF_LAYER, s);
     FDM_HIP(launch_layer(a, s));
@@ -1332,6 +1331,13 @@ int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T,
   FDM_HIP(launch_prefill_experts(q, true, s));
   if (y->down_q6) FDM_HIP(launch_batched_down(b, true, s));
   FDM_HIP(launch_combine(b, s));
+  return FDM_OK;
+}
+
+int fdm_set_layer_spin_limit(unsigned polls, unsigned* prev) {
+  if (int rc = check_ready()) return rc;
+  if (prev) *prev = g_layer_spin_limit;
+  g_layer_spin_limit = polls ? polls : kLayerSpinLimit;
   return FDM_OK;
 }
 

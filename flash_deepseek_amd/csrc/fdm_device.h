@@ -4,15 +4,20 @@
 // nibble (or 6-bit) unpack and a multiply-accumulate.  Done in fp32 that is
 // ~2.4 VALU instructions per weight, which at 8 TB/s of 4.5-bit weights
 // would keep the vector ALUs of all 256 CUs almost fully busy.  Instead the
-// activation vector x is split once per 32-element sub-block j into two
-// int8 "digits":  x ~= s_j * (a + b / 254),  s_j = max|x| / 127, a = rint(x/s_j),
-// b = rint((x/s_j - a) * 254), so |x - x'| <= max|x| / 64516 (about 1.5e-5 of
-// the sub-block's largest element).  The weights' integer quants then meet
-// the digits in v_dot4_i32_i8 (four 8-bit products per instruction, exact
-// int32 sums), and the block scales are applied once per sub-block in fp32.
-// The sub-block sums sum_j x (exact fp32) carry the Q4_K min term.
+// activation vector x is split once per 32-element sub-block j into three
+// int8 "digits" against a power-of-two scale s_j (the smallest with
+// max|x| / s_j <= 127, so x / s_j is exact):
+//   t = x / s_j,  a = rint(t),  b = rint((t - a) * 254),
+//   c = rint(((t - a) * 254 - b) * 254),
+//   x ~= s_j * (a + b / 254 + c / 254^2),  |x - x'| <= s_j / 129032
+// i.e. at most max|x| * 2^-23 per element: the precision of an fp32 product
+// relative to the sub-block's largest element.  The weights' integer quants
+// meet the digits in v_dot4_i32_i8 (four 8-bit products per instruction,
+// exact int32 sums), and the block scales are applied once per sub-block in
+// fp32.  The sub-block sums sum_j x (exact fp32 order) carry the Q4_K min
+// term.
 //
-// Digits of 64 consecutive elements live in one 144-byte record (XGroup),
+// Digits of 64 consecutive elements live in one 208-byte record (XGroup),
 // matching one Q4_K "group" (32 qs bytes = sub-blocks 2g and 2g+1).
 #pragma once
 
@@ -34,12 +39,14 @@ constexpr int kQ4KRowFfn = kFfn / kQK * kQ4KBlock;        // 1152 B: down row (Q
 constexpr int kQ6KRowFfn = kFfn / kQK * kQ6KBlock;        // 1680 B: down row (Q6_K)
 
 struct __attribute__((aligned(16))) XGroup {
-  int8_t a[64];    // high digit of elements 0..63
-  int8_t b[64];    // low digit
+  int8_t a[64];    // first digit of elements 0..63
+  int8_t b[64];    // second digit (units of 1/254)
+  int8_t c[64];    // third digit (units of 1/254^2)
   float s[2];      // digit scale of sub-blocks 0 (elements 0-31) and 1 (32-63)
-  float xsum[2];   // exact fp32 sum of the 32 elements of each sub-block
+  float xsum[2];   // fp32 sum of the 32 elements of each sub-block
 };
-static_assert(sizeof(XGroup) == 144, "XGroup must be 144 bytes");
+static_assert(sizeof(XGroup) == 208, "XGroup must be 208 bytes");
+constexpr int kXGroupVec = sizeof(XGroup) / 16;  // 16-byte vectors per record (13)
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -124,15 +131,16 @@ __device__ __forceinline__ void q4k_scale_min_pair(uint32_t s0, uint32_t s1, uin
   q4k_scale_min_pair(s0, s1, s2, q4k_scale_sel(g), sc_lo, m_lo, sc_hi, m_hi);
 }
 
-// One XGroup held in registers (36 VGPRs): digits a, b and {s0, s1, xsum0, xsum1}.
+// One XGroup held in registers (52 VGPRs): digits a, b, c and {s0, s1, xsum0, xsum1}.
 struct XDig {
-  i32x4 a0, a1, a2, a3, b0, b1, b2, b3;
+  i32x4 a0, a1, a2, a3, b0, b1, b2, b3, c0, c1, c2, c3;
   f32x4 meta;
 };
 
 __device__ __forceinline__ XDig load_xdig(const XGroup* __restrict__ xg) {
   const i32x4* av = reinterpret_cast<const i32x4*>(xg->a);
   const i32x4* bv = reinterpret_cast<const i32x4*>(xg->b);
+  const i32x4* cv = reinterpret_cast<const i32x4*>(xg->c);
   XDig x;
   x.a0 = av[0];
   x.a1 = av[1];
@@ -142,8 +150,19 @@ __device__ __forceinline__ XDig load_xdig(const XGroup* __restrict__ xg) {
   x.b1 = bv[1];
   x.b2 = bv[2];
   x.b3 = bv[3];
+  x.c0 = cv[0];
+  x.c1 = cv[1];
+  x.c2 = cv[2];
+  x.c3 = cv[3];
   x.meta = *reinterpret_cast<const f32x4*>(xg->s);
   return x;
+}
+
+// The three int32 digit sums of one sub-block, folded into units of s:
+// A + B / 254 + C / 254^2 (each sum is exact; the fold rounds twice).
+__device__ __forceinline__ float digit_fold(int A, int B, int C) {
+  constexpr float k1 = 1.0f / 254.0f, k2 = 1.0f / 64516.0f;
+  return fmaf((float)B, k1, fmaf((float)C, k2, (float)A));
 }
 
 // Dot product of one Q4_K group (qs bytes 32g..32g+31 of a block, i.e.
@@ -153,44 +172,85 @@ __device__ __forceinline__ XDig load_xdig(const XGroup* __restrict__ xg) {
 // Returns sum over the 64 elements of (d*sc*q - dmin*m) * x.
 __device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, const u32x4 q1,
                                                const Q4KScaleSel& sel, const XDig& x) {
-  const i32x4 a0 = x.a0, a1 = x.a1, a2 = x.a2, a3 = x.a3;
-  const i32x4 b0 = x.b0, b1 = x.b1, b2 = x.b2, b3 = x.b3;
-  const f32x4 meta = x.meta;
   const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-  const uint32_t alo[8] = {(uint32_t)a0.x, (uint32_t)a0.y, (uint32_t)a0.z, (uint32_t)a0.w,
-                           (uint32_t)a1.x, (uint32_t)a1.y, (uint32_t)a1.z, (uint32_t)a1.w};
-  const uint32_t ahi[8] = {(uint32_t)a2.x, (uint32_t)a2.y, (uint32_t)a2.z, (uint32_t)a2.w,
-                           (uint32_t)a3.x, (uint32_t)a3.y, (uint32_t)a3.z, (uint32_t)a3.w};
-  const uint32_t blo[8] = {(uint32_t)b0.x, (uint32_t)b0.y, (uint32_t)b0.z, (uint32_t)b0.w,
-                           (uint32_t)b1.x, (uint32_t)b1.y, (uint32_t)b1.z, (uint32_t)b1.w};
-  const uint32_t bhi[8] = {(uint32_t)b2.x, (uint32_t)b2.y, (uint32_t)b2.z, (uint32_t)b2.w,
-                           (uint32_t)b3.x, (uint32_t)b3.y, (uint32_t)b3.z, (uint32_t)b3.w};
-  int A0 = 0, B0 = 0, A1 = 0, B1 = 0;
+  const uint32_t alo[8] = {(uint32_t)x.a0.x, (uint32_t)x.a0.y, (uint32_t)x.a0.z, (uint32_t)x.a0.w,
+                           (uint32_t)x.a1.x, (uint32_t)x.a1.y, (uint32_t)x.a1.z, (uint32_t)x.a1.w};
+  const uint32_t ahi[8] = {(uint32_t)x.a2.x, (uint32_t)x.a2.y, (uint32_t)x.a2.z, (uint32_t)x.a2.w,
+                           (uint32_t)x.a3.x, (uint32_t)x.a3.y, (uint32_t)x.a3.z, (uint32_t)x.a3.w};
+  const uint32_t blo[8] = {(uint32_t)x.b0.x, (uint32_t)x.b0.y, (uint32_t)x.b0.z, (uint32_t)x.b0.w,
+                           (uint32_t)x.b1.x, (uint32_t)x.b1.y, (uint32_t)x.b1.z, (uint32_t)x.b1.w};
+  const uint32_t bhi[8] = {(uint32_t)x.b2.x, (uint32_t)x.b2.y, (uint32_t)x.b2.z, (uint32_t)x.b2.w,
+                           (uint32_t)x.b3.x, (uint32_t)x.b3.y, (uint32_t)x.b3.z, (uint32_t)x.b3.w};
+  const uint32_t clo[8] = {(uint32_t)x.c0.x, (uint32_t)x.c0.y, (uint32_t)x.c0.z, (uint32_t)x.c0.w,
+                           (uint32_t)x.c1.x, (uint32_t)x.c1.y, (uint32_t)x.c1.z, (uint32_t)x.c1.w};
+  const uint32_t chi[8] = {(uint32_t)x.c2.x, (uint32_t)x.c2.y, (uint32_t)x.c2.z, (uint32_t)x.c2.w,
+                           (uint32_t)x.c3.x, (uint32_t)x.c3.y, (uint32_t)x.c3.z, (uint32_t)x.c3.w};
+  int A0 = 0, B0 = 0, C0 = 0, A1 = 0, B1 = 0, C1 = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t lo = w[i] & 0x0F0F0F0Fu;
     const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
     A0 = sdot4(lo, alo[i], A0);
     B0 = sdot4(lo, blo[i], B0);
+    C0 = sdot4(lo, clo[i], C0);
     A1 = sdot4(hi, ahi[i], A1);
     B1 = sdot4(hi, bhi[i], B1);
+    C1 = sdot4(hi, chi[i], C1);
   }
   int sc0, m0, sc1, m1;
   q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, sel, sc0, m0, sc1, m1);
   const float d = half_to_float(hdr.x);
   const float dmin = half_to_float(hdr.x >> 16);
-  const float k254 = 1.0f / 254.0f;
-  const float f0 = meta.x * fmaf((float)B0, k254, (float)A0);
-  const float f1 = meta.y * fmaf((float)B1, k254, (float)A1);
+  const f32x4 meta = x.meta;
+  const float f0 = meta.x * digit_fold(A0, B0, C0);
+  const float f1 = meta.y * digit_fold(A1, B1, C1);
   const float qx = fmaf((float)sc0, f0, (float)sc1 * f1);
   const float mx = fmaf((float)m0, meta.z, (float)m1 * meta.w);
   return fmaf(d, qx, -dmin * mx);
 }
 
+// The same from a record in LDS, read in quarters (qs bytes 0-15, then
+// 16-31, each with the digits of its low-nibble and then of its high-nibble
+// elements), so at most 12 registers of digits are live at a time.
 __device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, const u32x4 q1,
                                                const Q4KScaleSel& sel,
                                                const XGroup* __restrict__ xg) {
-  return q4k_group_dot(hdr, q0, q1, sel, load_xdig(xg));
+  const i32x4* av = reinterpret_cast<const i32x4*>(xg->a);
+  const i32x4* bv = reinterpret_cast<const i32x4*>(xg->b);
+  const i32x4* cv = reinterpret_cast<const i32x4*>(xg->c);
+  int A[2] = {0, 0}, B[2] = {0, 0}, C[2] = {0, 0};
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      // n = 0: low nibbles (sub-block 0, digits 16h..16h+15); n = 1: high
+      // nibbles (sub-block 1, digits 32 + 16h ..)
+      const u32x4 q = h ? q1 : q0;
+      const i32x4 a = av[2 * n + h], b = bv[2 * n + h], c = cv[2 * n + h];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t v = n ? (q[i] >> 4) & 0x0F0F0F0Fu : q[i] & 0x0F0F0F0Fu;
+        A[n] = sdot4(v, (uint32_t)a[i], A[n]);
+        B[n] = sdot4(v, (uint32_t)b[i], B[n]);
+        C[n] = sdot4(v, (uint32_t)c[i], C[n]);
+      }
+      // the sums are complete here: the quarter's digits are dead before
+      // the next quarter's are read
+      __asm__ volatile("" : "+v"(A[n]), "+v"(B[n]), "+v"(C[n]));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  const int A0 = A[0], B0 = B[0], C0 = C[0], A1 = A[1], B1 = B[1], C1 = C[1];
+  const f32x4 meta = *reinterpret_cast<const f32x4*>(xg->s);
+  int sc0, m0, sc1, m1;
+  q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, sel, sc0, m0, sc1, m1);
+  const float d = half_to_float(hdr.x);
+  const float dmin = half_to_float(hdr.x >> 16);
+  const float f0 = meta.x * digit_fold(A0, B0, C0);
+  const float f1 = meta.y * digit_fold(A1, B1, C1);
+  const float qx = fmaf((float)sc0, f0, (float)sc1 * f1);
+  const float mx = fmaf((float)m0, meta.z, (float)m1 * meta.w);
+  return fmaf(d, qx, -dmin * mx);
 }
 
 // Broadcast lane `src` of each group of four lanes to the whole quad (DPP
@@ -298,12 +358,15 @@ __device__ __forceinline__ float q6k_half_dot(const uint32_t* ql, const uint32_t
                                               const XGroup* __restrict__ x1) {
   const uint32_t* a0 = reinterpret_cast<const uint32_t*>(x0->a);
   const uint32_t* b0 = reinterpret_cast<const uint32_t*>(x0->b);
+  const uint32_t* c0 = reinterpret_cast<const uint32_t*>(x0->c);
   const uint32_t* a1 = reinterpret_cast<const uint32_t*>(x1->a);
   const uint32_t* b1 = reinterpret_cast<const uint32_t*>(x1->b);
+  const uint32_t* c1 = reinterpret_cast<const uint32_t*>(x1->c);
   // acc[quarter][scale half]: quarter k covers elements 32k..32k+31 of the
   // half (k = 0..3); scale half = l / 16.
   int A[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
   int B[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
+  int C[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int s = i >> 2;
@@ -316,14 +379,17 @@ __device__ __forceinline__ float q6k_half_dot(const uint32_t* ql, const uint32_t
     const uint32_t v3 = (((wl2 >> 2) & 0x3C3C3C3Cu) | (wh & 0xC0C0C0C0u)) ^ 0x80808080u;
     A[0][s] = sdot4(v0, a0[i], A[0][s]);
     B[0][s] = sdot4(v0, b0[i], B[0][s]);
+    C[0][s] = sdot4(v0, c0[i], C[0][s]);
     A[1][s] = sdot4(v1, a0[8 + i], A[1][s]);
     B[1][s] = sdot4(v1, b0[8 + i], B[1][s]);
+    C[1][s] = sdot4(v1, c0[8 + i], C[1][s]);
     A[2][s] = sdot4(v2, a1[i], A[2][s]);
     B[2][s] = sdot4(v2, b1[i], B[2][s]);
+    C[2][s] = sdot4(v2, c1[i], C[2][s]);
     A[3][s] = sdot4(v3, a1[8 + i], A[3][s]);
     B[3][s] = sdot4(v3, b1[8 + i], B[3][s]);
+    C[3][s] = sdot4(v3, c1[8 + i], C[3][s]);
   }
-  const float k254 = 1.0f / 254.0f;
   const float xs[4] = {x0->s[0], x0->s[1], x1->s[0], x1->s[1]};
   float acc = 0.0f;
 #pragma unroll
@@ -333,9 +399,11 @@ __device__ __forceinline__ float q6k_half_dot(const uint32_t* ql, const uint32_t
     const int sh = (k & 1) * 16;
     const int sa = (int)(int8_t)((word >> sh) & 0xFF);
     const int sb = (int)(int8_t)((word >> (sh + 8)) & 0xFF);
+    // |sc * sum| < 2^31: 128 * 16 * 128 * 127 per scale half
     const int ia = sa * A[k][0] + sb * A[k][1];
     const int ib = sa * B[k][0] + sb * B[k][1];
-    acc = fmaf(xs[k], fmaf((float)ib, k254, (float)ia), acc);
+    const int ic = sa * C[k][0] + sb * C[k][1];
+    acc = fmaf(xs[k], digit_fold(ia, ib, ic), acc);
   }
   return acc * 0.25f;
 }
@@ -430,30 +498,42 @@ __device__ __forceinline__ float half_reduce(float v) {
 
 // Digits of the 32 elements of one sub-block.  Called by all 64 lanes of a
 // wave; each half-wave (lanes 0-31, 32-63) is one sub-block and each lane
-// holds one element v.  Returns the a / b digits for the lane and the
+// holds one element v.  Returns the a / b / c digits for the lane and the
 // sub-block's scale and fp32 sum (summed in one fixed order, so every
 // caller gets the same bits for the same elements).
-__device__ __forceinline__ void make_digits32(float v, int8_t& a_out, int8_t& b_out,
-                                              float& s_out, float& sum_out) {
+//   s = 2^e, the smallest power of two with max|v| / s <= 127: t = v / s is
+//   exact, a = rint(t), r = t - a (exact), b = rint(254 r), u = 254 r - b
+//   (one rounding, by fma), c = rint(254 u).  |t - (a + b/254 + c/254^2)|
+//   <= (0.5 + 2^-17) / 254^2.
+__device__ __forceinline__ void make_digits3(float v, int8_t& a_out, int8_t& b_out, int8_t& c_out,
+                                             float& s_out, float& sum_out) {
   const float amax = half_reduce<true>(fabsf(v));
   const float sum = half_reduce<false>(v);
-  int a = 0, b = 0;
+  int a = 0, b = 0, c = 0;
   float s;
   if (amax > 0.0f && amax <= 3.4028234e38f) {
-    const float inv = 127.0f / amax;
-    s = amax / 127.0f;
-    const float t = v * inv;
-    float ra = rintf(t);
-    ra = fminf(fmaxf(ra, -127.0f), 127.0f);
-    const float rb = fminf(fmaxf(rintf((t - ra) * 254.0f), -127.0f), 127.0f);
+    // amax = m * 2^E, m in [1, 2): s = 2^(E - 6) unless m > 127/64, then 2^(E - 5)
+    int E;
+    const float m = frexpf(amax, &E);  // amax = m * 2^E, m in [0.5, 1)
+    int e = E - 7;                     // amax / 2^e = 128 m in [64, 128)
+    if (m * 128.0f > 127.0f) e += 1;   // keep max |t| <= 127
+    s = ldexpf(1.0f, e);
+    const float t = ldexpf(v, -e);  // exact: a power-of-two scaling of a normal result
+    const float ra = rintf(t);
+    const float r = t - ra;         // exact, |r| <= 0.5
+    const float rb = rintf(r * 254.0f);
+    const float u = fmaf(r, 254.0f, -rb);  // |u| <= 0.5 + 2^-17
+    const float rc = fminf(fmaxf(rintf(u * 254.0f), -127.0f), 127.0f);
     a = (int)ra;
     b = (int)rb;
+    c = (int)rc;
   } else {
     // all zero: s = 0 gives exact zeros; inf/NaN: propagate a NaN scale
     s = (amax == 0.0f) ? 0.0f : __builtin_nanf("");
   }
   a_out = (int8_t)a;
   b_out = (int8_t)b;
+  c_out = (int8_t)c;
   s_out = s;
   sum_out = sum;
 }

@@ -106,7 +106,9 @@ struct LayerArgs {
   int* counters;           // kLayerCounters x kLayerStride ints, zero at first use
   unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
   unsigned epoch;          // non-zero, different from every earlier call's
+  unsigned spin_limit;     // polls before a wait gives up (kLayerSpinLimit)
 };
+constexpr unsigned kLayerSpinLimit = 1u << 17;  // polls of one wait (each >= ~1 us)
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
 
 // batched_kernels.hip

@@ -93,7 +93,6 @@ static_assert(kHidden % kDnRowsQ4 == 0 && kHidden % kDnRowsQ6 == 0, "down items 
 __host__ __device__ constexpr int dn_per_part(bool q6) { return kHidden / (q6 ? kDnRowsQ6 : kDnRowsQ4); }
 constexpr int kCombRows = 32;                // rows per combine tile
 constexpr int kCombTiles = kHidden / kCombRows;       // 224
-constexpr unsigned kSpinLimit = 1u << 17;    // polls of one wait (each >= ~1 us)
 
 // flag and counter slots (units of kStride)
 constexpr int kFlagXd = 0;
@@ -133,7 +132,7 @@ struct LayerSmem {
 };
 
 // Whole-workgroup wait: every thread runs try_once() (its share of the
-// loads and checks) until all of them succeed.  Gives up after kSpinLimit
+// loads and checks) until all of them succeed.  Gives up after a.spin_limit
 // rounds, or when another workgroup already gave up (looked at every 64th
 // round: each look is one more round trip), recording the epoch in the
 // error flag.  Returns false on giving up.
@@ -143,8 +142,8 @@ __device__ __forceinline__ bool poll_all(const LayerArgs& a, F&& try_once) {
   for (unsigned n = 0;; ++n) {
     if (__syncthreads_and(try_once())) return true;
     int give_up = 0;
-    if (threadIdx.x == 0 && (n & 63) == 63)
-      give_up = n >= kSpinLimit || load_u32_agent(err) == a.epoch;
+    if (threadIdx.x == 0)
+      give_up = n >= a.spin_limit || ((n & 63) == 63 && load_u32_agent(err) == a.epoch);
     if (__syncthreads_or(give_up)) {
       if (threadIdx.x == 0) store_u32_agent(err, a.epoch);
       return false;
@@ -179,11 +178,12 @@ __device__ __forceinline__ void wait_route_xd(const LayerArgs& a, int slot, bool
 // record g (two sub-blocks of 32, one per half-wave).
 __device__ __forceinline__ void digits_to_lds(float v, XGroup& g) {
   const int lane = threadIdx.x & 63;
-  int8_t da, db;
+  int8_t da, db, dc;
   float ds, dsum;
-  make_digits32(v, da, db, ds, dsum);
+  make_digits3(v, da, db, dc, ds, dsum);
   g.a[lane] = da;
   g.b[lane] = db;
+  g.c[lane] = dc;
   if ((lane & 31) == 0) {
     g.s[lane >> 5] = ds;
     g.xsum[lane >> 5] = dsum;
@@ -196,19 +196,20 @@ __device__ __forceinline__ void digits_to_lds(float v, XGroup& g) {
 __device__ __forceinline__ void xd_item(const LayerArgs& a, int i) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = 4 * i + wave;
-  int8_t da, db;
+  int8_t da, db, dc;
   float ds, dsum;
-  make_digits32(a.h[64 * G + lane], da, db, ds, dsum);
-  const unsigned ua = (uint8_t)da, ub = (uint8_t)db;
+  make_digits3(a.h[64 * G + lane], da, db, dc, ds, dsum);
   const int l = lane & 31, sub = lane >> 5;
-  const unsigned wa = ua | (__shfl_down(ua, 1, 32) << 8) | (__shfl_down(ua, 2, 32) << 16) |
-                      (__shfl_down(ua, 3, 32) << 24);
-  const unsigned wb = ub | (__shfl_down(ub, 1, 32) << 8) | (__shfl_down(ub, 2, 32) << 16) |
-                      (__shfl_down(ub, 3, 32) << 24);
+  auto pack4 = [](int8_t d) {
+    const unsigned u = (uint8_t)d;
+    return u | (__shfl_down(u, 1, 32) << 8) | (__shfl_down(u, 2, 32) << 16) | (__shfl_down(u, 3, 32) << 24);
+  };
+  const unsigned wa = pack4(da), wb = pack4(db), wc = pack4(dc);
   XGroup* xg = a.xd + G;
   if ((l & 3) == 0) {
     store_u32_agent(reinterpret_cast<unsigned*>(xg->a) + 8 * sub + l / 4, wa);
     store_u32_agent(reinterpret_cast<unsigned*>(xg->b) + 8 * sub + l / 4, wb);
+    store_u32_agent(reinterpret_cast<unsigned*>(xg->c) + 8 * sub + l / 4, wc);
   }
   if (l == 0) {
     store_agent(&xg->s[sub], ds);
@@ -423,7 +424,11 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
       const Q4KScaleSel sel = q4k_scale_sel(gl & 3);
 #pragma unroll
       for (int j = 0; j < kDnRowsQ4L; ++j) {
-        acc[j] = q4k_group_dot_ld(ld[j], sel, &sm.xs[gl]);
+        // re-read the digits per row: held across the seven rows they
+        // would take 52 more registers than the 128 of four waves per SIMD
+        int gi = gl;
+        __asm__ volatile("" : "+v"(gi));
+        acc[j] = q4k_group_dot_ld(ld[j], sel, &sm.xs[gi]);
         __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
       }
     }
@@ -451,7 +456,9 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
     if (blob) {
 #pragma unroll
       for (int j = 0; j < kDnRowsQ6L; ++j) {
-        acc[j] = q6k_half_dot_ld(l6[j], &sm.xs[2 * gl]);
+        int gi = 2 * gl;
+        __asm__ volatile("" : "+v"(gi));
+        acc[j] = q6k_half_dot_ld(l6[j], &sm.xs[gi]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }

@@ -7,7 +7,7 @@
 // in_dim/64 "groups" (a quarter block: 32 qs bytes + the block header), lane
 // l of the row takes groups l, l+16, l+32, ... so one 16-byte load per lane
 // covers the row contiguously across the 16 lanes.  The activation digits
-// of the whole x (in_dim/64 records of 144 bytes) are staged in LDS once
+// of the whole x (in_dim/64 records of 208 bytes) are staged in LDS once
 // per workgroup; every row of the workgroup reads them from there.  The
 // 16-lane partial sums are reduced with xor shuffles.
 #include "fdm_internal.h"
@@ -22,12 +22,13 @@ __global__ __launch_bounds__(256) void k_xdigits(const float* __restrict__ x, si
   const size_t G = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
   if (G >= n_groups) return;  // whole wave exits together
   const float v = x[G * 64 + lane];
-  int8_t a, b;
+  int8_t a, b, c;
   float s, sum;
-  make_digits32(v, a, b, s, sum);
+  make_digits3(v, a, b, c, s, sum);
   XGroup* g = xd + G;
   g->a[lane] = a;
   g->b[lane] = b;
+  g->c[lane] = c;
   if ((lane & 31) == 0) {
     g->s[lane >> 5] = s;
     g->xsum[lane >> 5] = sum;
@@ -38,7 +39,7 @@ __device__ __forceinline__ void stage_xgroups(XGroup* __restrict__ dst,
                                               const XGroup* __restrict__ src, int n) {
   const u32x4* s = reinterpret_cast<const u32x4*>(src);
   u32x4* d = reinterpret_cast<u32x4*>(dst);
-  for (int i = threadIdx.x; i < n * 9; i += blockDim.x) d[i] = s[i];
+  for (int i = threadIdx.x; i < n * kXGroupVec; i += blockDim.x) d[i] = s[i];
 }
 
 // GPL = groups per lane (in_dim / 1024) when known at compile time, 0 for

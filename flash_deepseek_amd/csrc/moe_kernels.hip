@@ -35,7 +35,7 @@ __device__ __forceinline__ void stage_groups(XGroup* __restrict__ dst,
                                              const XGroup* __restrict__ src, int n) {
   const u32x4* s = reinterpret_cast<const u32x4*>(src);
   u32x4* d = reinterpret_cast<u32x4*>(dst);
-  for (int i = threadIdx.x; i < n * 9; i += blockDim.x) d[i] = s[i];
+  for (int i = threadIdx.x; i < n * kXGroupVec; i += blockDim.x) d[i] = s[i];
 }
 
 constexpr int kGuRows = 8;                 // rows of gate (and up) per workgroup
@@ -86,13 +86,14 @@ __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __res
     if (threadIdx.x < 32) {
       const int base = (tile >> 2) * 32;
       const float v = load_agent(act + (size_t)slot * kFfn + base + threadIdx.x);
-      int8_t a, b;
+      int8_t a, b, c;
       float s, sum;
-      make_digits32(v, a, b, s, sum);
+      make_digits3(v, a, b, c, s, sum);
       XGroup* xg = act_xd + (size_t)slot * (kFfn / 64) + (tile >> 3);
       const int half = (tile >> 2) & 1;
       xg->a[32 * half + threadIdx.x] = a;
       xg->b[32 * half + threadIdx.x] = b;
+      xg->c[32 * half + threadIdx.x] = c;
       if (threadIdx.x == 0) {
         xg->s[half] = s;
         xg->xsum[half] = sum;

@@ -240,6 +240,14 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
 
+/* ---- the polls one wait inside fdm_moe_layer's kernel makes before it gives
+ * up (no counterpart in the reference, whose Metal waits are host-side,
+ * infer.m:1681).  0 restores the default (2^17 polls of >= ~1 us each).  A
+ * small limit makes the waits give up from the host side -- every workgroup
+ * still exits normally -- so the FDM_E_STATE report of fdm_stream_sync can be
+ * exercised.  *prev (optional) receives the previous limit. */
+int fdm_set_layer_spin_limit(unsigned polls, unsigned *prev);
+
 /* ---- batched decode: T tokens through the MoE branch of layer L in one
  * step, with token -> expert dispatch so that each selected expert's weights
  * are read once per step (config 3; the reference decodes one token at a

@@ -161,6 +161,19 @@ def expert_ffn(blob, down_is_q6, x, with_intermediates=False):
     return out
 
 
+def expert_ffn_f32(blob, down_is_q6, x):
+    """expert_worker (infer.m:1069-1091) in the reference's own precision:
+    fp32 dequant, fp32 dot products summed in index order, silu_mul in fp32
+    (infer.m:378-383).  The yardstick for "fp32 grade" errors."""
+    blob = np.ascontiguousarray(blob, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = matvec(blob[:GATE_BYTES], x, FFN, HIDDEN, "q4k", f32=True)
+    u = matvec(blob[GATE_BYTES:2 * GATE_BYTES], x, FFN, HIDDEN, "q4k", f32=True)
+    a = np.empty(FFN, dtype=np.float32)
+    L.orc_silu_mul(g, u, a, FFN)
+    return matvec(blob[2 * GATE_BYTES:], a, HIDDEN, FFN, "q6k" if down_is_q6 else "q4k", f32=True)
+
+
 def fp32_to_fp16(x):
     """(__fp16)x elementwise (infer.m:521-528): uint16 bits."""
     x = np.ascontiguousarray(x, dtype=np.float32)

@@ -36,6 +36,15 @@ def fdm():
     return F
 
 
+@pytest.fixture(autouse=True)
+def _kernel_waits_completed(request):
+    """After every test that used the library: no wait inside a layer kernel
+    gave up during it (fdm_stream_sync reports such a call once)."""
+    yield
+    if "fdm" in request.fixturenames:
+        request.getfixturevalue("fdm").sync()
+
+
 @pytest.fixture(scope="session")
 def golden():
     import numpy as np

@@ -1,6 +1,8 @@
 """Fused dequant matvecs (fdm_matvec_q4k / _q6k) against the oracle's
 bit-exact dequantisation with a float64 dot product.  Tolerance: 1e-3
-relative L2 (the bar for floating-point outputs)."""
+relative L2 (the bar for floating-point outputs), and fp32 grade: the error
+against float64 at most 4x that of the reference's own arithmetic (fp32
+products summed in fp32, shaders.metal:93-99), restated by the oracle."""
 import numpy as np
 import pytest
 
@@ -47,6 +49,42 @@ def test_matvec_heavy_tailed_input(fdm, oracle):
     x[::97] *= 50
     err = rel_l2(run(fdm, False, raw, x, rows, cols), oracle.matvec(raw, x, rows, cols))
     assert err <= TOL
+
+
+def activations(kind, n, seed):
+    """N(0,1); heavy-tailed (a product of normals, a few huge entries); or one
+    outlier of +-1e3 in every 32-element sub-block among N(0,1) values."""
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        return rng.standard_normal(n).astype(np.float32)
+    if kind == "heavy":
+        x = rng.standard_normal(n) * rng.standard_normal(n) * 300
+        x[::97] *= 50
+        return x.astype(np.float32)
+    x = rng.standard_normal(n)
+    x[rng.integers(0, 32, n // 32) + 32 * np.arange(n // 32)] = 1e3 * rng.choice([-1.0, 1.0], n // 32)
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("kind", ["normal", "heavy", "outlier"])
+@pytest.mark.parametrize("q6,rows,cols", [(False, 2048, 7168), (False, 7168, 2048), (True, 7168, 2048)])
+def test_matvec_fp32_grade(fdm, oracle, q6, rows, cols, kind):
+    """The activation digits keep the dot products at fp32 grade: both the
+    relative L2 error and the largest per-row error against float64 stay
+    within 4x of the fp32 restatement's."""
+    say(f"matvec fp32 grade q6={q6} rows={rows} cols={cols} input={kind}")
+    nb = rows * cols // 256
+    qt = "q6k" if q6 else "q4k"
+    raw = oracle.synth_q6k(nb, 31 + rows) if q6 else oracle.synth_q4k(nb, 31 + rows)
+    x = activations(kind, cols, rows + cols)
+    got = run(fdm, q6, raw, x, rows, cols).astype(np.float64)
+    want = oracle.matvec(raw, x, rows, cols, qt).astype(np.float64)
+    f32 = oracle.matvec(raw, x, rows, cols, qt, f32=True).astype(np.float64)
+    e_got, e_f32 = rel_l2(got, want), rel_l2(f32, want)
+    m_got, m_f32 = np.abs(got - want).max(), np.abs(f32 - want).max()
+    print(f"rel_l2 {e_got:.3e} (fp32 {e_f32:.3e}), max {m_got:.3e} (fp32 {m_f32:.3e})")
+    assert e_got <= 4 * e_f32
+    assert m_got <= 4 * m_f32
 
 
 def test_matvec_zero_input_gives_zero(fdm, oracle):

@@ -64,6 +64,26 @@ def test_moe_layer(fdm, oracle, layer, K, tok):
     assert err <= TOL and err_moe <= TOL
 
 
+def test_moe_layer_fp32_grade(fdm, oracle, layer):
+    """The MoE part of the layer (sum_k w_k E_k + S) against float64: within
+    4x the error of the same sum in the reference's fp32 arithmetic."""
+    L, lay = layer
+    K = 8
+    h_in, got, gi, gw, ri, rw, moe, sd, want = run_layer(fdm, oracle, L, lay, K, 5)
+    f32 = np.zeros(7168, np.float32)
+    for k in range(K):
+        f32 += rw[k] * oracle.expert_ffn_f32(lay.expert_bytes(int(ri[k])), lay.down_q6, lay_h(oracle, 5))
+    f32 += oracle.expert_ffn_f32(lay.expert_bytes(-1), lay.down_q6, lay_h(oracle, 5))
+    e_got = rel_l2(got.astype(np.float64) - h_in, moe + sd)
+    e_f32 = rel_l2(f32, moe + sd)
+    print(f"moe part rel_l2 {e_got:.3e} (fp32 restatement {e_f32:.3e})")
+    assert e_got <= 4 * e_f32
+
+
+def lay_h(oracle, tok):
+    return oracle.synth_normal(7168, 0.0, 1.0, 500 + tok)
+
+
 @pytest.mark.parametrize("K", [5, 7])
 def test_moe_layer_tied_set(fdm, oracle, layer, K):
     """Every router row and bias duplicated in adjacent experts (same group):
@@ -110,6 +130,31 @@ def test_moe_forward_given_routing(fdm, oracle, layer):
     host_out = np.empty(7168, np.float32)
     fdm.moe_forward_host(L, h, ids, ws, K, host_out)
     assert np.array_equal(host_out, to_host(out))
+
+
+def test_layer_wait_timeout_is_reported(fdm, oracle, layer):
+    """A launch whose kernel waits give up (forced from the host with a limit
+    of one poll; every workgroup still exits) is reported once by sync(),
+    and the next launch computes correctly again."""
+    L, lay = layer
+    fdm.sync()
+    h = oracle.synth_normal(7168, 0.0, 1.0, 42)
+    out = empty_f32(7168)
+    prev = fdm.set_layer_spin_limit(1)
+    try:
+        say(f"moe_layer L={L} with a one-poll wait limit")
+        fdm.moe_layer(L, to_dev(h), None, 8, out)
+        with pytest.raises(fdm.FdmError) as err:
+            fdm.sync()
+        assert err.value.code == -4  # FDM_E_STATE
+        fdm.sync()  # reported once
+    finally:
+        fdm.set_layer_spin_limit(prev)
+    say(f"moe_layer L={L} with the default wait limit")
+    fdm.moe_layer(L, to_dev(h), None, 8, out)
+    fdm.sync()
+    ri, rw, moe, sd, want = oracle_layer(oracle, lay, h, np.zeros(7168, np.float32), 8)
+    assert rel_l2(to_host(out), want) <= TOL
 
 
 def test_errors(fdm, layer):
