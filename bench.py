@@ -268,7 +268,11 @@ def main():
     for l in range(args.layers):
         lay = make_layer(1 + l, down_q6=(args.down == "q6k"))
         F.attach_layer(3 + l, lay.experts, lay.expert_size, lay.Wg, lay.bias, lay.shared)
+        # the library keeps its own resident copy of the experts; the router
+        # weights and bias stay borrowed from `lay`
+        lay.experts = lay.shared = None
         layers.append(lay)
+    torch.cuda.empty_cache()
     n_tok = args.warmup + max(args.steps, args.prof_steps)
     h_post = make_tokens(n_tok, 7001)
     h_in = make_tokens(n_tok, 7002)

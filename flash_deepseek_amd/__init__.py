@@ -170,14 +170,14 @@ def moe_forward_host(L, h_post, exp_idx, exp_w, K, moe_out):
 
 
 BATCH_AUTO, BATCH_DOT4, BATCH_MFMA = 0, 1, 2
-BATCH_MFMA_MIN_T = 96
+BATCH_MFMA_MIN_T = 6
 
 
 def set_batch_kernel(mode):
     """Expert kernels behind moe_forward_batched: BATCH_DOT4 (per-token int8
-    digit dot products), BATCH_MFMA (grouped GEMMs on MFMA, bf16 hi/lo pairs)
-    or BATCH_AUTO (MFMA from BATCH_MFMA_MIN_T tokens).  Returns the previous
-    mode."""
+    digit dot products), BATCH_MFMA (grouped GEMMs on MFMA, three fp16 planes
+    of the activations) or BATCH_AUTO (MFMA from BATCH_MFMA_MIN_T tokens).
+    Returns the previous mode."""
     prev = ctypes.c_int(-1)
     call("fdm_set_batch_kernel", mode, ctypes.byref(prev))
     return prev.value

@@ -26,6 +26,7 @@ SOURCES = [
     "layer_kernel.hip",
     "batched_kernels.hip",
     "prefill_kernels.hip",
+    "gemm_kernels.hip",
     "synth_kernels.hip",
     "dense_kernels.hip",
     "expert_stream.hip",

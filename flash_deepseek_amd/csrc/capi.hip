@@ -63,12 +63,18 @@ struct Workspace {
   float* b_act = nullptr;     // [b_rows][2048]
   XGroup* b_act_xd = nullptr; // [b_rows][32]
   float* b_eo = nullptr;      // [b_rows][7168]
+  // grouped GEMMs (batched decode, prefill): activation planes of the GEMM
+  // inputs, grown on demand
+  size_t q_elems = 0;         // elements per plane the buffers below hold (x 3 planes)
+  _Float16* q_planes = nullptr;  // [3][q_elems]
+  float* q_xs = nullptr;      // [q_elems / 32] sub-block sums
+  float* q_xe = nullptr;      // [q_rows] row scales
+  size_t q_rows = 0;
+  int4* q_chunks = nullptr;   // chunk list (kQMaxChunks)
+  int* q_nchunks = nullptr;   // [1]
   // prefill (fdm_moe_prefill)
-  int p_tokens = 0;           // tokens the buffers below hold
+  int p_tokens = 0;           // tokens the buffer below holds
   float* p_hpost = nullptr;   // [p_tokens][7168] rms_norm output
-  __bf16* p_xb = nullptr;     // 2 x [p_tokens][7168]: its bf16 pair (hi, lo)
-  size_t p_rows = 0;
-  __bf16* p_actb = nullptr;   // [p_rows][2048]
   float* w = nullptr;         // FDM_MAX_TOKENS x 16
   float* act = nullptr;       // (FDM_MAX_K + 1) x 2048
   XGroup* act_xd = nullptr;   // (FDM_MAX_K + 1) x 32
@@ -202,7 +208,7 @@ void free_workspace() {
                   w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w,
                   w.layer_cnt, w.layer_flags, w.layer_tagged, w.b_seg, w.b_pair_tok,
                   w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act, w.b_act_xd, w.b_eo,
-                  w.p_hpost, w.p_xb, w.p_actb, w.dense_act};
+                  w.p_hpost, w.q_planes, w.q_xs, w.q_xe, w.q_chunks, w.q_nchunks, w.dense_act};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   g.ws = Workspace();
@@ -237,6 +243,8 @@ int alloc_workspace() {
   FDM_HIP(hipMalloc(&w.stage_idx, FDM_MAX_K * sizeof(int)));
   FDM_HIP(hipMalloc(&w.stage_w, FDM_MAX_K * sizeof(float)));
   FDM_HIP(hipMalloc(&w.dense_act, kDenseMaxFfn * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.q_chunks, kQMaxChunks * sizeof(int4)));
+  FDM_HIP(hipMalloc(&w.q_nchunks, sizeof(int)));
   return FDM_OK;
 }
 
@@ -1166,29 +1174,85 @@ int ensure_batch_rows(size_t rows, hipStream_t s) {
 
 namespace fdm {
 namespace {
-// Prefill buffers for T tokens and `rows` expert rows (grown on demand).
-int ensure_prefill(int T, size_t rows, hipStream_t s) {
+// The rms_norm output of prefill for T tokens (grown on demand).
+int ensure_prefill(int T, hipStream_t s) {
   Workspace& w = g.ws;
   if (T > w.p_tokens) {
     FDM_HIP(hipStreamSynchronize(s));
     if (w.p_hpost) (void)hipFree(w.p_hpost);
-    if (w.p_xb) (void)hipFree(w.p_xb);
     w.p_hpost = nullptr;
-    w.p_xb = nullptr;
     w.p_tokens = 0;
     FDM_HIP(hipMalloc(&w.p_hpost, (size_t)T * FDM_HIDDEN * sizeof(float)));
-    FDM_HIP(hipMalloc(&w.p_xb, 2 * (size_t)T * FDM_HIDDEN * sizeof(__bf16)));
     w.p_tokens = T;
   }
-  if (rows > w.p_rows) {
-    FDM_HIP(hipStreamSynchronize(s));
-    if (w.p_actb) (void)hipFree(w.p_actb);
-    w.p_actb = nullptr;
-    w.p_rows = 0;
-    // two planes: the bf16 pair (hi, lo) of batched decode; prefill uses one
-    FDM_HIP(hipMalloc(&w.p_actb, 2 * rows * FDM_MOE_FFN * sizeof(__bf16)));
-    w.p_rows = rows;
+  return FDM_OK;
+}
+
+// Activation planes for the grouped GEMMs of T tokens and `rows` expert
+// rows: the larger of the token inputs (T x 7168) and the SwiGLU rows
+// (rows x 2048), three planes (grown on demand).
+int ensure_planes(int T, size_t rows, hipStream_t s) {
+  Workspace& w = g.ws;
+  const size_t elems = std::max((size_t)T * FDM_HIDDEN, rows * FDM_MOE_FFN);
+  const size_t nrows = std::max((size_t)T, rows);
+  if (elems <= w.q_elems && nrows <= w.q_rows) return FDM_OK;
+  FDM_HIP(hipStreamSynchronize(s));
+  for (void* q : {(void*)w.q_planes, (void*)w.q_xs, (void*)w.q_xe})
+    if (q) (void)hipFree(q);
+  w.q_planes = nullptr;
+  w.q_xs = nullptr;
+  w.q_xe = nullptr;
+  w.q_elems = w.q_rows = 0;
+  FDM_HIP(hipMalloc(&w.q_planes, 3 * elems * sizeof(_Float16)));
+  FDM_HIP(hipMalloc(&w.q_xs, elems / 32 * sizeof(float)));
+  FDM_HIP(hipMalloc(&w.q_xe, nrows * sizeof(float)));
+  w.q_elems = elems;
+  w.q_rows = nrows;
+  return FDM_OK;
+}
+
+// Upper bound of the chunk list of T tokens, K slots (+ shared).
+int max_chunks(int T, int K, int ch) {
+  return std::min(256, T * K) + (T * K + ch - 1) / ch + (T + ch - 1) / ch;
+}
+
+// The expert half of one step on the grouped GEMMs, after the dispatch:
+// chunk list, planes of the token rows, gate/up + SwiGLU into b.act, then
+// a Q4_K down on the GEMM (planes of b.act first) or a Q6_K down on the
+// dot4 kernels, into b.eo.  x: the fp32 token rows [T][7168].
+int run_qgemm_experts(const Layer* y, const BatchArgs& b, const float* x, int planes, hipStream_t s) {
+  Workspace& w = g.ws;
+  const int T = b.T, K = b.K;
+  const size_t rows = (size_t)T * K + (y->shared ? T : 0);
+  const int ch = qgemm_chunk_tokens(planes);
+  const int mc = max_chunks(T, K, ch);
+  if (mc > kQMaxChunks) return fail(FDM_E_INVAL, "chunk list of %d entries exceeds %d", mc, kQMaxChunks);
+  FDM_HIP(launch_qchunks(b.seg_start, b.distinct, b.n_distinct, T, y->shared != nullptr, ch, w.q_chunks,
+                         w.q_nchunks, s));
+  FDM_HIP(launch_xplanes(x, FDM_HIDDEN, (size_t)T, planes, w.q_planes, w.q_xs, w.q_xe, s));
+  QGemmArgs q;
+  q.T = T;
+  q.K = K;
+  q.experts = y->experts;
+  q.expert_size = y->expert_size;
+  q.shared = y->shared;
+  q.xp = w.q_planes;
+  q.plane = (size_t)T * FDM_HIDDEN;
+  q.xs = w.q_xs;
+  q.xe = w.q_xe;
+  q.pair_tok = b.pair_tok;
+  q.chunks = w.q_chunks;
+  q.n_chunks = w.q_nchunks;
+  q.out = b.act;
+  FDM_HIP(launch_qgemm(q, planes, false, mc, s));
+  if (y->down_q6) {
+    FDM_HIP(launch_batched_down(b, true, s));
+    return FDM_OK;
   }
+  FDM_HIP(launch_xplanes(b.act, FDM_MOE_FFN, rows, planes, w.q_planes, w.q_xs, w.q_xe, s));
+  q.plane = rows * FDM_MOE_FFN;
+  q.out = b.eo;
+  FDM_HIP(launch_qgemm(q, planes, true, mc, s));
   return FDM_OK;
 }
 }  // namespace
@@ -1198,7 +1262,7 @@ int fdm_rms_norm(const float* d_x, const float* d_w, float* d_o, int T, int d, v
   if (int rc = check_ready()) return rc;
   if (!d_x || !d_o) return fail(FDM_E_INVAL, "null pointer");
   if (T < 1 || d < 1 || d > FDM_HIDDEN) return fail(FDM_E_INVAL, "T=%d d=%d (d <= %d)", T, d, FDM_HIDDEN);
-  FDM_HIP(launch_rms_norm(d_x, d_w, d_o, nullptr, T, d, as_stream(stream)));
+  FDM_HIP(launch_rms_norm(d_x, d_w, d_o, T, d, as_stream(stream)));
   return FDM_OK;
 }
 
@@ -1212,19 +1276,18 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
   for (int l = 0; l < n_layers; ++l) {
     Layer* y = nullptr;
     if (int rc = get_layer(layers[l], &y)) return rc;
-    if (y->down_q6) return fail(FDM_E_INVAL, "prefill runs Q4_K-down layers (layer %d is Q6_K)", layers[l]);
   }
   hipStream_t s = as_stream(stream);
   const size_t rows = (size_t)T * K + T;
-  if (int rc = ensure_prefill(T, rows, s)) return rc;
+  if (int rc = ensure_prefill(T, s)) return rc;
   if (int rc = ensure_batch_rows(rows, s)) return rc;
+  if (int rc = ensure_planes(T, rows, s)) return rc;
   ProfScope prof(FDM_PROF_PREFILL, s);
   for (int l = 0; l < n_layers; ++l) {
     Layer* y = nullptr;
     (void)get_layer(layers[l], &y);
     int* idx = d_idx ? d_idx + (size_t)l * T * K : g.ws.idx;
-    FDM_HIP(launch_rms_norm(d_H, d_norm_w ? d_norm_w[l] : nullptr, g.ws.p_hpost, g.ws.p_xb, T,
-                            FDM_HIDDEN, s));
+    FDM_HIP(launch_rms_norm(d_H, d_norm_w ? d_norm_w[l] : nullptr, g.ws.p_hpost, T, FDM_HIDDEN, s));
     FDM_HIP(launch_router_logits(y->Wg, g.ws.p_hpost, FDM_N_EXPERTS, FDM_HIDDEN, T, g.ws.logits, s));
     FDM_HIP(launch_route(g.ws.logits, y->bias, T, K, idx, g.ws.w, s));
     BatchArgs b{};
@@ -1237,6 +1300,8 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     b.out = d_H;  // residual in place
     b.idx = idx;
     b.w = g.ws.w;
+    b.act = g.ws.b_act;
+    b.act_xd = g.ws.b_act_xd;
     b.eo = g.ws.b_eo;
     b.seg_start = g.ws.b_seg;
     b.pair_tok = g.ws.b_pair_tok;
@@ -1244,22 +1309,8 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     b.distinct = g.ws.b_distinct;
     b.n_distinct = g.ws.b_ndistinct;
     FDM_HIP(launch_dispatch(b, s));
-    PrefillArgs p;
-    p.T = T;
-    p.K = K;
-    p.experts = y->experts;
-    p.expert_size = y->expert_size;
-    p.shared = y->shared;
-    p.xb = g.ws.p_xb;
-    p.actb = g.ws.p_actb;
-    p.act_rows = g.ws.p_rows;
-    p.actf = nullptr;
-    p.eo = g.ws.b_eo;
-    p.seg_start = g.ws.b_seg;
-    p.pair_tok = g.ws.b_pair_tok;
-    p.distinct = g.ws.b_distinct;
-    p.n_distinct = g.ws.b_ndistinct;
-    FDM_HIP(launch_prefill_experts(p, false, s));
+    // prefill precision: one fp16 plane of the activations (the bar is 1e-2)
+    if (int rc = run_qgemm_experts(y, b, g.ws.p_hpost, 1, s)) return rc;
     FDM_HIP(launch_combine(b, s));
   }
   return FDM_OK;
@@ -1309,27 +1360,10 @@ int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T,
     FDM_HIP(launch_batched_experts(b, y->down_q6, s));
     return FDM_OK;
   }
-  // grouped MFMA GEMMs at pair precision (a Q6_K down runs on the dot4 kernel)
-  if (int rc = ensure_prefill(T, rows, s)) return rc;
+  // grouped MFMA GEMMs at fp32 grade (three fp16 planes of the activations)
+  if (int rc = ensure_planes(T, rows, s)) return rc;
   FDM_HIP(launch_dispatch(b, s));
-  FDM_HIP(launch_bf16_pair(d_X, g.ws.p_xb, (size_t)T * FDM_HIDDEN, s));
-  PrefillArgs q;
-  q.T = T;
-  q.K = K;
-  q.experts = y->experts;
-  q.expert_size = y->expert_size;
-  q.shared = y->shared;
-  q.xb = g.ws.p_xb;
-  q.actb = g.ws.p_actb;
-  q.act_rows = g.ws.p_rows;
-  q.actf = y->down_q6 ? g.ws.b_act : nullptr;
-  q.eo = g.ws.b_eo;
-  q.seg_start = g.ws.b_seg;
-  q.pair_tok = g.ws.b_pair_tok;
-  q.distinct = g.ws.b_distinct;
-  q.n_distinct = b.n_distinct;
-  FDM_HIP(launch_prefill_experts(q, true, s));
-  if (y->down_q6) FDM_HIP(launch_batched_down(b, true, s));
+  if (int rc = run_qgemm_experts(y, b, d_X, 3, s)) return rc;
   FDM_HIP(launch_combine(b, s));
   return FDM_OK;
 }
@@ -1663,12 +1697,12 @@ int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
   AttnScratch& ws = g.attn_ws;
   hipStream_t s = as_stream(stream);
   ProfScope prof(FDM_PROF_ATTN, s);
-  FDM_HIP(launch_rms_norm(d_hidden, a.attn_norm, ws.normed, nullptr, 1, FDM_HIDDEN, s));
+  FDM_HIP(launch_rms_norm(d_hidden, a.attn_norm, ws.normed, 1, FDM_HIDDEN, s));
   FDM_HIP(launch_mv_f16(a.q_a, ws.normed, nullptr, ws.q_a, 1536, FDM_HIDDEN, s));
-  FDM_HIP(launch_rms_norm(ws.q_a, a.q_a_norm, ws.q_a_n, nullptr, 1, 1536, s));
+  FDM_HIP(launch_rms_norm(ws.q_a, a.q_a_norm, ws.q_a_n, 1, 1536, s));
   FDM_HIP(launch_mv_f16(a.q_b, ws.q_a_n, nullptr, ws.q, 128 * 192, 1536, s));
   FDM_HIP(launch_mv_f16(a.kv_a, ws.normed, nullptr, ws.kv_a, 576, FDM_HIDDEN, s));
-  FDM_HIP(launch_rms_norm(ws.kv_a, a.kv_a_norm, ws.c_kv_n, nullptr, 1, 512, s));
+  FDM_HIP(launch_rms_norm(ws.kv_a, a.kv_a_norm, ws.c_kv_n, 1, 512, s));
   // softmax scale with the YaRN mscale (infer.m:802-815), in float as there
   const float mscale = 0.1f * logf(40.0f) + 1.0f;
   MlaArgs m;

@@ -143,35 +143,37 @@ hipError_t launch_dispatch(const BatchArgs& b, hipStream_t s);
 hipError_t launch_combine(const BatchArgs& b, hipStream_t s);
 
 // prefill_kernels.hip
-// rms_norm per token (infer.m:369-374), bit-exact: o = x * inv * w; also
-// the bf16 pair of o into xb when not null: hi [T][d], then lo [T][d].
-// d <= 7168.
-hipError_t launch_rms_norm(const float* x, const float* w, float* o, __bf16* xb, int T, int d,
-                           hipStream_t s);
-// Grouped expert GEMMs of one prefill layer (Q4_K down): gate/up + SwiGLU
-// into actb, down into eo.  Rows: pair position p (routed), T*K + t (shared).
-struct PrefillArgs {
+// rms_norm per token (infer.m:369-374), bit-exact: o = x * inv * w.  d <= 7168.
+hipError_t launch_rms_norm(const float* x, const float* w, float* o, int T, int d, hipStream_t s);
+
+// gemm_kernels.hip: grouped expert GEMMs (batched decode, prefill) on MFMA.
+// Rows: pair position p (routed), T*K + t (shared expert of token t).
+struct QGemmArgs {
   int T, K;
-  const uint8_t* experts;
+  const uint8_t* experts;  // resident expert layout
   size_t expert_size;
   const uint8_t* shared;
-  const __bf16* xb;        // rms_norm output as bf16 pairs: hi [T][7168], lo [T][7168]
-  __bf16* actb;            // [rows][2048] (pair precision: hi plane, then lo plane at + act_rows)
-  size_t act_rows;         // rows of each actb plane
-  float* actf;             // pair precision only, optional: fp32 SwiGLU activations [rows][2048]
-                           // written instead of actb (a Q6_K down runs on the dot4 kernels)
-  float* eo;               // [rows][7168]
-  const int* seg_start;    // from the dispatch
-  const int* pair_tok;
-  const int* distinct;
-  const int* n_distinct;
+  const _Float16* xp;      // activation planes [P][plane]: input row r at r * kd
+  size_t plane;            // elements per plane
+  const float* xs;         // [rows][kd / 32] sub-block sums of the planes
+  const float* xe;         // [rows] 2^-s of each input row
+  const int* pair_tok;     // token of each pair position (gate/up input rows)
+  const int4* chunks;      // {expert or -1, first pair / token, count, 0}
+  const int* n_chunks;
+  float* out;              // gate/up: act [rows][2048] (SwiGLU); down: eo [rows][7168]
 };
-// pair = false: prefill precision (bf16 weights, 1e-2).  pair = true: batched
-// decode precision (bf16 hi/lo weights and activations, ~1e-5), Q4_K down;
-// with actf set only the gate/up GEMM runs.
-hipError_t launch_prefill_experts(const PrefillArgs& p, bool pair, hipStream_t s);
-// x [n] fp32 -> its bf16 pair: hi at xb[i], lo at xb[n + i]
-hipError_t launch_bf16_pair(const float* x, __bf16* xb, size_t n, hipStream_t s);
+// n_rows x [kd] fp32 -> `planes` (1 or 3) fp16 planes of x * 2^s, the
+// sub-block sums and 2^-s per row.
+hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
+                          hipStream_t s);
+// The chunk list of one step from the dispatch (chunks of `ch` tokens).
+hipError_t launch_qchunks(const int* seg_start, const int* distinct, const int* n_distinct, int T, bool with_shared,
+                          int ch, int4* chunks, int* n_chunks, hipStream_t s);
+int qgemm_chunk_tokens(int planes);
+constexpr int kQMaxChunks = 1024;  // >= 256 + 512 * 16 / 16 + 512 / 16
+// Q4_K gate/up + SwiGLU (down = false) or Q4_K down (down = true) over the
+// chunk list; max_chunks bounds the list length.
+hipError_t launch_qgemm(const QGemmArgs& g, int planes, bool down, int max_chunks, hipStream_t s);
 
 // dense_kernels.hip: the dense FFN of the first layers (F16 weights)
 constexpr int kDenseMaxFfn = 18432;  // DENSE_INTERMEDIATE (infer.m:59): the down kernel's LDS bound

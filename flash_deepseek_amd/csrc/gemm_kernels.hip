@@ -1,0 +1,457 @@
+// gemm_kernels.hip -- the grouped expert GEMMs of batched decode and prefill
+// on MFMA: per distinct expert (and the shared one), its tokens' activations
+// against the expert's Q4_K rows, for gate/up (+ SwiGLU) and for a Q4_K down.
+//
+// Numerics.  Inside one Q4_K block a weight is d*sc*q - dmin*m (quant.c:49-57)
+// with 6-bit sc, m and 4-bit q, so
+//   sum_k w_k x_k = d * sum_k sc_k q_k x_k - dmin * sum_sb m_sb X_sb
+// (X_sb: the sum of the sub-block's 32 activations).  The integer sc*q <= 945
+// is exact in fp16 and is built per element by one packed integer multiply-
+// add straight into fp16 bits: 0x6400 + sc*q is the half 1024 + sc*q.  The
+// MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation) contracts it with the
+// activations, so the MFMA sums 1024 X + sum sc q x over a whole block and
+// the scales are applied once per block:
+//   y += d * C  -  sum_sb X_sb (1024 d + dmin m_sb)
+// the second term by a 16x16x4 fp32 MFMA over the block's eight sub-blocks.
+// Activations enter as P fp16 planes of x' = x * 2^s (a per-row power of
+// two: the largest |x'| lies in [2^13, 2^14)): P = 3 carries every fp32
+// value exactly (hi + mid + lo, 33 significant bits) -- batched decode, fp32
+// grade; P = 1 carries 11 bits -- prefill, whose bar is 1e-2.  X_sb is the
+// fp32 sum of the planes, so the 1024 X part of C cancels against it.
+//
+// Mapping.  A workgroup of 8 waves owns 128 gate and 128 up rows (wave w:
+// rows 16 w .. 16 w + 15 of both, so SwiGLU is applied in registers) or 256
+// down rows (wave w: two tiles of 16), for one chunk of <= 16 NB tokens of
+// one expert.  Weight rows are the MFMA columns (B operand): lane (c, j)
+// holds row c and group j (qs bytes 32 j .. 32 j + 31, sub-blocks 2j, 2j+1)
+// of every block, read as two whole 16-byte pieces of the resident expert
+// layout, so the four lanes of a row read one 64-byte line per load and
+// each lane needs only its own group's two scales and mins.  MFMA step m
+// (0..7) of a block takes from lane j the 8 elements 64 j + 8 m .. + 7 (low
+// nibbles for m < 4, high nibbles for m >= 4); the token operand (A, from
+// LDS) reads the same elements.  Per block the chunk's token planes are
+// copied global -> LDS by direct loads into one of two buffers, so block
+// b + 1 streams in while block b is contracted.
+#include "fdm_internal.h"
+
+namespace fdm {
+
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kQWaves = 4;            // waves per workgroup
+constexpr int kQRowB = kQK * 2;       // LDS token row: one block of fp16 (512 B)
+constexpr int kQGuRows = 16 * kQWaves;   // gate (and up) rows per workgroup: 128
+constexpr int kQDnRows = 32 * kQWaves;   // down rows per workgroup: 256
+
+// One lane's share of one block of one weight row (resident expert layout):
+// its group's 32 qs bytes and the 16-byte block header.
+struct QLane {
+  u32x4 q0, q1, hdr;
+};
+
+// In the resident layout the q0 (and q1) pieces of blocks 2i and 2i + 1 of a
+// row share one 128-byte line: block 2i reads its half with the default
+// policy (the line stays in L2 for the next iteration), block 2i + 1 the
+// other half as its last use (nontemporal).
+template <bool DOWN, bool LAST>
+__device__ __forceinline__ QLane qlane_load(const uint8_t* mat, int row, int block, int j) {
+  constexpr int N = DOWN ? kRelDnPieces : kRelGuPieces;
+  const uint8_t* st = rel_step<DOWN>(mat, row, block);
+  const int L0 = rel_piece<DOWN>(row, block, 0);
+  const u32x4* p0 = reinterpret_cast<const u32x4*>(st + 16 * (L0 + j));
+  const u32x4* p1 = reinterpret_cast<const u32x4*>(st + 16 * N + 16 * (L0 + j));
+  QLane r;
+  if (LAST) {
+    r.q0 = __builtin_nontemporal_load(p0);
+    r.q1 = __builtin_nontemporal_load(p1);
+  } else {
+    r.q0 = *p0;
+    r.q1 = *p1;
+  }
+  r.hdr = *reinterpret_cast<const u32x4*>(st + 32 * N + 4 * L0);
+  return r;
+}
+
+// Bytes 0, 1 (and 2, 3) of w into the low bytes of the two halves.
+__device__ __forceinline__ uint32_t spread01(uint32_t w) { return (w & 0xFFu) | ((w << 8) & 0x00FF0000u); }
+__device__ __forceinline__ uint32_t spread23(uint32_t w) {
+  return ((w >> 16) & 0xFFu) | ((w >> 8) & 0x00FF0000u);
+}
+
+// fp16 bits of 1024 + sc * q for the two q held in the low bytes of the
+// halves of s (q < 16, so sc * q < 1024 fits the 10-bit mantissa).
+__device__ __forceinline__ uint32_t magic2(uint32_t q2, u16x2 sc2) {
+  const u16x2 q = __builtin_bit_cast(u16x2, q2);
+  const u16x2 v = q * sc2 + (u16x2){0x6400, 0x6400};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// The B operands of MFMA steps m (low nibbles) and m + 4 (high nibbles):
+// bytes 8 m' .. 8 m' + 7 of the lane's group, m' = m & 3 (q0 for m' < 2).
+struct BPair {
+  f16x8 lo, hi;
+};
+
+__device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, u16x2 sc_hi) {
+  const uint32_t s0 = spread01(w0), s1 = spread23(w0), s2 = spread01(w1), s3 = spread23(w1);
+  u32x4 lo, hi;
+  lo.x = magic2(s0 & 0x000F000Fu, sc_lo);
+  lo.y = magic2(s1 & 0x000F000Fu, sc_lo);
+  lo.z = magic2(s2 & 0x000F000Fu, sc_lo);
+  lo.w = magic2(s3 & 0x000F000Fu, sc_lo);
+  hi.x = magic2((s0 >> 4) & 0x000F000Fu, sc_hi);
+  hi.y = magic2((s1 >> 4) & 0x000F000Fu, sc_hi);
+  hi.z = magic2((s2 >> 4) & 0x000F000Fu, sc_hi);
+  hi.w = magic2((s3 >> 4) & 0x000F000Fu, sc_hi);
+  BPair b;
+  b.lo = __builtin_bit_cast(f16x8, lo);
+  b.hi = __builtin_bit_cast(f16x8, hi);
+  return b;
+}
+
+// Per-block constants of the lane's row and group.
+struct QScale {
+  float d;
+  u16x2 sc_lo, sc_hi;  // sc of sub-blocks 2j, 2j+1, in both halves
+  float bc_lo, bc_hi;  // -(1024 d + dmin m) of sub-blocks 2j, 2j+1
+};
+
+__device__ __forceinline__ QScale qscale(const u32x4 hdr, const Q4KScaleSel& sel) {
+  int sc0, m0, sc1, m1;
+  q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, sel, sc0, m0, sc1, m1);
+  QScale s;
+  s.d = half_to_float(hdr.x);
+  const float dmin = half_to_float(hdr.x >> 16);
+  s.sc_lo = (u16x2){(unsigned short)sc0, (unsigned short)sc0};
+  s.sc_hi = (u16x2){(unsigned short)sc1, (unsigned short)sc1};
+  const float off = 1024.0f * s.d;  // exact: a power-of-two multiple of a half
+  s.bc_lo = -fmaf(dmin, (float)m0, off);
+  s.bc_hi = -fmaf(dmin, (float)m1, off);
+  return s;
+}
+
+__device__ __forceinline__ f32x4 mfma_h(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_f(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// One 16-byte direct global -> LDS load per lane (lane i writes lds_dst + 16 i).
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(gsrc, lds_dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+}  // namespace
+
+// ---- activation planes ---------------------------------------------------------------
+// One workgroup per row of n_rows x [kd] fp32: s = the power of two that puts
+// the row's largest |x| in [2^13, 2^14), x' = x * 2^s split into P fp16
+// planes (round to nearest, each the rounding of what the previous planes
+// left), xs[sb] = the fp32 sum over the sub-block of the planes' values,
+// xe = 2^-s.  Planes: [P][n_rows][kd].
+template <int P>
+__global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, int kd, size_t n_rows,
+                                                 _Float16* __restrict__ xp, float* __restrict__ xs,
+                                                 float* __restrict__ xe) {
+  __shared__ float red[4];
+  const size_t row = blockIdx.x;
+  const float* xr = x + row * kd;
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < kd; i += 256) m = fmaxf(m, fabsf(xr[i]));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int s = 0;
+  if (amax > 0.0f && amax <= 3.4028234e38f) {
+    int E;
+    (void)frexpf(amax, &E);  // amax in [2^(E-1), 2^E)
+    s = 14 - E;
+  }
+  if (threadIdx.x == 0) xe[row] = ldexpf(1.0f, -s);
+  const int nsb = kd / 32;
+  for (int sb = threadIdx.x; sb < nsb; sb += 256) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(xr + 32 * sb);
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // 8 elements: one 16-byte store per plane
+      _Float16 h[P][8];
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const f32x4 a = src[2 * q + v];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float r = ldexpf(a[e], s);
+          float tot = 0.0f;
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            const _Float16 hp = (_Float16)r;
+            h[p][4 * v + e] = hp;
+            r -= (float)hp;
+            tot += (float)hp;
+          }
+          sum += tot;
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        *reinterpret_cast<f16x8*>(xp + ((size_t)p * n_rows + row) * kd + 32 * sb + 8 * q) =
+            (f16x8){h[p][0], h[p][1], h[p][2], h[p][3], h[p][4], h[p][5], h[p][6], h[p][7]};
+    }
+    xs[row * nsb + sb] = sum;
+  }
+}
+
+// ---- the chunk list -------------------------------------------------------------------
+// One thread: every distinct routed expert's pair segment in chunks of `ch`
+// pairs, then the shared expert's tokens in chunks of `ch`.  Entry:
+// {expert (-1: shared), first pair position (or token), count, 0}.
+__global__ void k_qchunks(const int* __restrict__ seg_start, const int* __restrict__ distinct,
+                          const int* __restrict__ n_distinct, int T, int with_shared, int ch,
+                          int4* __restrict__ chunks, int* __restrict__ n_chunks) {
+  if (threadIdx.x != 0) return;
+  int n = 0;
+  const int D = *n_distinct;
+  for (int d = 0; d < D; ++d) {
+    const int e = distinct[d];
+    const int a = seg_start[e], b = seg_start[e + 1];
+    for (int f = a; f < b; f += ch) chunks[n++] = make_int4(e, f, min(ch, b - f), 0);
+  }
+  if (with_shared)
+    for (int f = 0; f < T; f += ch) chunks[n++] = make_int4(-1, f, min(ch, T - f), 0);
+  *n_chunks = n;
+}
+
+// ---- the grouped GEMM ------------------------------------------------------------------
+template <int P, int NB, bool DOWN>
+__device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int* rows, int chunk, int rg) {
+  constexpr int KD = DOWN ? kFfn : kHidden;  // contraction length
+  constexpr int NBLK = KD / kQK;             // 8 or 28 (even)
+  constexpr int NT = 16 * NB;                // token rows per buffer and plane
+  constexpr int BUF = P * NT * kQRowB;       // bytes per buffer
+  constexpr int ROUNDS = P * NT / (2 * kQWaves);  // direct loads per wave per block (2 rows each)
+  static_assert(ROUNDS * 2 * kQWaves == P * NT, "the direct loads tile the buffer");
+  const int4 ck = g.chunks[chunk];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c16 = lane & 15, j = lane >> 4;
+  const int n = ck.z;
+  const bool shared = ck.x < 0;
+  const int P0 = g.T * g.K;
+  int* rin = rows;          // input row of chunk token t (activation plane row)
+  int* rout = rows + NT;    // output row
+  if (threadIdx.x < NT) {
+    const int t = min((int)threadIdx.x, n - 1);  // pad rows repeat the last token
+    const int orow = shared ? P0 + ck.y + t : ck.y + t;
+    rout[threadIdx.x] = orow;
+    rin[threadIdx.x] = DOWN ? orow : (shared ? ck.y + t : g.pair_tok[ck.y + t]);
+  }
+  __syncthreads();
+  const uint8_t* blob = shared ? g.shared : g.experts + (size_t)ck.x * g.expert_size;
+  const uint8_t* mat0;
+  const uint8_t* mat1;
+  int row0, row1;
+  if (DOWN) {
+    mat0 = mat1 = blob + 2 * (size_t)kGateBytes;
+    row0 = rg * kQDnRows + 32 * wave + c16;
+    row1 = row0 + 16;
+  } else {
+    mat0 = blob;
+    mat1 = blob + kGateBytes;
+    row0 = row1 = rg * kQGuRows + 16 * wave + c16;
+  }
+  // direct-load sources: round k of wave w fills LDS rows 2 (w + 8 k), +1 of
+  // the buffer (row rho = plane * NT + token); lane i: row rho0 + i / 32,
+  // slot i % 32 holds piece (i % 32) ^ (rho & 15) of that row's block
+  uint32_t src[ROUNDS];
+#pragma unroll
+  for (int k = 0; k < ROUNDS; ++k) {
+    const int rho = 2 * (wave + kQWaves * k) + (lane >> 5);
+    const int p = rho / NT, t = rho - p * NT;
+    const uint32_t piece = (uint32_t)((lane & 31) ^ (t & 15));
+    src[k] = (uint32_t)((size_t)rin[t] * KD) + 8u * piece;  // element offset inside plane p
+  }
+  auto dma = [&](int b, int buf) {
+    uint8_t* base = lds + buf * BUF;
+#pragma unroll
+    for (int k = 0; k < ROUNDS; ++k) {
+      const int rho0 = 2 * (wave + kQWaves * k);
+      const int p = rho0 / NT;
+      lds_dma16(g.xp + (size_t)p * g.plane + src[k] + (size_t)b * kQK, base + rho0 * kQRowB);
+    }
+  };
+  const Q4KScaleSel sel = q4k_scale_sel(j);
+  // corr operand A: token c16 of block nb, sub-blocks 2j and 2j+1 of block b
+  auto load_xs = [&](int b, int nb) {
+    const float2 v = *reinterpret_cast<const float2*>(g.xs + (size_t)rin[16 * nb + c16] * (KD / 32) + 8 * b + 2 * j);
+    return v;
+  };
+  f32x4 acc[2][NB];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // One block: both tiles' B operands are built per MFMA step and share
+  // every token operand read from LDS.
+  auto block = [&](int buf, const QLane& w0, const QLane& w1, const float2 (&xsv)[NB]) {
+    const uint8_t* base = lds + buf * BUF;
+    const QScale s0 = qscale(w0.hdr, sel), s1 = qscale(w1.hdr, sel);
+    f32x4 C0[NB], C1[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      C0[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      C1[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int i0 = 2 * (m & 1);
+      const u32x4& qa = m < 2 ? w0.q0 : w0.q1;
+      const u32x4& qb = m < 2 ? w1.q0 : w1.q1;
+      const BPair B0 = build_b(qa[i0], qa[i0 + 1], s0.sc_lo, s0.sc_hi);
+      const BPair B1 = build_b(qb[i0], qb[i0 + 1], s1.sc_lo, s1.sc_hi);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const uint8_t* r = base + (p * NT + 16 * nb + c16) * kQRowB;
+          const f16x8 alo = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ c16));
+          const f16x8 ahi = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ c16));
+          C0[nb] = mfma_h(alo, B0.lo, C0[nb]);
+          C1[nb] = mfma_h(alo, B1.lo, C1[nb]);
+          C0[nb] = mfma_h(ahi, B0.hi, C0[nb]);
+          C1[nb] = mfma_h(ahi, B1.hi, C1[nb]);
+        }
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      f32x4 a0 = acc[0][nb], a1 = acc[1][nb];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a0[i] = fmaf(s0.d, C0[nb][i], a0[i]);
+        a1[i] = fmaf(s1.d, C1[nb][i], a1[i]);
+      }
+      a0 = mfma_f(xsv[nb].x, s0.bc_lo, a0);
+      a0 = mfma_f(xsv[nb].y, s0.bc_hi, a0);
+      a1 = mfma_f(xsv[nb].x, s1.bc_lo, a1);
+      a1 = mfma_f(xsv[nb].y, s1.bc_hi, a1);
+      acc[0][nb] = a0;
+      acc[1][nb] = a1;
+    }
+  };
+
+  dma(0, 0);
+  QLane wa0 = qlane_load<DOWN, false>(mat0, row0, 0, j), wa1 = qlane_load<DOWN, false>(mat1, row1, 0, j);
+  float2 xa[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) xa[nb] = load_xs(0, nb);
+  for (int b = 0; b < NBLK; b += 2) {
+    // even block b from buffer 0 while b + 1 lands in buffer 1, then odd
+    // block b + 1 from buffer 1 while b + 2 lands in buffer 0 (the last pair
+    // re-stages the final block into the idle buffer: branch-free, so the
+    // wait counts stay exact)
+    wait_vm();
+    __syncthreads();  // block b staged by every wave; buffer 1 read by all (block b - 1)
+    dma(b + 1, 1);
+    QLane wb0 = qlane_load<DOWN, true>(mat0, row0, b + 1, j), wb1 = qlane_load<DOWN, true>(mat1, row1, b + 1, j);
+    float2 xb[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) xb[nb] = load_xs(b + 1, nb);
+    block(0, wa0, wa1, xa);
+    const int b2 = min(b + 2, NBLK - 1);
+    wait_vm();
+    __syncthreads();  // block b + 1 staged; buffer 0 read by all (block b)
+    dma(b2, 0);
+    wa0 = qlane_load<DOWN, false>(mat0, row0, b2, j);
+    wa1 = qlane_load<DOWN, false>(mat1, row1, b2, j);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) xa[nb] = load_xs(b2, nb);
+    block(1, wb0, wb1, xb);
+  }
+  wait_vm();  // the re-staged copy has landed before the LDS is released
+  // D of a 16x16 MFMA: lane (c16, j) holds row (column) c16 of the tile and
+  // tokens 4 j .. 4 j + 3 of the token block
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * nb + 4 * j + i;
+      if (t >= n) continue;
+      const float e = g.xe[rin[t]];
+      if (DOWN) {
+        float* o = g.out + (size_t)rout[t] * kHidden;
+        o[row0] = acc[0][nb][i] * e;
+        o[row1] = acc[1][nb][i] * e;
+      } else {
+        g.out[(size_t)rout[t] * kFfn + row0] = silu_mul(acc[0][nb][i] * e, acc[1][nb][i] * e);
+      }
+    }
+  }
+}
+
+// NB: the largest token block count of a chunk; a chunk of <= 16 tokens
+// runs the one-block body.  One-dimensional grid, mapped so that every row
+// group of a chunk runs on the same XCD: workgroups are handed to the eight
+// XCDs in turn (id % 8), so id -> (xcd = id % 8, k = id / 8) and chunk
+// 8 (k / RG) + xcd, row group k % RG.  The chunk's token planes are then
+// read from HBM into one L2 and served from there to all its row groups.
+template <int P, int NB, bool DOWN>
+__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(QGemmArgs g) {
+  constexpr int RG = DOWN ? kHidden / kQDnRows : kFfn / kQGuRows;
+  const int id = blockIdx.x, xcd = id & 7, k = id >> 3;
+  const int chunk = (k / RG) * 8 + xcd, rg = k % RG;
+  if (chunk >= *g.n_chunks) return;
+  constexpr int NT = 16 * NB;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * P * NT * kQRowB];
+  __shared__ int rows[2 * NT];
+  if (NB > 1 && g.chunks[chunk].z > 16)
+    qgemm_body<P, NB, DOWN>(g, lds, rows, chunk, rg);
+  else
+    qgemm_body<P, 1, DOWN>(g, lds, rows, chunk, rg);
+}
+
+hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
+                          hipStream_t s) {
+  if (planes == 3)
+    hipLaunchKernelGGL(k_xplanes<3>, dim3((unsigned)n_rows), dim3(256), 0, s, x, kd, n_rows, xp, xs, xe);
+  else
+    hipLaunchKernelGGL(k_xplanes<1>, dim3((unsigned)n_rows), dim3(256), 0, s, x, kd, n_rows, xp, xs, xe);
+  return hipGetLastError();
+}
+
+hipError_t launch_qchunks(const int* seg_start, const int* distinct, const int* n_distinct, int T, bool with_shared,
+                          int ch, int4* chunks, int* n_chunks, hipStream_t s) {
+  hipLaunchKernelGGL(k_qchunks, dim3(1), dim3(64), 0, s, seg_start, distinct, n_distinct, T, with_shared ? 1 : 0,
+                     ch, chunks, n_chunks);
+  return hipGetLastError();
+}
+
+int qgemm_chunk_tokens(int planes) { return planes == 3 ? 16 : 32; }
+
+hipError_t launch_qgemm(const QGemmArgs& g, int planes, bool down, int max_chunks, hipStream_t s) {
+  const dim3 blk(kQWaves * 64);
+  const int RG = down ? kHidden / kQDnRows : kFfn / kQGuRows;
+  const dim3 grid((unsigned)(RG * 8 * ((max_chunks + 7) / 8)));
+  if (planes == 3) {
+    if (down)
+      hipLaunchKernelGGL((k_qgemm<3, 1, true>), grid, blk, 0, s, g);
+    else
+      hipLaunchKernelGGL((k_qgemm<3, 1, false>), grid, blk, 0, s, g);
+  } else {
+    if (down)
+      hipLaunchKernelGGL((k_qgemm<1, 2, true>), grid, blk, 0, s, g);
+    else
+      hipLaunchKernelGGL((k_qgemm<1, 2, false>), grid, blk, 0, s, g);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace fdm

@@ -264,14 +264,15 @@ int fdm_moe_forward_batched(int L, const float *d_X, const float *d_H_in, int T,
 /* Expert kernels behind fdm_moe_forward_batched (no counterpart in the
  * reference; a tuning and test switch).  FDM_BATCH_DOT4: per-token int8
  * digit dot products, each expert tile held in registers while its tokens
- * stream through LDS.  FDM_BATCH_MFMA: the grouped GEMMs on MFMA at pair
- * precision (weights and activations as bf16 hi/lo pairs, ~1e-5 relative
- * error).  FDM_BATCH_AUTO: MFMA from FDM_BATCH_MFMA_MIN_T tokens per step,
- * DOT4 below.  Stores the previous mode in *prev when prev is not NULL. */
+ * stream through LDS.  FDM_BATCH_MFMA: the grouped GEMMs on MFMA (exact
+ * integer weights 1024 + sc*q in fp16, the activations as three fp16
+ * planes: fp32 grade).  FDM_BATCH_AUTO: MFMA from FDM_BATCH_MFMA_MIN_T
+ * tokens per step, DOT4 below.  Stores the previous mode in *prev when prev
+ * is not NULL. */
 #define FDM_BATCH_AUTO 0
 #define FDM_BATCH_DOT4 1
 #define FDM_BATCH_MFMA 2
-#define FDM_BATCH_MFMA_MIN_T 96
+#define FDM_BATCH_MFMA_MIN_T 6
 int fdm_set_batch_kernel(int mode, int *prev);
 
 /* ---- rms_norm on the device (infer.m:369-374, the h_post of infer.m:1850):
@@ -283,9 +284,10 @@ int fdm_rms_norm(const float *d_x, const float *d_w, float *d_o, int T, int d, v
 /* ---- prefill: T tokens through n_layers resident MoE layers,
  *   h <- h + MoE_l(rms_norm(h, norm_w[l]))   for l = 0 .. n_layers-1
  * (infer.m:1850, 1878-1922), in place on d_H [T][7168] fp32.  Routing is
- * route() per token on the fp32 rms_norm output (bit-exact); the expert
- * GEMMs dequantise Q4_K to bf16 and run on MFMA with fp32 accumulation
- * (layers must have Q4_K down).  layers / d_norm_w: host arrays of
+ * route() per token on the fp32 rms_norm output (bit-exact); the Q4_K
+ * expert GEMMs run on MFMA with fp32 accumulation, the weights as the exact
+ * integers 1024 + sc*q in fp16 and the activations as one fp16 plane (a Q6_K
+ * down runs on the digit kernels).  layers / d_norm_w: host arrays of
  * n_layers layer ids / device pointers to [7168] fp32.  d_idx (optional,
  * [n_layers][T][K]) receives every layer's routing.  1 <= T <= FDM_MAX_TOKENS. */
 int fdm_moe_prefill(const int *layers, int n_layers, float *d_H, int T, int K,

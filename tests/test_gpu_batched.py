@@ -26,7 +26,8 @@ def layer(request, fdm):
 @pytest.fixture(params=["dot4", "mfma"])
 def batch_kernel(request, fdm):
     """Runs the test under each expert path behind moe_forward_batched: the
-    per-token digit dot products and the grouped MFMA GEMMs (pair precision)."""
+    per-token digit dot products and the grouped MFMA GEMMs (three fp16
+    planes of the activations)."""
     mode = fdm.BATCH_DOT4 if request.param == "dot4" else fdm.BATCH_MFMA
     prev = fdm.set_batch_kernel(mode)
     yield request.param
@@ -85,7 +86,8 @@ def test_batched_matches_per_token_oracle(fdm, oracle, layer, batch_kernel, T, K
 
 def test_batched_paths_agree(fdm, layer):
     """The two expert paths on the same 96-token step: identical routing,
-    outputs within 1e-3 of each other."""
+    outputs within 1e-4 of each other (both carry the activations at fp32
+    grade)."""
     import torch
     from flash_deepseek_amd.synthetic import make_tokens
     L, _ = layer
@@ -104,7 +106,7 @@ def test_batched_paths_agree(fdm, layer):
             fdm.set_batch_kernel(prev)
     assert np.array_equal(outs[0][1], outs[1][1])
     for t in range(T):
-        assert rel_l2(outs[1][0][t], outs[0][0][t].astype(np.float64)) <= TOL, t
+        assert rel_l2(outs[1][0][t], outs[0][0][t].astype(np.float64)) <= 1e-4, t
 
 
 def test_batched_equals_single_token_layer(fdm, oracle, layer, batch_kernel):
