@@ -43,6 +43,46 @@ def layer_bytes(down, K=8):
     return weights + acts
 
 
+def percentiles(us):
+    """median, p10, p90 of a list of microsecond timings."""
+    a = sorted(us)
+    pick = lambda q: a[min(len(a) - 1, int(round(q * (len(a) - 1))))]
+    return {"median_us": round(pick(0.5), 3), "p10_us": round(pick(0.1), 3), "p90_us": round(pick(0.9), 3)}
+
+
+def event_times(torch, fn, n):
+    """fn(i) for i < n, each bracketed by HIP events on torch's current stream
+    (the stream the library launches on); per-call microseconds."""
+    st = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    en = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for i in range(n):
+        st[i].record()
+        fn(i)
+        en[i].record()
+    torch.cuda.synchronize()
+    return [st[i].elapsed_time(en[i]) * 1e3 for i in range(n)]
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def load_profile_json(name, key):
+    """A summary committed under profiles/ (rocprofv3 counters), or None."""
+    try:
+        with open(os.path.join(ROOT, "profiles", name)) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+
+
 def load_traffic(kernel, workload):
     """HBM bytes per launch measured by rocprofv3 counters (profiles/)."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
@@ -54,7 +94,10 @@ def load_traffic(kernel, workload):
 
 
 def cpu_baseline(down, seconds, K=8):
-    """Median us/token of the reference-shaped CPU path on a bounded sample."""
+    """Median us/token of the two CPU versions of the layer on bounded
+    samples of the same workload: the reference-shaped path (one thread per
+    expert, full fp32 dequant then sgemv) and the tuned one (fused row
+    dequant-dot over every host core)."""
     sys.path.insert(0, ROOT)
     from oracle import oracle as O
     q6 = down == "q6k"
@@ -63,22 +106,118 @@ def cpu_baseline(down, seconds, K=8):
     bias = O.synth_normal(256, 0.0, 0.1, 902)
     x = O.synth_normal(HIDDEN, 0.0, 1.0, 903)
     h_in = O.synth_normal(HIDDEN, 0.0, 1.0, 904)
+    model = cpu_model()
     t0 = time.perf_counter()
-    first, _ = O.cpu_layer_baseline(blobs, q6, Wg, bias, x, h_in, 2)
+    O.cpu_layer_baseline(blobs, q6, Wg, bias, x, h_in, 2)
     per = max(time.perf_counter() - t0, 1e-3) / 2
     reps = int(max(3, min(200, seconds / per)))
     us, _ = O.cpu_layer_baseline(blobs, q6, Wg, bias, x, h_in, reps)
-    return {
+    ref = {
         "value": round(us, 1),
         "unit": "us/token",
         "cores": K + 1,
         "kind": "port",
-        "sample": (f"{reps} tokens through one R1 MoE layer on the host: router sgemv + "
-                   f"route() + {K} routed and 1 shared expert, each dequantised to fp32 and "
-                   f"run as 3 sgemv + SiLU*mul on its own thread (infer.m:1878-1922, "
-                   f"USE_CPU_EXPERTS), {down.upper()} down; median per token; "
-                   f"{os.cpu_count()} host CPUs visible"),
+        "sample": (f"{reps} tokens through one R1 MoE layer on the host ({model}, {os.cpu_count()} CPUs "
+                   f"visible): router sgemv + route() + {K} routed and 1 shared expert, each "
+                   f"dequantised to fp32 and run as 3 sgemv + SiLU*mul on its own thread "
+                   f"(infer.m:1878-1922, USE_CPU_EXPERTS), {down.upper()} down; median per token"),
     }
+    t0 = time.perf_counter()
+    O.cpu_layer_tuned(blobs, q6, Wg, bias, x, h_in, 2)
+    per = max(time.perf_counter() - t0, 1e-3) / 2
+    reps = int(max(3, min(2000, seconds / per)))
+    us, _, threads = O.cpu_layer_tuned(blobs, q6, Wg, bias, x, h_in, reps)
+    tuned = {
+        "value": round(us, 1),
+        "unit": "us/token",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{reps} tokens through the same layer on {threads} host threads ({model}): rows "
+                   f"dequantised and dotted in one pass (AVX2 FMA), no fp32 matrix copies; "
+                   f"median per token"),
+    }
+    return ref, tuned
+
+
+def bench_matvec(F, torch, args, n_sets=64, calls=256):
+    """Config 0: y = W x for a Q4_K W [2048 x 7168] (the dequant_matvec_q4k
+    of one gate matrix) over n_sets distinct weight sets (> the 256 MB
+    Infinity Cache), a new set each call; per-call HIP events."""
+    from flash_deepseek_amd.synthetic import make_tokens
+    rows, cols = 2048, 7168
+    nb = rows * cols // 256
+    W = torch.empty(n_sets * nb * 144, dtype=torch.uint8, device="cuda")
+    for i in range(n_sets):
+        F.synth_q4k(W.data_ptr() + i * nb * 144, nb, 5000 + i)
+    x = make_tokens(1, 5100)[0]
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    run = lambda i: F.matvec_q4k(W.data_ptr() + (i % n_sets) * nb * 144, x, y, rows, cols)
+    for i in range(16):
+        run(i)
+    us = event_times(torch, run, calls)
+    del W
+    nbytes = nb * 144 + cols * 4 + rows * 4
+    r = {"workload": "Q4_K matvec 2048x7168, batch 1 (fdm_matvec_q4k: digits of x + fused dequant matvec)",
+         "weight_sets": n_sets, "calls": calls, "bytes_per_call": nbytes}
+    r.update(percentiles(us))
+    r["gbps"] = round(nbytes / (r["median_us"] * 1e-6) / 1e9, 1)
+    r["frac"] = round(r["gbps"] / HBM_PEAK_GBPS, 4)
+    return r
+
+
+def bench_expert(F, torch, down, n_sets=64, calls=256):
+    """Config 1: one SwiGLU expert at batch 1 (fdm_expert_ffn on the packed
+    blob) over n_sets distinct experts, a new one each call."""
+    from flash_deepseek_amd.synthetic import fill_blob, make_tokens
+    q6 = down == "q6k"
+    es = F.EXPERT_Q6K_BYTES if q6 else F.EXPERT_Q4K_BYTES
+    blobs = torch.empty(n_sets * es, dtype=torch.uint8, device="cuda")
+    for i in range(n_sets):
+        fill_blob(blobs, i * es, 6000 + i, 0, q6)
+    x = make_tokens(1, 6100)[0]
+    out = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    run = lambda i: F.expert_ffn(blobs.data_ptr() + (i % n_sets) * es, es, x, out)
+    for i in range(16):
+        run(i)
+    us = event_times(torch, run, calls)
+    del blobs
+    nbytes = es + HIDDEN * 4 * 2 + FFN * 4 * 2
+    r = {"workload": f"one SwiGLU expert, batch 1: Q4_K gate/up 2048x7168, {down.upper()} down 7168x2048 "
+                     "(fdm_expert_ffn)", "weight_sets": n_sets, "calls": calls, "bytes_per_call": nbytes}
+    r.update(percentiles(us))
+    r["gbps"] = round(nbytes / (r["median_us"] * 1e-6) / 1e9, 1)
+    r["frac"] = round(r["gbps"] / HBM_PEAK_GBPS, 4)
+    return r
+
+
+def bench_layer_q6k(F, torch, args, stream, K, n_layers=6, steps=200):
+    """The batch-1 layer with Q6_K down matrices (k_layer_q6k), n_layers
+    resident layers rotated, a new token per step; per-step HIP events."""
+    from flash_deepseek_amd.synthetic import make_layer, make_tokens
+    keep = []
+    for l in range(n_layers):
+        lay = make_layer(700 + l, down_q6=True)
+        F.attach_layer(40 + l, lay.experts, lay.expert_size, lay.Wg, lay.bias, lay.shared)
+        lay.experts = lay.shared = None
+        keep.append(lay)
+    torch.cuda.empty_cache()
+    h = make_tokens(steps + 20, 7101)
+    h_in = make_tokens(steps + 20, 7102)
+    out = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    run = lambda i: F.moe_layer(40 + i % n_layers, h[i], h_in[i], K, out, stream=stream)
+    for i in range(20):
+        run(i)
+    us = event_times(torch, lambda i: run(20 + i), steps)
+    F.sync(stream)
+    for l in range(n_layers):
+        F.release_layer(40 + l)
+    nbytes = layer_bytes("q6k", K)
+    r = {"workload": "the batch-1 layer with Q6_K down (k_layer_q6k)", "layers_rotated": n_layers,
+         "steps": steps, "bytes_per_token": nbytes}
+    r.update(percentiles(us))
+    r["gbps"] = round(nbytes / (r["median_us"] * 1e-6) / 1e9, 1)
+    r["frac"] = round(r["gbps"] / HBM_PEAK_GBPS, 4)
+    return r
 
 
 def bench_batched(F, torch, layers, args, stream, K, steps=20, warmup=3):
@@ -139,12 +278,40 @@ def bench_prefill(F, torch, layers, args, stream, K, n_layers=4, iters=5):
     d = [len(torch.unique(idx[l])) for l in range(n_layers)]
     step_bytes = sum((dl + 1) * es for dl in d) + n_layers * (ROUTER_BYTES + T * HIDDEN * 4 * 2)
     flops = n_layers * T * (K + 1) * 3 * 2 * HIDDEN * FFN
-    return {"tokens": T, "layers": n_layers, "ms": round(dt * 1e3, 3),
-            "tokens_per_s": round(T / dt, 1), "distinct_experts": d,
-            "gbps": round(step_bytes / dt / 1e9, 1),
-            "frac": round(step_bytes / dt / 1e9 / HBM_PEAK_GBPS, 4),
-            "tflops": round(flops / dt / 1e12, 2),
-            "mfma_util_est": round(flops / dt / 2.5e15, 4)}
+    out = {"tokens": T, "layers": n_layers, "ms": round(dt * 1e3, 3),
+           "tokens_per_s": round(T / dt, 1), "distinct_experts": d,
+           "gbps": round(step_bytes / dt / 1e9, 1),
+           "frac": round(step_bytes / dt / 1e9 / HBM_PEAK_GBPS, 4),
+           "tflops": round(flops / dt / 1e12, 2),
+           "mfma_flops_frac": round(flops / dt / 2.5e15, 4),
+           "note": ("the stack chains the synthetic layers as the workload states; their Q4_K weights "
+                    "have a positive mean, so the residual grows by orders of magnitude per layer and "
+                    "layers 2-4 route the tokens onto few experts (distinct_experts); "
+                    "per_layer_fresh below times each layer on fresh N(0,1) tokens")}
+    # each layer alone on fresh tokens: the routing spread of a real prompt
+    fresh = [make_tokens(T, 9300 + l) for l in range(n_layers)]
+    ft, fd = [], []
+    for rep in range(3):
+        for l in range(n_layers):
+            H.copy_(fresh[l])
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            F.moe_prefill([ids[l]], H, T, K, [norms[l]], idx=idx[l], stream=stream)
+            torch.cuda.synchronize()
+            if rep:
+                ft.append(time.perf_counter() - t0)
+            if rep == 2:
+                fd.append(len(torch.unique(idx[l])))
+    lt = sorted(ft)[len(ft) // 2]
+    fbytes = sum(dl + 1 for dl in fd) / n_layers * es + ROUTER_BYTES + T * HIDDEN * 4 * 2
+    out["per_layer_fresh"] = {"ms_per_layer": round(lt * 1e3, 3), "distinct_experts": fd,
+                              "tokens_per_s_4_layers": round(T / (lt * n_layers), 1),
+                              "gbps": round(fbytes / lt / 1e9, 1),
+                              "frac": round(fbytes / lt / 1e9 / HBM_PEAK_GBPS, 4)}
+    mf = load_profile_json("mfma.json", "prefill_512tok")
+    if mf:
+        out["mfma_counters"] = mf
+    return out
 
 
 def bench_dense(F, torch, args, stream, steps=60, warmup=6):
@@ -234,7 +401,8 @@ def main():
     ap.add_argument("--layers", type=int, default=12, help="resident layers rotated per step")
     ap.add_argument("--down", choices=["q4k", "q6k"], default="q4k")
     ap.add_argument("--prof-steps", type=int, default=200)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="bounded sample of each CPU baseline (seconds of host work)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--batched", default="16,64,256",
                     help="also time batched decode at these token counts ('' to skip)")
@@ -244,6 +412,9 @@ def main():
                     help="also time MLA attention of decode tokens at this KV cache length (0 to skip)")
     ap.add_argument("--dense", type=int, default=3,
                     help="also time the dense FFN over this many F16 dense layers (0 to skip)")
+    ap.add_argument("--configs", type=int, default=1,
+                    help="also time the single matvec, the single expert (Q4_K and Q6_K down) "
+                         "and the Q6_K-down layer (0 to skip)")
     ap.add_argument("--pmc-workload", action="store_true",
                     help="counter-collection run: a few layer steps, then plain 256 MiB "
                          "copies (read + write of known size) that calibrate the counters")
@@ -319,6 +490,9 @@ def main():
         phases[name] = {"launches": n, "avg_us": round(tot / max(n, 1) * 1e3, 2),
                         "min_us": round(mn * 1e3, 2), "max_us": round(mx * 1e3, 2)}
     F.prof_enable(False)
+    # per-step HIP events over the same steps: the spread of the step time
+    step_us = event_times(torch, lambda i: step(args.warmup + i), args.prof_steps)
+    F.sync(stream)
 
     lb = layer_bytes(args.down, K)
     k_us = phases["layer"]["avg_us"]
@@ -341,11 +515,12 @@ def main():
             "workload": ("DeepSeek-R1 MoE layer, batch-1 decode: fp32 router 256x7168 + "
                          "group-limited top-8 + 8 routed and 1 shared SwiGLU expert "
                          f"(Q4_K gate/up 2048x7168, {args.down.upper()} down 7168x2048), "
-                         "combine + residual; 256 experts resident per layer"),
-            "hidden": HIDDEN, "expert_ffn": FFN, "experts": 256, "top_k": K, "shared": 1,
-            "batch": 1, "down": args.down, "layers_rotated": args.layers,
-            "resident_gb": round(args.layers * (256 + 1) * layers[0].expert_size / 1e9, 1),
+                         "combine + residual; 256 experts resident per layer; "
+                         f"{args.layers} layers rotated per step "
+                         f"({round(args.layers * (256 + 1) * layers[0].expert_size / 1e9, 1)} GB "
+                         "resident), a new seeded token per step"),
         },
+        "step_us": percentiles(step_us),
         "layer_bytes": lb,
         "layer_gbps": round(layer_gbps, 1),
         "layer_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
@@ -358,10 +533,17 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": load_traffic("k_layer", f"deepseek_r1_batch1_{args.down}"),
+            "traffic_source": ("HBM bytes per launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE passes "
+                               "committed in profiles/ (traffic.json), not measured in this run"),
             "bytes_per_launch": lb,
         },
         "cpu_baseline": None,
     }
+    if args.configs:
+        result["matvec_q4k"] = bench_matvec(F, torch, args)
+        result["expert_q4k_down"] = bench_expert(F, torch, "q4k")
+        result["expert_q6k_down"] = bench_expert(F, torch, "q6k")
+        result["layer_q6k_down"] = bench_layer_q6k(F, torch, args, stream, K)
     if args.batched:
         result["batched"] = bench_batched(F, torch, layers, args, stream, K)
     if args.prefill:
@@ -371,9 +553,11 @@ def main():
     if args.attn:
         result["attn"] = bench_attn(F, torch, args, stream)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.down, args.cpu_seconds, K)
-        cb = result["cpu_baseline"]["value"]
-        result["speedup_vs_cpu"] = round(cb / us_per_token, 1)
+        ref, tuned = cpu_baseline(args.down, args.cpu_seconds, K)
+        result["cpu_baseline"] = ref
+        result["cpu_baseline_tuned"] = tuned
+        result["speedup_vs_cpu"] = {"reference_shaped": round(ref["value"] / us_per_token, 1),
+                                    "tuned_all_cores": round(tuned["value"] / us_per_token, 1)}
     print(json.dumps(result), flush=True)
 
 

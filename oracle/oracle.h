@@ -90,6 +90,9 @@ void orc_router_logits(const float *Wg, const float *x, float *logits, int n_exp
 void orc_route_ex(const float *logits, const float *bias, int n_exp, int n_group,
                   int topk_group, int K, float scale, int *exp_idx, float *exp_w);
 void orc_route(const float *logits, const float *bias, int K, int *exp_idx, float *exp_w);
+double orc_cpu_layer_tuned(const void *const *blobs, int K, int down_is_q6, const float *Wg, const float *bias,
+                           const float *x, const float *h_in, float *out, int reps, int n_threads,
+                           int *threads_used);
 
 /* ---- MoE layer ------------------------------------------------------- */
 /* The MoE branch of layer_forward for one token (infer.m:1878-1922):

@@ -77,6 +77,9 @@ def _load():
         "orc_cpu_layer_baseline": (ctypes.c_double, [ctypes.POINTER(_vp), ctypes.c_int,
                                                      ctypes.c_int, _f32p, _f32p, _f32p, _f32p,
                                                      _f32p, ctypes.c_int]),
+        "orc_cpu_layer_tuned": (ctypes.c_double, [ctypes.POINTER(_vp), ctypes.c_int, ctypes.c_int,
+                                                  _f32p, _f32p, _f32p, _f32p, _f32p, ctypes.c_int,
+                                                  ctypes.c_int, ctypes.POINTER(ctypes.c_int)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -334,6 +337,19 @@ def cpu_layer_baseline(blobs, down_is_q6, Wg, bias, x, h_in, reps):
                                   np.ascontiguousarray(x, np.float32),
                                   np.ascontiguousarray(h_in, np.float32), out, reps)
     return us, out
+
+
+def cpu_layer_tuned(blobs, down_is_q6, Wg, bias, x, h_in, reps, n_threads=0):
+    """Median microseconds per token of the tuned CPU MoE layer (fused
+    row dequant-dot over every host core); returns (us, out, threads)."""
+    arr = (ctypes.c_void_p * len(blobs))(*[b.ctypes.data for b in blobs])
+    out = np.empty(HIDDEN, dtype=np.float32)
+    used = ctypes.c_int(0)
+    us = L.orc_cpu_layer_tuned(arr, len(blobs) - 1, int(down_is_q6),
+                               np.ascontiguousarray(Wg, np.float32), np.ascontiguousarray(bias, np.float32),
+                               np.ascontiguousarray(x, np.float32), np.ascontiguousarray(h_in, np.float32),
+                               out, reps, n_threads, ctypes.byref(used))
+    return us, out, used.value
 
 
 # ---- the reference's own quant.c, compiled under _ref -------------------------
