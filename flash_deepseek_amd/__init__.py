@@ -171,6 +171,8 @@ def moe_forward_host(L, h_post, exp_idx, exp_w, K, moe_out):
 
 BATCH_AUTO, BATCH_DOT4, BATCH_MFMA = 0, 1, 2
 BATCH_MFMA_MIN_T = 6
+NOALLOC_MAX_T = 32  # FDM_NOALLOC_MAX_T
+NOALLOC_MAX_PAIRS = 256  # FDM_NOALLOC_MAX_PAIRS
 
 
 def set_batch_kernel(mode):
@@ -194,6 +196,15 @@ def moe_forward_batched(L, X, H_in, T, K, hidden, idx=None, w=None, n_distinct=N
     """T tokens through the MoE branch of layer L in one step, each selected
     expert's weights read once: hidden[t] = H_in[t] + routed + shared."""
     call("fdm_moe_forward_batched", L, _p(X), _p(H_in), T, K, _p(hidden), _p(idx), _p(w),
+         _p(n_distinct), _stream(stream))
+
+
+def moe_forward_batched_noalloc(L, X, H_in, T, K, hidden, idx=None, w=None, n_distinct=None,
+                                stream=None):
+    """moe_forward_batched on the library's fixed device scratch: allocates
+    nothing (T <= NOALLOC_MAX_T, T*K <= NOALLOC_MAX_PAIRS).  Calls that
+    overlap on one device share that scratch and race."""
+    call("fdm_moe_forward_batched_noalloc", L, _p(X), _p(H_in), T, K, _p(hidden), _p(idx), _p(w),
          _p(n_distinct), _stream(stream))
 
 

@@ -18,6 +18,50 @@
 #include "fdm_internal.h"
 
 namespace fdm {
+// ---- the scratch of fdm_moe_forward_batched_noalloc ------------------------------------
+// A file-scope device array holding every BatchScratch buffer of a step of
+// up to FDM_NOALLOC_MAX_T tokens and FDM_NOALLOC_MAX_PAIRS (token, expert)
+// pairs, each at a 256-byte boundary.  Each device holds its own copy until
+// the process ends.  In host code `scratch` is only a stand-in for the
+// symbol: its device address comes from hipGetSymbolAddress at fdm_init
+// (g_scratch_ptr), and only that address is handed to kernels.
+constexpr size_t kNaRows = (size_t)FDM_NOALLOC_MAX_PAIRS + FDM_NOALLOC_MAX_T;
+constexpr size_t kNaElems = (size_t)FDM_NOALLOC_MAX_T * FDM_HIDDEN > kNaRows * FDM_MOE_FFN
+                                ? (size_t)FDM_NOALLOC_MAX_T * FDM_HIDDEN
+                                : kNaRows * FDM_MOE_FFN;
+enum NaPart { kNaXd, kNaLogits, kNaIdx, kNaW, kNaSeg, kNaPairTok, kNaPairOf, kNaDistinct, kNaNDistinct,
+              kNaAct, kNaActXd, kNaEo, kNaPlanes, kNaXs, kNaXe, kNaChunks, kNaNChunks, kNaParts };
+constexpr size_t kNaBytes[kNaParts] = {
+    (size_t)FDM_NOALLOC_MAX_T * (FDM_HIDDEN / 64) * sizeof(XGroup),  // xd
+    (size_t)FDM_NOALLOC_MAX_T * FDM_N_EXPERTS * sizeof(float),      // logits
+    (size_t)FDM_NOALLOC_MAX_PAIRS * sizeof(int),                    // idx
+    (size_t)FDM_NOALLOC_MAX_PAIRS * sizeof(float),                  // w
+    (FDM_N_EXPERTS + 1) * sizeof(int),                              // seg
+    (size_t)FDM_NOALLOC_MAX_PAIRS * sizeof(int),                    // pair_tok
+    (size_t)FDM_NOALLOC_MAX_PAIRS * sizeof(int),                    // pair_of
+    FDM_N_EXPERTS * sizeof(int),                                    // distinct
+    sizeof(int),                                                    // n_distinct
+    kNaRows * FDM_MOE_FFN * sizeof(float),                          // act
+    kNaRows * (FDM_MOE_FFN / 64) * sizeof(XGroup),                  // act_xd
+    kNaRows * FDM_HIDDEN * sizeof(float),                           // eo
+    3 * kNaElems * sizeof(_Float16),                                // planes
+    kNaElems / 32 * sizeof(float),                                  // xs
+    kNaRows * sizeof(float),                                        // xe
+    kQMaxChunks * sizeof(int4),                                     // chunks
+    sizeof(int),                                                    // n_chunks
+};
+constexpr size_t na_offset(int part) {
+  size_t o = 0;
+  for (int i = 0; i < part; ++i) o += (kNaBytes[i] + 255) / 256 * 256;
+  return o;
+}
+constexpr size_t kNaTotal = na_offset(kNaParts);
+static_assert(kNaTotal == FDM_NOALLOC_SCRATCH_BYTES, "FDM_NOALLOC_SCRATCH_BYTES is out of date");
+}  // namespace fdm
+
+static __device__ __align__(256) unsigned char scratch[fdm::kNaTotal];
+
+namespace fdm {
 
 int g_num_cus = 0;
 int g_batch_mode = FDM_BATCH_AUTO;
@@ -44,6 +88,19 @@ int hip_fail(hipError_t e, const char* what) {
     hipError_t e_ = (call);                             \
     if (e_ != hipSuccess) return hip_fail(e_, #call);   \
   } while (0)
+
+constexpr int kMaxDevices = 64;
+unsigned char* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch`, per device
+
+// Records the device address of `scratch` on the current device (once).
+int bind_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return fail(FDM_E_INVAL, "device %d >= %d", device, kMaxDevices);
+  if (g_scratch_ptr[device]) return FDM_OK;
+  void* ptr = nullptr;
+  FDM_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  g_scratch_ptr[device] = static_cast<unsigned char*>(ptr);
+  return FDM_OK;
+}
 
 struct Workspace {
   XGroup* xd = nullptr;       // digits of activations (up to FDM_MAX_TOKENS x 112)
@@ -633,6 +690,7 @@ int fdm_init(int device) {
     return fail(FDM_E_NODEV, "device %d is %s; this build targets gfx950", device,
                 prop.gcnArchName);
   g_num_cus = prop.multiProcessorCount;
+  if (int rc = bind_scratch(device)) return rc;
   if (int rc = alloc_workspace()) {
     free_workspace();
     return rc;
@@ -1148,6 +1206,8 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
 }
 
 // ---- batched decode ---------------------------------------------------------------------
+}  // extern "C"
+
 namespace fdm {
 namespace {
 // Per-row buffers of the batched path, grown (never shrunk) to `rows`.
@@ -1216,40 +1276,55 @@ int max_chunks(int T, int K, int ch) {
   return std::min(256, T * K) + (T * K + ch - 1) / ch + (T + ch - 1) / ch;
 }
 
+// Buffers of the grouped GEMMs: activation planes ([3][elems] fp16), their
+// sub-block sums and row scales, and the chunk list.
+struct QScratch {
+  _Float16* planes;
+  float* xs;
+  float* xe;
+  int4* chunks;
+  int* n_chunks;
+};
+
+QScratch workspace_q() {
+  const Workspace& w = g.ws;
+  return QScratch{w.q_planes, w.q_xs, w.q_xe, w.q_chunks, w.q_nchunks};
+}
+
 // The expert half of one step on the grouped GEMMs, after the dispatch:
 // chunk list, planes of the token rows, gate/up + SwiGLU into b.act, then
 // a Q4_K down on the GEMM (planes of b.act first) or a Q6_K down on the
 // dot4 kernels, into b.eo.  x: the fp32 token rows [T][7168].
-int run_qgemm_experts(const Layer* y, const BatchArgs& b, const float* x, int planes, hipStream_t s) {
-  Workspace& w = g.ws;
+int run_qgemm_experts(const Layer* y, const BatchArgs& b, const float* x, int planes, const QScratch& w,
+                      hipStream_t s) {
   const int T = b.T, K = b.K;
   const size_t rows = (size_t)T * K + (y->shared ? T : 0);
   const int ch = qgemm_chunk_tokens(planes);
   const int mc = max_chunks(T, K, ch);
   if (mc > kQMaxChunks) return fail(FDM_E_INVAL, "chunk list of %d entries exceeds %d", mc, kQMaxChunks);
-  FDM_HIP(launch_qchunks(b.seg_start, b.distinct, b.n_distinct, T, y->shared != nullptr, ch, w.q_chunks,
-                         w.q_nchunks, s));
-  FDM_HIP(launch_xplanes(x, FDM_HIDDEN, (size_t)T, planes, w.q_planes, w.q_xs, w.q_xe, s));
+  FDM_HIP(launch_qchunks(b.seg_start, b.distinct, b.n_distinct, T, y->shared != nullptr, ch, w.chunks,
+                         w.n_chunks, s));
+  FDM_HIP(launch_xplanes(x, FDM_HIDDEN, (size_t)T, planes, w.planes, w.xs, w.xe, s));
   QGemmArgs q;
   q.T = T;
   q.K = K;
   q.experts = y->experts;
   q.expert_size = y->expert_size;
   q.shared = y->shared;
-  q.xp = w.q_planes;
+  q.xp = w.planes;
   q.plane = (size_t)T * FDM_HIDDEN;
-  q.xs = w.q_xs;
-  q.xe = w.q_xe;
+  q.xs = w.xs;
+  q.xe = w.xe;
   q.pair_tok = b.pair_tok;
-  q.chunks = w.q_chunks;
-  q.n_chunks = w.q_nchunks;
+  q.chunks = w.chunks;
+  q.n_chunks = w.n_chunks;
   q.out = b.act;
   FDM_HIP(launch_qgemm(q, planes, false, mc, s));
   if (y->down_q6) {
     FDM_HIP(launch_batched_down(b, true, s));
     return FDM_OK;
   }
-  FDM_HIP(launch_xplanes(b.act, FDM_MOE_FFN, rows, planes, w.q_planes, w.q_xs, w.q_xe, s));
+  FDM_HIP(launch_xplanes(b.act, FDM_MOE_FFN, rows, planes, w.planes, w.xs, w.xe, s));
   q.plane = rows * FDM_MOE_FFN;
   q.out = b.eo;
   FDM_HIP(launch_qgemm(q, planes, true, mc, s));
@@ -1257,6 +1332,8 @@ int run_qgemm_experts(const Layer* y, const BatchArgs& b, const float* x, int pl
 }
 }  // namespace
 }  // namespace fdm
+
+extern "C" {
 
 int fdm_rms_norm(const float* d_x, const float* d_w, float* d_o, int T, int d, void* stream) {
   if (int rc = check_ready()) return rc;
@@ -1310,30 +1387,46 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     b.n_distinct = g.ws.b_ndistinct;
     FDM_HIP(launch_dispatch(b, s));
     // prefill precision: one fp16 plane of the activations (the bar is 1e-2)
-    if (int rc = run_qgemm_experts(y, b, g.ws.p_hpost, 1, s)) return rc;
+    if (int rc = run_qgemm_experts(y, b, g.ws.p_hpost, 1, workspace_q(), s)) return rc;
     FDM_HIP(launch_combine(b, s));
   }
   return FDM_OK;
 }
 
-int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T, int K,
-                            float* d_hidden, int* d_idx, float* d_w, int* d_n_distinct,
-                            void* stream) {
-  Layer* y = nullptr;
-  if (int rc = get_layer(L, &y)) return rc;
-  if (int rc = check_K(K)) return rc;
-  if (T < 1 || T > FDM_MAX_TOKENS)
-    return fail(FDM_E_INVAL, "T=%d outside 1..%d", T, FDM_MAX_TOKENS);
-  if (!d_X || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
-  if (!aligned(d_X, 16)) return fail(FDM_E_INVAL, "X must be 16-byte aligned");
-  hipStream_t s = as_stream(stream);
-  const size_t rows = (size_t)T * K + (y->shared ? T : 0);
-  if (int rc = ensure_batch_rows(rows, s)) return rc;
-  int* idx = d_idx ? d_idx : g.ws.idx;
-  float* w = d_w ? d_w : g.ws.w;
+}  // extern "C"
+
+namespace fdm {
+namespace {
+// Every buffer one batched step uses besides its inputs and outputs.
+struct BatchScratch {
+  XGroup* xd;       // [T][112] digits of the tokens (dot4 path)
+  float* logits;    // [T][256]
+  int* idx;         // [T][K] routing when the caller passes none
+  float* w;         // [T][K]
+  int* seg;         // [257]
+  int* pair_tok;    // [T*K]
+  int* pair_of;     // [T*K]
+  int* distinct;    // [256]
+  int* n_distinct;  // [1] when the caller passes none
+  float* act;       // [rows][2048]
+  XGroup* act_xd;   // [rows][32]
+  float* eo;        // [rows][7168]
+  QScratch q;       // grouped GEMM buffers (MFMA path)
+};
+
+bool batch_uses_mfma(int T) {
+  return g_batch_mode == FDM_BATCH_MFMA || (g_batch_mode == FDM_BATCH_AUTO && T >= FDM_BATCH_MFMA_MIN_T);
+}
+
+// One batched step (the body of fdm_moe_forward_batched and of its
+// no-allocation variant) on buffers the caller has sized for T, K.
+int batched_step(const Layer* y, const float* d_X, const float* d_H_in, int T, int K, float* d_hidden,
+                 int* d_idx, float* d_w, int* d_n_distinct, const BatchScratch& sc, hipStream_t s) {
+  int* idx = d_idx ? d_idx : sc.idx;
+  float* w = d_w ? d_w : sc.w;
   ProfScope p(FDM_PROF_BATCH, s);
-  FDM_HIP(launch_router_logits(y->Wg, d_X, FDM_N_EXPERTS, FDM_HIDDEN, T, g.ws.logits, s));
-  FDM_HIP(launch_route(g.ws.logits, y->bias, T, K, idx, w, s));
+  FDM_HIP(launch_router_logits(y->Wg, d_X, FDM_N_EXPERTS, FDM_HIDDEN, T, sc.logits, s));
+  FDM_HIP(launch_route(sc.logits, y->bias, T, K, idx, w, s));
   BatchArgs b;
   b.T = T;
   b.K = K;
@@ -1345,27 +1438,90 @@ int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T,
   b.out = d_hidden;
   b.idx = idx;
   b.w = w;
-  b.xd = g.ws.xd;
-  b.act = g.ws.b_act;
-  b.act_xd = g.ws.b_act_xd;
-  b.eo = g.ws.b_eo;
-  b.seg_start = g.ws.b_seg;
-  b.pair_tok = g.ws.b_pair_tok;
-  b.pair_of = g.ws.b_pair_of;
-  b.distinct = g.ws.b_distinct;
-  b.n_distinct = d_n_distinct ? d_n_distinct : g.ws.b_ndistinct;
-  const bool mfma = g_batch_mode == FDM_BATCH_MFMA ||
-                    (g_batch_mode == FDM_BATCH_AUTO && T >= FDM_BATCH_MFMA_MIN_T);
-  if (!mfma) {
+  b.xd = sc.xd;
+  b.act = sc.act;
+  b.act_xd = sc.act_xd;
+  b.eo = sc.eo;
+  b.seg_start = sc.seg;
+  b.pair_tok = sc.pair_tok;
+  b.pair_of = sc.pair_of;
+  b.distinct = sc.distinct;
+  b.n_distinct = d_n_distinct ? d_n_distinct : sc.n_distinct;
+  if (!batch_uses_mfma(T)) {
     FDM_HIP(launch_batched_experts(b, y->down_q6, s));
     return FDM_OK;
   }
   // grouped MFMA GEMMs at fp32 grade (three fp16 planes of the activations)
-  if (int rc = ensure_planes(T, rows, s)) return rc;
   FDM_HIP(launch_dispatch(b, s));
-  if (int rc = run_qgemm_experts(y, b, d_X, 3, s)) return rc;
+  if (int rc = run_qgemm_experts(y, b, d_X, 3, sc.q, s)) return rc;
   FDM_HIP(launch_combine(b, s));
   return FDM_OK;
+}
+
+int check_batched_args(int L, const float* d_X, int T, int K, float* d_hidden, Layer** y) {
+  if (int rc = get_layer(L, y)) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (T < 1 || T > FDM_MAX_TOKENS) return fail(FDM_E_INVAL, "T=%d outside 1..%d", T, FDM_MAX_TOKENS);
+  if (!d_X || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(d_X, 16)) return fail(FDM_E_INVAL, "X must be 16-byte aligned");
+  return FDM_OK;
+}
+
+BatchScratch noalloc_scratch(unsigned char* base) {
+  auto at = [base](NaPart part) { return static_cast<void*>(base + na_offset(part)); };
+  BatchScratch sc;
+  sc.xd = static_cast<XGroup*>(at(kNaXd));
+  sc.logits = static_cast<float*>(at(kNaLogits));
+  sc.idx = static_cast<int*>(at(kNaIdx));
+  sc.w = static_cast<float*>(at(kNaW));
+  sc.seg = static_cast<int*>(at(kNaSeg));
+  sc.pair_tok = static_cast<int*>(at(kNaPairTok));
+  sc.pair_of = static_cast<int*>(at(kNaPairOf));
+  sc.distinct = static_cast<int*>(at(kNaDistinct));
+  sc.n_distinct = static_cast<int*>(at(kNaNDistinct));
+  sc.act = static_cast<float*>(at(kNaAct));
+  sc.act_xd = static_cast<XGroup*>(at(kNaActXd));
+  sc.eo = static_cast<float*>(at(kNaEo));
+  sc.q = QScratch{static_cast<_Float16*>(at(kNaPlanes)), static_cast<float*>(at(kNaXs)),
+                  static_cast<float*>(at(kNaXe)), static_cast<int4*>(at(kNaChunks)),
+                  static_cast<int*>(at(kNaNChunks))};
+  return sc;
+}
+}  // namespace
+}  // namespace fdm
+
+extern "C" {
+
+int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T, int K,
+                            float* d_hidden, int* d_idx, float* d_w, int* d_n_distinct,
+                            void* stream) {
+  Layer* y = nullptr;
+  if (int rc = check_batched_args(L, d_X, T, K, d_hidden, &y)) return rc;
+  hipStream_t s = as_stream(stream);
+  const size_t rows = (size_t)T * K + (y->shared ? T : 0);
+  if (int rc = ensure_batch_rows(rows, s)) return rc;
+  if (batch_uses_mfma(T)) {
+    if (int rc = ensure_planes(T, rows, s)) return rc;
+  }
+  const Workspace& w = g.ws;
+  const BatchScratch sc{w.xd,         w.logits,   w.idx,      w.w,        w.b_seg,
+                        w.b_pair_tok, w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act,
+                        w.b_act_xd,   w.b_eo,      workspace_q()};
+  return batched_step(y, d_X, d_H_in, T, K, d_hidden, d_idx, d_w, d_n_distinct, sc, s);
+}
+
+int fdm_moe_forward_batched_noalloc(int L, const float* d_X, const float* d_H_in, int T, int K,
+                                    float* d_hidden, int* d_idx, float* d_w, int* d_n_distinct,
+                                    void* stream) {
+  Layer* y = nullptr;
+  if (int rc = check_batched_args(L, d_X, T, K, d_hidden, &y)) return rc;
+  if (T > FDM_NOALLOC_MAX_T || T * K > FDM_NOALLOC_MAX_PAIRS)
+    return fail(FDM_E_INVAL, "T=%d, K=%d exceed the no-allocation scratch (T <= %d, T*K <= %d)", T, K,
+                FDM_NOALLOC_MAX_T, FDM_NOALLOC_MAX_PAIRS);
+  unsigned char* base = g_scratch_ptr[g.device];
+  if (!base) return fail(FDM_E_STATE, "no-allocation scratch not bound on device %d", g.device);
+  return batched_step(y, d_X, d_H_in, T, K, d_hidden, d_idx, d_w, d_n_distinct, noalloc_scratch(base),
+                      as_stream(stream));
 }
 
 int fdm_set_layer_spin_limit(unsigned polls, unsigned* prev) {

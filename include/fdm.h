@@ -261,6 +261,24 @@ int fdm_moe_forward_batched(int L, const float *d_X, const float *d_H_in, int T,
                             float *d_hidden, int *d_idx, float *d_w, int *d_n_distinct,
                             void *stream);
 
+/* ---- fdm_moe_forward_batched without allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as fdm_moe_forward_batched, but
+ * every buffer of the step lives in one device array of the library
+ * (FDM_NOALLOC_SCRATCH_BYTES, about 16 MiB per device, held until the
+ * process ends) instead of the workspace fdm_moe_forward_batched grows on
+ * demand; the call allocates nothing.  Limits: T <= FDM_NOALLOC_MAX_T and
+ * T*K <= FDM_NOALLOC_MAX_PAIRS, else FDM_E_INVAL.  All calls on one device
+ * share that array: calls that overlap on one device (on different
+ * streams) race. */
+#define FDM_NOALLOC_MAX_T 32
+#define FDM_NOALLOC_MAX_PAIRS 256
+#define FDM_NOALLOC_SCRATCH_BYTES 16949248ull
+int fdm_moe_forward_batched_noalloc(int L, const float *d_X, const float *d_H_in, int T, int K,
+                                    float *d_hidden, int *d_idx, float *d_w, int *d_n_distinct,
+                                    void *stream);
+
 /* Expert kernels behind fdm_moe_forward_batched (no counterpart in the
  * reference; a tuning and test switch).  FDM_BATCH_DOT4: per-token int8
  * digit dot products, each expert tile held in registers while its tokens
