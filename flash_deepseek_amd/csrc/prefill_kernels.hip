@@ -1,69 +1,75 @@
-// prefill_kernels.hip -- rms_norm of the tokens of a prefill step (and of
-// the attention's norms): rms_norm (infer.m:369-374) on the device,
-// bit-exact.  Prefill runs h <- h + MoE(rms_norm(h, w_l)) per layer
-// (infer.m:1850, 1878-1922); its expert GEMMs are in gemm_kernels.hip.
+// prefill_kernels.hip -- rms_norm (infer.m:369-374) on the device, bit-exact:
+// the tokens of a prefill step (infer.m:1850, 1878-1922) and the attention's
+// norms.  Its expert GEMMs are in gemm_kernels.hip.
 #include "fdm_internal.h"
+#include "rms_device.h"
 
 namespace fdm {
 
-// ---- rms_norm: h_post = x * (1 / sqrt(sum x^2 / d + 1e-6)) * w ---------------------------
-// One workgroup per token.  The sum of squares is taken in index order by
-// one thread with one fused multiply-add per element, as the reference's
-// loop compiles (infer.m:369-374: clang contracts `ss += x[i]*x[i]`), so
-// h_post -- and with it the routing -- is bit-exact; sqrt and division are
-// IEEE.
-__global__ __launch_bounds__(256) void k_rms_norm(const float* __restrict__ x,
-                                                  const float* __restrict__ w, float* __restrict__ o,
-                                                  int d, float eps) {
-#pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float row[kHidden];
-  __shared__ float inv_s;
+// ---- rms_norm: o = x * (1 / sqrt(sum x^2 / d + 1e-6)) * w -------------------------------
+// One workgroup per token.  The sum of squares is the reference's
+// sequential fma chain, evaluated bit for bit by rms_sumsq_exact (runs of
+// integer steps inside a binade, the steps at binade edges and ties walked
+// in order); sqrt and division are IEEE; o = (x * inv) * w as infer.m:372.
+// At d = 7168 (16-byte aligned rows) every load is a 16-byte vector load
+// issued before the sum, so the row's latency is paid once.
+__global__ __launch_bounds__(kRmsThreads) void k_rms_norm(const float* __restrict__ x,
+                                                          const float* __restrict__ w, float* o, int d) {
+  __shared__ RmsSmem sm;
   const float* xr = x + (size_t)blockIdx.x * d;
-  for (int i = threadIdx.x; i < d; i += 256) row[i] = xr[i];
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    // the reference's loop as compiled: ss = fma(x_i, x_i, ss) in index order
-    // (clang contracts `ss += x[i]*x[i]`); one dependent chain, fed 16
-    // values at a time from LDS so the reads run ahead of it
-    float ss = 0.0f;
-    const int n64 = d / 64;
-    const f32x4* r4 = reinterpret_cast<const f32x4*>(row);
-    f32x4 buf[2][16];  // 64 values per chunk, the next chunk's reads in flight
-    if (n64 > 0) {
+  float* orow = o + (size_t)blockIdx.x * d;
+  const int n = (d + kRmsThreads - 1) / kRmsThreads;
+  const int i0 = threadIdx.x * n;
+  const bool vec = d == kHidden && (reinterpret_cast<uintptr_t>(xr) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(orow) & 15) == 0 &&
+                   (!w || (reinterpret_cast<uintptr_t>(w) & 15) == 0);
+  float xv[kRmsMaxPer];
+  if (vec) {
+    constexpr int kV = kHidden / 4 / kRmsThreads;  // 7 vectors per thread
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(xr);
+    f32x4 xc[kV], wc[kV];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) buf[0][k] = r4[k];
+    for (int k = 0; k < kV; ++k) {
+      const f32x4 v = x4[i0 / 4 + k];  // the thread's 28 consecutive elements
+      xv[4 * k] = v.x;
+      xv[4 * k + 1] = v.y;
+      xv[4 * k + 2] = v.z;
+      xv[4 * k + 3] = v.w;
+      xc[k] = x4[threadIdx.x + kRmsThreads * k];  // coalesced, for the output
+      wc[k] = w ? reinterpret_cast<const f32x4*>(w)[threadIdx.x + kRmsThreads * k] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
     }
-    for (int c = 0; c < n64; c += 2) {
+    const float inv = rms_inv(rms_sumsq_exact(xv, d, sm), d);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        if (c + h >= n64) break;
-        if (c + h + 1 < n64) {
-#pragma unroll
-          for (int k = 0; k < 16; ++k) buf[h ^ 1][k] = r4[16 * (c + h + 1) + k];
-        }
-#pragma unroll
-        for (int k = 0; k < 16; ++k) {
-          const f32x4 v = buf[h][k];
-          ss = fmaf(v.x, v.x, ss);
-          ss = fmaf(v.y, v.y, ss);
-          ss = fmaf(v.z, v.z, ss);
-          ss = fmaf(v.w, v.w, ss);
-        }
+    for (int k = 0; k < kV; ++k) {
+      f32x4 v;
+      v.x = xc[k].x * inv;
+      v.y = xc[k].y * inv;
+      v.z = xc[k].z * inv;
+      v.w = xc[k].w * inv;
+      if (w) {
+        v.x = v.x * wc[k].x;
+        v.y = v.y * wc[k].y;
+        v.z = v.z * wc[k].z;
+        v.w = v.w * wc[k].w;
       }
+      reinterpret_cast<f32x4*>(orow)[threadIdx.x + kRmsThreads * k] = v;
     }
-    for (int i = 64 * n64; i < d; ++i) ss = fmaf(row[i], row[i], ss);
-    inv_s = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ss, (float)d) + eps));
+    return;
   }
-  __syncthreads();
-  const float inv = inv_s;
-  for (int i = threadIdx.x; i < d; i += 256) {
-    const float v = w ? (row[i] * inv) * w[i] : row[i] * inv;
-    o[(size_t)blockIdx.x * d + i] = v;
+#pragma unroll
+  for (int j = 0; j < kRmsMaxPer; ++j) {
+    const float v = xr[min(i0 + j, d - 1)];  // every slot loads; past the row it is a zero step
+    xv[j] = (j < n && i0 + j < d) ? v : 0.0f;
+  }
+  const float inv = rms_inv(rms_sumsq_exact(xv, d, sm), d);
+  for (int i = threadIdx.x; i < d; i += kRmsThreads) {
+    const float v = xr[i] * inv;
+    orow[i] = w ? v * w[i] : v;
   }
 }
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* o, int T, int d, hipStream_t s) {
-  hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(256), 0, s, x, w, o, d, 1e-6f);
+  hipLaunchKernelGGL(k_rms_norm, dim3(T), dim3(kRmsThreads), 0, s, x, w, o, d);
   return hipGetLastError();
 }
 

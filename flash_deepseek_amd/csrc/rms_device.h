@@ -1,0 +1,231 @@
+// rms_device.h -- the sum of squares of rms_norm (infer.m:369-374) on one
+// 256-thread workgroup, bit for bit, without its 7,168 dependent steps.
+//
+// The reference's loop compiles to one chain ss <- fma(x_i, x_i, ss) in
+// index order (clang contracts `ss += x[i]*x[i]`).  Each step rounds
+// ss + x_i^2 (exact product) to float.  While ss stays inside one binade
+// [2^e, 2^(e+1)) its grid is u = 2^(e-23) and ss is a multiple of u, so the
+// step is ss + u * rint(x_i^2 / u) -- independent of ss -- unless the sum
+// leaves the binade or x_i^2 / u is a tie (then round-half-even looks at
+// ss).  The chain is therefore a sum of integers inside each binade, and
+// only the steps near a binade boundary (and ties) need the real fma:
+//
+//  1. P_i = sum_{j<i} x_j^2, summed in float (a block scan), approximates
+//     the true chain value before step i: every step of the chain rounds by
+//     at most 2^-24 of the running sum, so |ss_i - sum_{j<i} x_j^2| <=
+//     i 2^-24 ss_i <= 2^-11 ss_i (d <= 8192), and the float prefix adds
+//     less than 2^-18 more.
+//  2. Step i is a "run" step when P_i and P_i + x_i^2 both lie inside one
+//     binade with a relative margin of 2^-10 to its ends (so the true ss_i
+//     and ss_(i+1) lie in it too), P_i >= 2^-100 (normal grid) and the
+//     exact x_i^2 / u (in double) is not a tie; it then adds
+//     K_i = rint(x_i^2 / u) < 2^23.  Every other step is "risky" (the first
+//     step always is: P_0 = 0).
+//  3. Consecutive run steps share one binade, so a run adds exactly
+//     u * (sum of its K) -- one float addition, exact because the result
+//     stays on the grid inside the binade.  The K are summed mod 2^32 (a
+//     run's sum is < 2^24, so differences of the prefix are exact).  The
+//     risky steps, in order, are walked by one lane:
+//     ss <- ss + c_k; ss <- fma(x_r, x_r, ss).
+//
+// Inputs with more than kRmsMaxRisky risky steps (sums that stay below
+// 2^-100, ties everywhere) take the plain chain instead, as do non-finite
+// inputs (every step after them is risky).
+#pragma once
+
+#include "fdm_device.h"
+
+namespace fdm {
+
+constexpr int kRmsThreads = 256;
+constexpr int kRmsMaxPer = kHidden / kRmsThreads;  // elements per thread at d = 7168 (28)
+constexpr int kRmsMaxRisky = 512;
+
+struct RmsSmem {
+  unsigned k[kHidden];        // per element: K_i of a run step, kRmsRisky for a risky step
+  float rx[kRmsMaxRisky];     // risky steps in order: x_r,
+  unsigned rq[kRmsMaxRisky];  //   sum of K before r (mod 2^32),
+  int re[kRmsMaxRisky];       //   exponent E of P_r (the run before r lies in [2^(E-1), 2^E))
+  float rc[kRmsMaxRisky + 1];  // the run added before risky step k (and after the last)
+  float wf[4];
+  unsigned wk[4];
+  int wr[4];
+  float ss;
+};
+constexpr unsigned kRmsRisky = 0xFFFFFFFFu;
+
+// DPP move of a 32-bit value (lanes without a source receive 0).
+template <int CTRL, int ROW_MASK, typename T>
+__device__ __forceinline__ T dpp_zero(T x) {
+  int bits;
+  __builtin_memcpy(&bits, &x, 4);
+  bits = __builtin_amdgcn_update_dpp(0, bits, CTRL, ROW_MASK, 0xF, false);
+  T r;
+  __builtin_memcpy(&r, &bits, 4);
+  return r;
+}
+
+// Inclusive scan over the 64 lanes of a wave by DPP: row shifts 1, 2, 4, 8
+// within each row of 16 lanes, then row_bcast 15 / 31 carry rows 0 -> 1,
+// 2 -> 3 and 1 -> 2, 3 (lanes without a source add 0).
+template <typename T>
+__device__ __forceinline__ T wave_scan_incl(T v) {
+  v = v + dpp_zero<0x111, 0xF>(v);  // row_shr:1
+  v = v + dpp_zero<0x112, 0xF>(v);  // row_shr:2
+  v = v + dpp_zero<0x114, 0xF>(v);  // row_shr:4
+  v = v + dpp_zero<0x118, 0xF>(v);  // row_shr:8
+  v = v + dpp_zero<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+  v = v + dpp_zero<0x143, 0xC>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
+// Exclusive prefix over the workgroup (256 threads, thread order) of a
+// value; the total in *tot.  Ends with every thread past its reads of the
+// wave sums (the array may be reused).
+template <typename T>
+__device__ __forceinline__ T rms_block_excl(T v, T* wsum, T& tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const T inc = wave_scan_incl(v);
+  if (lane == 63) wsum[wave] = inc;
+  __syncthreads();
+  T base = T(0), all = T(0);
+#pragma unroll
+  for (int w = 0; w < kRmsThreads / 64; ++w) {
+    const T s = wsum[w];
+    base = w < wave ? base + s : base;
+    all = all + s;
+  }
+  tot = all;
+  __syncthreads();
+  return base + (inc - v);
+}
+
+// The sum of squares below for one thread layout: FULL when every thread
+// holds kRmsMaxPer elements (d = 7168: straight-line code), else the first
+// n slots of xv are the thread's (a uniform test per slot).
+template <bool FULL>
+__device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], int d, int n, RmsSmem& sm) {
+#pragma clang fp contract(off)
+  const int t = threadIdx.x;
+  const int i0 = t * n;
+  auto mine = [&](int j) { return FULL || j < n; };
+  // 1. the approximate prefix before the thread's first element
+  float tot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRmsMaxPer; ++j)
+    if (mine(j)) tot = tot + xv[j] * xv[j];
+  float total_f;
+  const float base = rms_block_excl(tot, sm.wf, total_f);
+  // 2. classify each step; K of the run steps into LDS
+  const float lo_margin = 0.5f * (1.0f + 0x1p-10f);  // frexp mantissa of P_i at least this
+  const float hi_margin = 1.0f - 0x1p-10f;           // (P_i + x^2) / 2^E at most this
+  float p = base;
+  unsigned ksum = 0;
+  int nrisky = 0;
+#pragma unroll
+  for (int j = 0; j < kRmsMaxPer; ++j) {
+    if (mine(j)) {
+      const float after = p + xv[j] * xv[j];
+      int E;
+      const float m = frexpf(p, &E);  // p = m 2^E, m in [0.5, 1)
+      const double q = ldexp((double)xv[j] * (double)xv[j], 24 - E);  // exact x^2 / u, u = 2^(E - 24)
+      const double K = rint(q);
+      const bool risky = !(p >= 0x1p-100f) || !(after < 0x1p126f) || !(m >= lo_margin) ||
+                         !(ldexpf(after, -E) <= hi_margin) || fabs(q - K) == 0.5;
+      const unsigned k = risky ? kRmsRisky : (unsigned)K;
+      sm.k[i0 + j] = k;
+      ksum += risky ? 0u : k;
+      nrisky += risky ? 1 : 0;
+      p = after;
+    }
+  }
+  unsigned ktot;
+  int rtot;
+  const unsigned kbase = rms_block_excl(ksum, sm.wk, ktot);
+  const int rbase = rms_block_excl(nrisky, sm.wr, rtot);
+  if (rtot > kRmsMaxRisky) {
+    // too many risky steps for the list: the plain chain by one lane, over
+    // the inputs gathered in LDS (in place of the K values)
+#pragma unroll
+    for (int j = 0; j < kRmsMaxPer; ++j)
+      if (mine(j)) sm.k[i0 + j] = __float_as_uint(xv[j]);
+    __syncthreads();
+    if (t == 0) {
+      float ss = 0.0f;
+      for (int i = 0; i < d; ++i) ss = fmaf(__uint_as_float(sm.k[i]), __uint_as_float(sm.k[i]), ss);
+      sm.ss = ss;
+    }
+    __syncthreads();
+    return sm.ss;
+  }
+  // 3. the risky steps in order: x, the K sum before them, the binade of P
+  p = base;
+  unsigned kq = kbase;
+  int r = rbase;
+#pragma unroll
+  for (int j = 0; j < kRmsMaxPer; ++j) {
+    if (mine(j)) {
+      const unsigned k = sm.k[i0 + j];
+      if (k == kRmsRisky) {
+        int E;
+        (void)frexpf(p, &E);
+        sm.rx[r] = xv[j];
+        sm.rq[r] = kq;
+        sm.re[r] = E;
+        ++r;
+      } else {
+        kq += k;
+      }
+      p = p + xv[j] * xv[j];
+    }
+  }
+  __syncthreads();
+  // 4. the run before each risky step, and the final run, as exact floats
+  for (int k = t; k <= rtot; k += kRmsThreads) {
+    unsigned q1;
+    int E;
+    if (k < rtot) {
+      q1 = sm.rq[k];
+      E = sm.re[k];
+    } else {
+      q1 = ktot;
+      (void)frexpf(total_f, &E);
+    }
+    const unsigned q0 = k > 0 ? sm.rq[k - 1] : 0u;
+    const unsigned run = q1 - q0;  // < 2^24 when not 0: a run stays in one binade
+    sm.rc[k] = run ? ldexpf((float)run, E - 24) : 0.0f;
+  }
+  __syncthreads();
+  // 5. the walk: one lane, two dependent operations per risky step
+  if (t == 0) {
+    float ss = 0.0f;
+#pragma unroll 4
+    for (int k = 0; k < rtot; ++k) {
+      ss = ss + sm.rc[k];
+      ss = fmaf(sm.rx[k], sm.rx[k], ss);
+    }
+    sm.ss = ss + sm.rc[rtot];
+  }
+  __syncthreads();
+  return sm.ss;
+}
+
+// The reference's sum of squares of x[0..d) (d <= 7168), as a float, in
+// every thread.  Thread t passes its elements t*n .. t*n+n-1 (n = ceil(d /
+// 256)) in xv[0..n), zeros for those past d (steps that leave the chain
+// unchanged: fma(0, 0, ss) = ss, K = 0).
+__device__ __forceinline__ float rms_sumsq_exact(const float (&xv)[kRmsMaxPer], int d, RmsSmem& sm) {
+  const int n = (d + kRmsThreads - 1) / kRmsThreads;
+  return n == kRmsMaxPer ? rms_sumsq_impl<true>(xv, d, n, sm) : rms_sumsq_impl<false>(xv, d, n, sm);
+}
+
+// 1 / sqrt(ss / d + 1e-6) with IEEE operations, as infer.m:371.  HIP's
+// float `/` and sqrtf are correctly rounded (clang's default
+// -fhip-fp32-correctly-rounded-divide-sqrt); __fsqrt_rn is not (it is the
+// hardware square root, off by an ulp for a few percent of inputs).
+__device__ __forceinline__ float rms_inv(float ss, int d) {
+#pragma clang fp contract(off)
+  return 1.0f / sqrtf(ss / (float)d + 1e-6f);
+}
+
+}  // namespace fdm

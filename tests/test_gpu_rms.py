@@ -1,0 +1,98 @@
+"""rms_norm on the device (fdm_rms_norm), bit for bit against the oracle's
+sequential loop (infer.m:369-374: one fused multiply-add per element in
+index order, which tests/test_oracle_rms.py pins against exact rational
+arithmetic).  The device evaluates that chain in parallel: integer runs
+inside a binade, and only the steps near binade edges and the ties walked
+in order.  The inputs are chosen to exercise every branch of that scheme:
+many Gaussian tokens at scales from 2^-40 to 2^40 (binade crossings at
+every position), small integers and powers of two (exact ties under
+round-half-even), a few large outliers, leading zeros, a tiny first element,
+sums that stay below 2^-100 (the plain-chain fallback), non-finite values,
+and widths other than 7168."""
+import zlib
+
+import numpy as np
+import pytest
+
+from tests._helpers import bits_equal_nan_class, empty_f32, say, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+
+def tokens(kind, T, d, rng):
+    x = np.empty((T, d), np.float32)
+    for t in range(T):
+        if kind == "normal":
+            v = rng.standard_normal(d)
+        elif kind == "scaled":
+            v = rng.standard_normal(d) * np.ldexp(1.0, int(rng.integers(-40, 41)))
+        elif kind == "integers":
+            v = np.trunc(rng.uniform(-64, 64, d))
+        elif kind == "small_ints":
+            v = rng.integers(1, 4, d).astype(np.float64)
+        elif kind == "powers_of_two":
+            v = np.ldexp(1.0, rng.integers(-10, 10, d))
+        elif kind == "outliers":
+            v = np.where(rng.integers(0, 16, d) == 0, rng.standard_normal(d) * 1e3, rng.standard_normal(d) * 1e-3)
+        elif kind == "leading_zeros":
+            v = rng.standard_normal(d)
+            v[: int(rng.integers(1, min(d, 500)))] = 0.0
+        elif kind == "tiny_first":
+            v = rng.standard_normal(d)
+            v[0] = 1e-30
+        elif kind == "tiny":
+            v = rng.standard_normal(d) * 1e-20
+        else:
+            raise ValueError(kind)
+        x[t] = v.astype(np.float32)
+    return x
+
+
+def run(fdm, x, w, inplace=False):
+    T, d = x.shape
+    xd = to_dev(x.ravel())
+    o = xd if inplace else empty_f32(T * d)
+    fdm.rms_norm(xd, None if w is None else to_dev(w), o, T, d)
+    return to_host(o).reshape(T, d)
+
+
+KINDS = [("normal", 64), ("scaled", 512), ("integers", 64), ("small_ints", 32), ("powers_of_two", 32),
+         ("outliers", 64), ("leading_zeros", 32), ("tiny_first", 16), ("tiny", 8)]
+
+
+@pytest.mark.parametrize("kind,T", KINDS, ids=[k for k, _ in KINDS])
+def test_rms_norm_bit_exact(fdm, oracle, kind, T):
+    rng = np.random.default_rng(zlib.crc32(kind.encode()))
+    d = 7168
+    x = tokens(kind, T, d, rng)
+    w = rng.normal(1.0, 0.1, d).astype(np.float32)
+    say(f"rms_norm kind={kind} T={T} d={d}")
+    got = run(fdm, x, w)
+    for t in range(T):
+        want = oracle.rms_norm(x[t], w)
+        assert bits_equal_nan_class(got[t], want), (kind, t)
+
+
+@pytest.mark.parametrize("d", [1, 3, 300, 512, 1000, 1536, 7167])
+def test_rms_norm_widths(fdm, oracle, d):
+    rng = np.random.default_rng(d)
+    x = tokens("scaled", 16, d, rng)
+    say(f"rms_norm widths d={d}")
+    got = run(fdm, x, None)
+    for t in range(16):
+        assert bits_equal_nan_class(got[t], oracle.rms_norm(x[t])), (d, t)
+
+
+def test_rms_norm_non_finite_and_in_place(fdm, oracle):
+    rng = np.random.default_rng(7)
+    x = tokens("normal", 6, 7168, rng)
+    x[0, 100] = np.inf
+    x[1, 7000] = np.nan
+    x[2, 7167] = -np.inf
+    x[3, 0] = np.nan
+    x[4] = 0.0
+    w = rng.normal(1.0, 0.1, 7168).astype(np.float32)
+    say("rms_norm non-finite, in place")
+    got = run(fdm, x, w, inplace=True)
+    for t in range(6):
+        assert bits_equal_nan_class(got[t], oracle.rms_norm(x[t], w)), t
