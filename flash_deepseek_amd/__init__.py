@@ -191,6 +191,14 @@ def moe_layer(L, h_post, h_in, K, hidden, idx=None, w=None, stream=None):
          _stream(stream))
 
 
+def moe_layer_norm(L, h, norm_w, K, hidden, h_post=None, idx=None, w=None, stream=None):
+    """The MoE branch with its rms_norm fused in: hidden = h + routed(h_post)
+    + shared(h_post), h_post = rms_norm(h, norm_w) (written to h_post if
+    given).  hidden may be h itself."""
+    call("fdm_moe_layer_norm", L, _p(h), _p(norm_w), K, _p(hidden), _p(h_post), _p(idx), _p(w),
+         _stream(stream))
+
+
 def moe_forward_batched(L, X, H_in, T, K, hidden, idx=None, w=None, n_distinct=None,
                         stream=None):
     """T tokens through the MoE branch of layer L in one step, each selected

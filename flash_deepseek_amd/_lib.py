@@ -95,6 +95,7 @@ SIGNATURES = {
     "fdm_moe_forward": [_i, _vp, _vp, _vp, _i, _vp, _vp],
     "fdm_moe_forward_host": [_i, _vp, _vp, _vp, _i, _vp],
     "fdm_moe_layer": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
+    "fdm_moe_layer_norm": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp],
     "fdm_moe_forward_batched": [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp],
     "fdm_moe_forward_batched_noalloc": [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp],
     "fdm_rms_norm": [_vp, _vp, _vp, _i, _i, _vp],

@@ -1162,20 +1162,29 @@ int fdm_moe_forward_host(int L, const float* h_post, const int* exp_idx, const f
   return FDM_OK;
 }
 
-int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, float* d_hidden,
-                  int* d_idx, float* d_w, void* stream) {
+}  // extern "C"
+
+namespace fdm {
+namespace {
+// One launch of the batch-1 layer kernel.  h: h_post, or with norm_w the
+// hidden state whose rms_norm the kernel computes.
+int run_layer(int L, const float* h, const float* norm_w, float* h_post_out, const float* h_in, int K,
+              float* hidden, int* idx, float* w, void* stream) {
   Layer* y = nullptr;
   if (int rc = get_layer(L, &y)) return rc;
   if (int rc = check_K(K)) return rc;
-  if (!d_h_post || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
-  if (!aligned(d_h_post, 16)) return fail(FDM_E_INVAL, "h_post must be 16-byte aligned");
+  if (!h || !hidden) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(h, 16)) return fail(FDM_E_INVAL, "h / h_post must be 16-byte aligned");
+  if (norm_w && !aligned(norm_w, 16)) return fail(FDM_E_INVAL, "norm_w must be 16-byte aligned");
   hipStream_t s = as_stream(stream);
   LayerArgs a;
   a.Wg = y->Wg;
   a.bias = y->bias;
-  a.h = d_h_post;
-  a.h_in = d_h_in;
-  a.out = d_hidden;
+  a.h = h;
+  a.norm_w = norm_w;
+  a.h_post_out = h_post_out;
+  a.h_in = h_in;
+  a.out = hidden;
   a.moe_out = nullptr;
   a.experts = y->experts;
   a.expert_size = y->expert_size;
@@ -1184,8 +1193,8 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   a.down_q6 = y->down_q6 ? 1 : 0;
   a.K = K;
   a.n_slots = K + (y->shared ? 1 : 0);
-  a.idx = d_idx ? d_idx : g.ws.idx;
-  a.w = d_w ? d_w : g.ws.w;
+  a.idx = idx ? idx : g.ws.idx;
+  a.w = w ? w : g.ws.w;
   a.xd = g.ws.xd;
   uint64_t* tg = g.ws.layer_tagged;
   a.scores = tg;
@@ -1194,6 +1203,7 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
   a.route_perm = tg + 256 + 32;
   a.act = tg + 256 + 48;
   a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
+  a.norm_inv = tg + kLayerTagged - 16;  // its own 128-byte line
   a.counters = g.ws.layer_cnt;
   a.flags = g.ws.layer_flags;
   a.epoch = g.ws.epochs.next();
@@ -1203,6 +1213,21 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
     FDM_HIP(launch_layer(a, s));
   }
   return FDM_OK;
+}
+}  // namespace
+}  // namespace fdm
+
+extern "C" {
+
+int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, float* d_hidden,
+                  int* d_idx, float* d_w, void* stream) {
+  return run_layer(L, d_h_post, nullptr, nullptr, d_h_in, K, d_hidden, d_idx, d_w, stream);
+}
+
+int fdm_moe_layer_norm(int L, const float* d_h, const float* d_norm_w, int K, float* d_hidden,
+                       float* d_h_post, int* d_idx, float* d_w, void* stream) {
+  if (!d_norm_w) return fail(FDM_E_INVAL, "null norm weight");
+  return run_layer(L, d_h, d_norm_w, d_h_post, d_h, K, d_hidden, d_idx, d_w, stream);
 }
 
 // ---- batched decode ---------------------------------------------------------------------

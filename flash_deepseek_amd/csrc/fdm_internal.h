@@ -79,11 +79,14 @@ constexpr int kLayerMaxParts = 8;               // down matrices split in <= 8 c
 // tagged words: scores 256, prov 16, route_w 16, route_perm 16,
 // act 17 x 2048, eo 17 x 8 x 7168 (per-part down outputs)
 constexpr size_t kLayerTagged =
-    256 + 3 * 16 + (size_t)kLayerMaxSlots * (2048 + (size_t)kLayerMaxParts * 7168);
+    256 + 3 * 16 + (size_t)kLayerMaxSlots * (2048 + (size_t)kLayerMaxParts * 7168) + 16;  // + the rms line
 struct LayerArgs {
   const float* Wg;         // router weights [256][7168] fp32
   const float* bias;       // [256] or null
-  const float* h;          // h_post [7168]
+  const float* h;          // h_post [7168]; with norm_w: the hidden state h_post is the rms_norm of
+  const float* norm_w = nullptr;  // or the rms_norm weight [7168]: h_post = rms_norm(h, norm_w) inside
+  float* h_post_out = nullptr;    // or receives h_post [7168] (with norm_w)
+  uint64_t* norm_inv = nullptr;   // tagged: 1 / sqrt(mean h^2 + eps) of the fused rms_norm
   const float* h_in;       // residual [7168] or null
   float* out;              // hidden = h_in + moe + shared [7168]
   float* moe_out;          // sum_k w_k E_k [7168] or null

@@ -11,6 +11,7 @@
 // drain, and no weight of a later step is fetched before the earlier step
 // has ended.  Here each workgroup is one item of an ordered work list:
 //
+//   with a norm weight: the fused rms_norm of the hidden state (1)
 //   digits of h_post (28: four 64-element groups each)
 //   router row e (256)
 //   route: the expert set (1);  the exact route() (1)
@@ -25,9 +26,9 @@
 // for the slot's last activation.  The combine sums a slot's parts in part
 // order.  (Measured on MI355X: 2 parts beat 1, 4 and 8; finer parts read
 // 144-byte row slices that share 64-byte sectors with the neighbour part.)
-// (The shared expert's gate/up items wait for the digits before they load,
-// so their weights do not compete with the router rows, which are on the
-// route's critical path.)
+// (The shared expert's gate/up items request their weights before they
+// wait for the digits: they fill the front of the launch while the router
+// rows, the route and -- with the fused rms_norm -- the norm are in flight.)
 //
 // Items only wait for items earlier in the list, and a waiting item has
 // already issued every weight load it can (down tiles load their weights
@@ -49,6 +50,7 @@
 // h_post is published untagged, behind a flag set by the last of its 28
 // producers, and staged with 16-byte coherent loads.
 #include "fdm_internal.h"
+#include "rms_device.h"
 #include "route_device.h"
 
 namespace fdm {
@@ -124,8 +126,10 @@ struct LayerSmem {
   union {
     XGroup xs[kHidden / 64];  // digits of h_post (gate/up) or of a part's activations (down)
     float part[kLayerMaxSlots][kParts][kCombRows];  // combine: per-part down outputs
+    RmsSmem rms;              // the fused rms_norm (router rows and digit items)
   };
   float red[4];
+  float inv;                  // the fused rms_norm's 1 / rms
   float cw[kLayerMaxSlots];   // combine: route() weights in slot order
   int cperm[kLayerMaxSlots];  // combine: the expert-set slot of each
   int eid;                  // expert of the item's slot
@@ -190,15 +194,69 @@ __device__ __forceinline__ void digits_to_lds(float v, XGroup& g) {
   }
 }
 
+// ---- the fused rms_norm --------------------------------------------------------------
+// The first item of the list computes 1 / sqrt(sum h^2 / 7168 + 1e-6) of the
+// hidden state, bit-exact with infer.m:369-374 (rms_sumsq_exact), and
+// publishes it as one tagged word; the router rows and digit items wait for
+// it (router rows after their weight loads are issued) and form
+// h_post = (h * inv) * w element by element as infer.m:372.  Whole
+// workgroup; h is 16-byte aligned.
+__device__ __forceinline__ float layer_inv(const LayerArgs& a, LayerSmem& sm) {
+  const f32x4* h4 = reinterpret_cast<const f32x4*>(a.h) + threadIdx.x * (kRmsMaxPer / 4);
+  float xv[kRmsMaxPer];
+#pragma unroll
+  for (int k = 0; k < kRmsMaxPer / 4; ++k) {
+    const f32x4 v = h4[k];  // the thread's 28 consecutive elements
+    xv[4 * k] = v.x;
+    xv[4 * k + 1] = v.y;
+    xv[4 * k + 2] = v.z;
+    xv[4 * k + 3] = v.w;
+  }
+  const float inv = rms_inv(rms_sumsq_exact(xv, kHidden, sm.rms), kHidden);
+  __syncthreads();  // sm.rms is reused by the caller's next stage
+  return inv;
+}
+
+// h_post_out is written before inv is published: every read of h happens
+// before any item can depend on the publication (the output may alias h).
+__device__ __forceinline__ void norm_item(const LayerArgs& a, LayerSmem& sm) {
+#pragma clang fp contract(off)
+  __builtin_amdgcn_s_setprio(3);  // first on the critical path: issue ahead of the CU's streaming waves
+  const float inv = layer_inv(a, sm);
+  if (a.h_post_out) {
+    for (int i = threadIdx.x; i < kHidden; i += 256) a.h_post_out[i] = (a.h[i] * inv) * a.norm_w[i];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) put_tagged(a.norm_inv, a.epoch, __float_as_uint(inv));
+}
+
+// The published 1 / rms, in every thread.
+__device__ __forceinline__ float wait_inv(const LayerArgs& a, LayerSmem& sm) {
+  poll_all(a, [&] {
+    if (threadIdx.x != 0) return true;
+    const uint64_t v = get_tagged(a.norm_inv);
+    sm.inv = tagged_f(v);
+    return tag_is(v, a.epoch);
+  });
+  return sm.inv;
+}
+
 // ---- digits of h_post: groups 4i .. 4i+3, one per wave ------------------------------
 // Published untagged (16 KB read by every gate/up tile): agent-scope stores,
-// then the last of the 28 items sets the digit flag.
-__device__ __forceinline__ void xd_item(const LayerArgs& a, int i) {
+// then the last of the 28 items sets the digit flag.  With the fused norm,
+// h_post = (h * inv) * w as infer.m:372 (and optionally written out).
+__device__ __forceinline__ void xd_item(const LayerArgs& a, int i, LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int G = 4 * i + wave;
+  float v = a.h[64 * G + lane];
+  if (a.norm_w) {
+#pragma clang fp contract(off)
+    const float w = a.norm_w[64 * G + lane];
+    v = (v * wait_inv(a, sm)) * w;
+  }
   int8_t da, db, dc;
   float ds, dsum;
-  make_digits3(a.h[64 * G + lane], da, db, dc, ds, dsum);
+  make_digits3(v, da, db, dc, ds, dsum);
   const int l = lane & 31, sub = lane >> 5;
   auto pack4 = [](int8_t d) {
     const unsigned u = (uint8_t)d;
@@ -242,6 +300,22 @@ __device__ __forceinline__ void router_row(const LayerArgs& a, int e, LayerSmem&
   for (int i = 0; i < kHidden / 1024; ++i) {
     wv[i] = *reinterpret_cast<const u32x4*>(w4 + t + 256 * i);
     xv[i] = x4[t + 256 * i];
+  }
+  if (a.norm_w) {
+    // h_post = (h * inv) * w, element by element as infer.m:372; the norm
+    // weights are requested before the wait as well
+    const float4* n4 = reinterpret_cast<const float4*>(a.norm_w);
+    float4 nw[kHidden / 1024];
+#pragma unroll
+    for (int i = 0; i < kHidden / 1024; ++i) nw[i] = n4[t + 256 * i];
+    const float inv = wait_inv(a, sm);
+#pragma unroll
+    for (int i = 0; i < kHidden / 1024; ++i) {
+      xv[i].x = (xv[i].x * inv) * nw[i].x;
+      xv[i].y = (xv[i].y * inv) * nw[i].y;
+      xv[i].z = (xv[i].z * inv) * nw[i].z;
+      xv[i].w = (xv[i].w * inv) * nw[i].w;
+    }
   }
   float acc = 0.0f;
 #pragma unroll
@@ -337,7 +411,9 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
                                            LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
-  wait_route_xd(a, slot, routed, true, sm);
+  // a routed slot waits for its expert before loading; the shared expert's
+  // weights are requested first and the digits waited for after
+  if (routed) wait_route_xd(a, slot, true, true, sm);
   const uint8_t* blob = routed ? expert_blob(a, sm.eid) : a.shared;
   const Q4KScaleSel sel = q4k_scale_sel(g);
   for (int t = 0; t < kGuPer; ++t) {
@@ -350,6 +426,7 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
       for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     }
     if (t == 0) {
+      if (!routed) wait_route_xd(a, slot, false, true, sm);
       // the digit record: 16-byte loads with the coherent (sc1) cache policy
       const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
           (void*)a.xd, 0, (int)sizeof(XGroup) * (kHidden / 64), 0x00020000);
@@ -531,7 +608,8 @@ __device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile, Layer
 }
 
 // First workgroup of each section of the work list:
-//   digits | router rows | route set | exact route
+//   (with a norm weight: the fused rms_norm) | digits | router rows
+//   | route set | exact route
 //   | shared expert: gate/up of parts 0..P-1, then down of parts 0..P-1
 //   | routed experts, part-major: step q holds gate/up of part q of every
 //     slot (q < P), then down of part q - lag of every slot (q >= lag)
@@ -541,13 +619,13 @@ struct LayerList {
   int gup, dnp;  // gate/up and down items per (slot, part)
 };
 
-__host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6) {
+__host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6, bool norm) {
   const int hs = n_slots - K;  // 1 with a shared expert
   LayerList l;
   l.gup = kGuPerPart;
   l.dnp = dn_per_part(q6);
-  l.xd = 0;
-  l.router = kXdItems;
+  l.xd = norm ? 1 : 0;  // item 0: the fused rms_norm
+  l.router = l.xd + kXdItems;
   l.route = l.router + kRows;
   l.exact = l.route + 1;
   l.shared = l.exact + 1;
@@ -592,10 +670,12 @@ __device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, 
 
 template <bool Q6>
 __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
-  const LayerList l = layer_list(a.K, a.n_slots, Q6);
+  const LayerList l = layer_list(a.K, a.n_slots, Q6, a.norm_w != nullptr);
   const int it = blockIdx.x;
-  if (it < l.router) {
-    xd_item(a, it - l.xd);
+  if (it < l.xd) {
+    norm_item(a, sm);
+  } else if (it < l.router) {
+    xd_item(a, it - l.xd, sm);
   } else if (it < l.route) {
     router_row(a, it - l.router, sm);
   } else if (it == l.route) {
@@ -635,7 +715,7 @@ __global__ __launch_bounds__(256) void k_layer_q6k(LayerArgs a) {
 }
 
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s) {
-  const LayerList l = layer_list(a.K, a.n_slots, a.down_q6 != 0);
+  const LayerList l = layer_list(a.K, a.n_slots, a.down_q6 != 0, a.norm_w != nullptr);
   if (a.down_q6)
     hipLaunchKernelGGL(k_layer_q6k, dim3(l.total), dim3(256), 0, s, a);
   else

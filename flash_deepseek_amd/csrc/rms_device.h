@@ -100,6 +100,35 @@ __device__ __forceinline__ T rms_block_excl(T v, T* wsum, T& tot) {
   return base + (inc - v);
 }
 
+// Two exclusive prefixes at once (one pair of barriers).
+__device__ __forceinline__ void rms_block_excl2(unsigned v, int c, unsigned* wv, int* wc, unsigned& ex_v, int& ex_c,
+                                                unsigned& tot_v, int& tot_c) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const unsigned iv = wave_scan_incl(v);
+  const int ic = wave_scan_incl(c);
+  if (lane == 63) {
+    wv[wave] = iv;
+    wc[wave] = ic;
+  }
+  __syncthreads();
+  unsigned bv = 0, av = 0;
+  int bc = 0, ac = 0;
+#pragma unroll
+  for (int w = 0; w < kRmsThreads / 64; ++w) {
+    const unsigned sv = wv[w];
+    const int sc = wc[w];
+    bv = w < wave ? bv + sv : bv;
+    bc = w < wave ? bc + sc : bc;
+    av += sv;
+    ac += sc;
+  }
+  tot_v = av;
+  tot_c = ac;
+  ex_v = bv + (iv - v);
+  ex_c = bc + (ic - c);
+  __syncthreads();
+}
+
 // The sum of squares below for one thread layout: FULL when every thread
 // holds kRmsMaxPer elements (d = 7168: straight-line code), else the first
 // n slots of xv are the thread's (a uniform test per slot).
@@ -141,8 +170,9 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
   }
   unsigned ktot;
   int rtot;
-  const unsigned kbase = rms_block_excl(ksum, sm.wk, ktot);
-  const int rbase = rms_block_excl(nrisky, sm.wr, rtot);
+  unsigned kbase;
+  int rbase;
+  rms_block_excl2(ksum, nrisky, sm.wk, sm.wr, kbase, rbase, ktot, rtot);
   if (rtot > kRmsMaxRisky) {
     // too many risky steps for the list: the plain chain by one lane, over
     // the inputs gathered in LDS (in place of the K values)
@@ -164,7 +194,7 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
   int r = rbase;
 #pragma unroll
   for (int j = 0; j < kRmsMaxPer; ++j) {
-    if (mine(j)) {
+    if (nrisky > 0 && mine(j)) {
       const unsigned k = sm.k[i0 + j];
       if (k == kRmsRisky) {
         int E;

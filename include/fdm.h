@@ -240,6 +240,17 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
 int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, float *d_hidden,
                   int *d_idx, float *d_w, void *stream);
 
+/* ---- the same MoE branch with its rms_norm fused in (infer.m:1846-1850
+ * and 1878-1922: h_in = hidden; h_post = rms_norm(hidden, ffn_norm_w);
+ * hidden = h_in + moe + shared), in the same single launch:
+ *   d_hidden = d_h + sum_k w[k] E_k(h_post) + S(h_post),
+ *   h_post = rms_norm(d_h, d_norm_w), bit-exact with infer.m:369-374.
+ * d_h, d_norm_w: [7168] fp32, 16-byte aligned; d_hidden may alias d_h;
+ * d_h_post (optional) receives h_post.  Routing, results and the rules for
+ * overlapping calls are fdm_moe_layer's on that h_post. */
+int fdm_moe_layer_norm(int L, const float *d_h, const float *d_norm_w, int K, float *d_hidden,
+                       float *d_h_post, int *d_idx, float *d_w, void *stream);
+
 /* ---- the polls one wait inside fdm_moe_layer's kernel makes before it gives
  * up (no counterpart in the reference, whose Metal waits are host-side,
  * infer.m:1681).  0 restores the default (2^17 polls of >= ~1 us each).  A

@@ -164,3 +164,39 @@ def test_errors(fdm, layer):
         fdm.moe_layer(L, h, None, 17, empty_f32(7168))
     with pytest.raises(fdm.FdmError):
         fdm.moe_layer(60, h, None, 8, empty_f32(7168))  # not resident
+
+
+@pytest.mark.parametrize("scale,tok", [(1.0, 20), (37.0, 21), (1e-3, 22)])
+def test_moe_layer_norm_fused(fdm, oracle, layer, scale, tok):
+    """fdm_moe_layer_norm (rms_norm inside the layer launch) against
+    fdm_rms_norm followed by fdm_moe_layer on the same hidden state: the
+    same h_post bits (and the oracle's rms_norm), the same routing and the
+    same output bits; then once more in place (hidden = h)."""
+    import torch
+    L, lay = layer
+    K = 8
+    h = (oracle.synth_normal(7168, 0.0, 1.0, 700 + tok) * scale).astype(np.float32)
+    nw = oracle.synth_normal(7168, 1.0, 0.1, 800 + tok)
+    hd, nwd = to_dev(h), to_dev(nw)
+    hid, hp = empty_f32(7168), empty_f32(7168)
+    idx = torch.empty(K, dtype=torch.int32, device="cuda")
+    w = empty_f32(K)
+    say(f"moe_layer_norm L={L} tok={tok} scale={scale}")
+    fdm.moe_layer_norm(L, hd, nwd, K, hid, hp, idx, w)
+    hp_ref, hid_ref = empty_f32(7168), empty_f32(7168)
+    idx_ref = torch.empty(K, dtype=torch.int32, device="cuda")
+    w_ref = empty_f32(K)
+    say(f"rms_norm + moe_layer L={L} tok={tok}")
+    fdm.rms_norm(hd, nwd, hp_ref, 1)
+    fdm.moe_layer(L, hp_ref, hd, K, hid_ref, idx_ref, w_ref)
+    assert np.array_equal(to_host(hp).view(np.uint32), oracle.rms_norm(h, nw).view(np.uint32))
+    assert np.array_equal(to_host(hp).view(np.uint32), to_host(hp_ref).view(np.uint32))
+    assert np.array_equal(to_host(idx), to_host(idx_ref))
+    assert np.array_equal(to_host(w).view(np.uint32), to_host(w_ref).view(np.uint32))
+    assert np.array_equal(to_host(hid).view(np.uint32), to_host(hid_ref).view(np.uint32))
+    ri, _ = oracle.route(oracle.router_logits(to_host(lay.Wg), oracle.rms_norm(h, nw)), to_host(lay.bias), K=K)
+    assert np.array_equal(to_host(idx), ri)
+    say(f"moe_layer_norm in place L={L} tok={tok}")
+    hio = hd.clone()
+    fdm.moe_layer_norm(L, hio, nwd, K, hio)
+    assert np.array_equal(to_host(hio).view(np.uint32), to_host(hid_ref).view(np.uint32))
