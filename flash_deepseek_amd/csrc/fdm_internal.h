@@ -161,7 +161,7 @@ struct QGemmArgs {
   const float* xs;         // [rows][kd / 32] sub-block sums of the planes
   const float* xe;         // [rows] 2^-s of each input row
   const int* pair_tok;     // token of each pair position (gate/up input rows)
-  const int4* chunks;      // {expert or -1, first pair / token, count, 0}
+  const int4* chunks;      // {expert or -1, first pair / token, count, first chunk | count << 16}
   const int* n_chunks;
   float* out;              // gate/up: act [rows][2048] (SwiGLU); down: eo [rows][7168]
 };

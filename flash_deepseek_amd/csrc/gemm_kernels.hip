@@ -213,20 +213,23 @@ __global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, in
 // ---- the chunk list -------------------------------------------------------------------
 // One thread: every distinct routed expert's pair segment in chunks of `ch`
 // pairs, then the shared expert's tokens in chunks of `ch`.  Entry:
-// {expert (-1: shared), first pair position (or token), count, 0}.
+// {expert (-1: shared), first pair position (or token), count, group}, where
+// group = first chunk of the expert | (the expert's chunk count << 16).
 __global__ void k_qchunks(const int* __restrict__ seg_start, const int* __restrict__ distinct,
                           const int* __restrict__ n_distinct, int T, int with_shared, int ch,
                           int4* __restrict__ chunks, int* __restrict__ n_chunks) {
   if (threadIdx.x != 0) return;
   int n = 0;
+  auto group = [&](int e, int a, int b) {
+    const int first = n, cnt = (b - a + ch - 1) / ch;
+    for (int f = a; f < b; f += ch) chunks[n++] = make_int4(e, f, min(ch, b - f), first | (cnt << 16));
+  };
   const int D = *n_distinct;
   for (int d = 0; d < D; ++d) {
     const int e = distinct[d];
-    const int a = seg_start[e], b = seg_start[e + 1];
-    for (int f = a; f < b; f += ch) chunks[n++] = make_int4(e, f, min(ch, b - f), 0);
+    group(e, seg_start[e], seg_start[e + 1]);
   }
-  if (with_shared)
-    for (int f = 0; f < T; f += ch) chunks[n++] = make_int4(-1, f, min(ch, T - f), 0);
+  if (with_shared) group(-1, 0, T);
   *n_chunks = n;
 }
 
@@ -398,17 +401,26 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 }
 
 // NB: the largest token block count of a chunk; a chunk of <= 16 tokens
-// runs the one-block body.  One-dimensional grid, mapped so that every row
-// group of a chunk runs on the same XCD: workgroups are handed to the eight
-// XCDs in turn (id % 8), so id -> (xcd = id % 8, k = id / 8) and chunk
-// 8 (k / RG) + xcd, row group k % RG.  The chunk's token planes are then
-// read from HBM into one L2 and served from there to all its row groups.
+// runs the one-block body.  One-dimensional grid, mapped so that all the
+// chunks of one expert that share a row group run on the same XCD, back to
+// back: workgroups are handed to the eight XCDs in turn (id % 8), so
+// id -> (xcd = id % 8, k = id / 8); XCD x owns row groups x, x + 8, ...
+// (RG / 8 of them) of every chunk, and its k-th item is, within the item
+// range q f .. q (f + c) - 1 of the expert whose chunks are f .. f + c - 1
+// (q = RG / 8), row group 8 ((k - q f) / c) + x of chunk f + (k - q f) % c.
+// An expert's weights are then read from HBM once per row group and served
+// from that XCD's L2 to its other chunks; every XCD does the same work.
 template <int P, int NB, bool DOWN>
 __global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(QGemmArgs g) {
   constexpr int RG = DOWN ? kHidden / kQDnRows : kFfn / kQGuRows;
+  constexpr int Q = RG / 8;
+  static_assert(Q * 8 == RG, "row groups split evenly over the XCDs");
   const int id = blockIdx.x, xcd = id & 7, k = id >> 3;
-  const int chunk = (k / RG) * 8 + xcd, rg = k % RG;
-  if (chunk >= *g.n_chunks) return;
+  const int m = k / Q;  // a chunk of the item's expert
+  if (m >= *g.n_chunks) return;
+  const int grp = g.chunks[m].w, f = grp & 0xFFFF, c = grp >> 16;
+  const int off = k - Q * f;
+  const int chunk = f + off % c, rg = 8 * (off / c) + xcd;
   constexpr int NT = 16 * NB;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * P * NT * kQRowB];
   __shared__ int rows[2 * NT];
@@ -439,7 +451,7 @@ int qgemm_chunk_tokens(int planes) { return planes == 3 ? 16 : 32; }
 hipError_t launch_qgemm(const QGemmArgs& g, int planes, bool down, int max_chunks, hipStream_t s) {
   const dim3 blk(kQWaves * 64);
   const int RG = down ? kHidden / kQDnRows : kFfn / kQGuRows;
-  const dim3 grid((unsigned)(RG * 8 * ((max_chunks + 7) / 8)));
+  const dim3 grid((unsigned)(RG * max_chunks));
   if (planes == 3) {
     if (down)
       hipLaunchKernelGGL((k_qgemm<3, 1, true>), grid, blk, 0, s, g);
