@@ -220,6 +220,38 @@ def bench_layer_q6k(F, torch, args, stream, K, n_layers=6, steps=200):
     return r
 
 
+def bench_norm(F, torch, args, stream, K, steps=200):
+    """rms_norm on the device (fdm_rms_norm: one token of 7168, and 512
+    tokens), and the batch-1 layer with the rms_norm fused into its launch
+    (fdm_moe_layer_norm) over the same rotated layers as the headline, each
+    timed per call with HIP events."""
+    from flash_deepseek_amd.synthetic import make_tokens
+    out = {}
+    w = make_tokens(1, 7301)[0]
+    for T in (1, 512):
+        x = make_tokens(T, 7302 + T)
+        o = torch.empty_like(x)
+        for _ in range(10):
+            F.rms_norm(x, w, o, T, stream=stream)
+        us = event_times(torch, lambda i: F.rms_norm(x, w, o, T, stream=stream), steps)
+        r = percentiles(us)
+        r["bytes"] = 2 * T * HIDDEN * 4 + HIDDEN * 4
+        out[f"rms_norm_t{T}"] = r
+    h = make_tokens(steps + 20, 7303)
+    hid = torch.empty((steps + 20, HIDDEN), dtype=torch.float32, device="cuda")
+    run = lambda i: F.moe_layer_norm(3 + i % args.layers, h[i], w, K, hid[i], stream=stream)
+    for i in range(20):
+        run(i)
+    us = event_times(torch, lambda i: run(20 + i), steps)
+    F.sync(stream)
+    r = {"workload": "the batch-1 layer with its rms_norm fused in (hidden state in, rms_norm + "
+                     "router + route + 8 routed and 1 shared expert + combine + residual)",
+         "layers_rotated": args.layers, "steps": steps}
+    r.update(percentiles(us))
+    out["layer_with_rms_norm"] = r
+    return out
+
+
 def bench_batched(F, torch, layers, args, stream, K, steps=20, warmup=3):
     """Batched decode through the resident layers: per token count T, the
     mean over `steps` steps (new seeded tokens each, next layer each)."""
@@ -544,6 +576,7 @@ def main():
         result["expert_q4k_down"] = bench_expert(F, torch, "q4k")
         result["expert_q6k_down"] = bench_expert(F, torch, "q6k")
         result["layer_q6k_down"] = bench_layer_q6k(F, torch, args, stream, K)
+    result["norm"] = bench_norm(F, torch, args, stream, K)
     if args.batched:
         result["batched"] = bench_batched(F, torch, layers, args, stream, K)
     if args.prefill:

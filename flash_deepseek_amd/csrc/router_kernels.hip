@@ -57,6 +57,64 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
   }
 }
 
+// The same logits for a block of EPB experts x TPW tokens per workgroup:
+// each weight chunk and each token chunk is loaded once per block and used
+// EPB (TPW) times, so the L2 traffic of many tokens is (n_exp / EPB) token
+// reads + (T / TPW) weight reads instead of n_exp token reads.  Every
+// logit is still its own canonical chain: partial t over chunks t, t+256, ...
+// with one fma per element, butterfly, (s0 + s1) + (s2 + s3).
+template <int EPB, int TPW>
+__global__ __launch_bounds__(256) void k_router_logits_blk(const float* __restrict__ Wg,
+                                                           const float* __restrict__ x, int n_exp,
+                                                           int dim, int T,
+                                                           float* __restrict__ logits) {
+#pragma clang fp contract(off)
+  __shared__ float red[4][EPB][TPW];
+  const int e0 = blockIdx.x * EPB, t0 = blockIdx.y * TPW;
+  const int n4 = dim >> 2;
+  float acc[EPB][TPW];
+#pragma unroll
+  for (int k = 0; k < EPB; ++k)
+#pragma unroll
+    for (int q = 0; q < TPW; ++q) acc[k][q] = 0.0f;
+  for (int c = threadIdx.x; c < n4; c += 256) {
+    float4 xv[TPW];
+#pragma unroll
+    for (int q = 0; q < TPW; ++q)
+      xv[q] = reinterpret_cast<const float4*>(x + (size_t)min(t0 + q, T - 1) * dim)[c];
+#pragma unroll
+    for (int k = 0; k < EPB; ++k) {
+      const float4 w = reinterpret_cast<const float4*>(Wg + (size_t)(e0 + k) * dim)[c];
+#pragma unroll
+      for (int q = 0; q < TPW; ++q) {
+        float a = acc[k][q];
+        a = fmaf(w.x, xv[q].x, a);
+        a = fmaf(w.y, xv[q].y, a);
+        a = fmaf(w.z, xv[q].z, a);
+        a = fmaf(w.w, xv[q].w, a);
+        acc[k][q] = a;
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < EPB; ++k) {
+#pragma unroll
+    for (int q = 0; q < TPW; ++q) {
+      float v = acc[k][q];
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
+      if (lane == 0) red[wave][k][q] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < EPB * TPW) {
+    const int k = threadIdx.x / TPW, q = threadIdx.x % TPW;
+    if (t0 + q < T)
+      logits[(size_t)(t0 + q) * n_exp + e0 + k] = (red[0][k][q] + red[1][k][q]) + (red[2][k][q] + red[3][k][q]);
+  }
+}
+
 __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
                                                const float* __restrict__ bias, int T, int K,
                                                int* __restrict__ idx, float* __restrict__ w) {
@@ -70,6 +128,9 @@ hipError_t launch_router_logits(const float* Wg, const float* x, int n_exp, int 
   if (T <= 1) {
     hipLaunchKernelGGL(k_router_logits<1>, dim3(n_exp, T), dim3(256), 0, s, Wg, x, n_exp, dim,
                        T, logits);
+  } else if (T >= 16 && n_exp % 8 == 0) {
+    hipLaunchKernelGGL((k_router_logits_blk<8, 8>), dim3(n_exp / 8, (T + 7) / 8), dim3(256), 0, s, Wg, x,
+                       n_exp, dim, T, logits);
   } else {
     hipLaunchKernelGGL(k_router_logits<8>, dim3(n_exp, (T + 7) / 8), dim3(256), 0, s, Wg, x,
                        n_exp, dim, T, logits);

@@ -17,7 +17,7 @@ def route_dev(fdm, logits, bias, K, T):
     return to_host(idx).reshape(T, K), to_host(w).reshape(T, K)
 
 
-@pytest.mark.parametrize("T", [1, 5, 64])
+@pytest.mark.parametrize("T", [1, 5, 21, 64])
 def test_router_logits_bit_exact(fdm, oracle, T):
     say(f"router_logits T={T}")
     Wg = oracle.synth_normal(256 * 7168, 0.0, 0.01, 40).reshape(256, 7168)
