@@ -253,6 +253,43 @@ __device__ __forceinline__ float q4k_group_dot(const u32x4 hdr, const u32x4 q0, 
   return fmaf(d, qx, -dmin * mx);
 }
 
+// A workgroup's copy of n (<= MAXN) digit records from global memory into
+// LDS in one round trip: every 16-byte load of a thread is issued (load)
+// before any is stored (store).  Issue the loads ahead of a kernel's weight
+// loads: loads complete in order, so the stores then wait for the records
+// only, and each weight group is used as soon as it arrives.
+template <int MAXN>
+struct XStage {
+  static constexpr int kSteps = (MAXN * kXGroupVec + 255) / 256;
+  u32x4 v[kSteps];
+  __device__ __forceinline__ void load(const XGroup* __restrict__ src, int n) {
+    const u32x4* s = reinterpret_cast<const u32x4*>(src);
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n * kXGroupVec) v[k] = s[i];
+    }
+  }
+  __device__ __forceinline__ void store(XGroup* __restrict__ dst, int n) const {
+    u32x4* d = reinterpret_cast<u32x4*>(dst);
+#pragma unroll
+    for (int k = 0; k < kSteps; ++k) {
+      const int i = threadIdx.x + 256 * k;
+      if (i < n * kXGroupVec) d[i] = v[k];
+    }
+  }
+};
+
+// Any number of records, XStage<112> at a time (for lengths known only at
+// run time).
+__device__ __forceinline__ void xstage_copy(XGroup* __restrict__ dst, const XGroup* __restrict__ src, int n) {
+  for (int b = 0; b < n; b += 112) {
+    XStage<112> st;
+    st.load(src + b, min(112, n - b));
+    st.store(dst + b, min(112, n - b));
+  }
+}
+
 // Broadcast lane `src` of each group of four lanes to the whole quad (DPP
 // quad_perm [src,src,src,src]; no LDS traffic).
 template <int SRC>

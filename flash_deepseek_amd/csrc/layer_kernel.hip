@@ -411,9 +411,34 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
                                            LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
-  // a routed slot waits for its expert before loading; the shared expert's
-  // weights are requested first and the digits waited for after
-  if (routed) wait_route_xd(a, slot, true, true, sm);
+  // The digit record (23 KB, every gate/up item reads all of it): all of a
+  // thread's 16-byte loads are issued before any is written to LDS (loads
+  // past the record return 0 through the buffer's range check), with the
+  // coherent (sc1) cache policy.
+  constexpr int kXsVec = (int)sizeof(sm.xs) / 16;
+  constexpr int kXsPer = (kXsVec + 255) / 256;
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)a.xd, 0, (int)sizeof(XGroup) * (kHidden / 64), 0x00020000);
+  u32x4 xv[kXsPer];
+  auto load_xd = [&] {
+#pragma unroll
+    for (int k = 0; k < kXsPer; ++k)
+      xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, (threadIdx.x + 256 * k) * 16, 0, 16);
+  };
+  auto store_xd = [&] {
+#pragma unroll
+    for (int k = 0; k < kXsPer; ++k)
+      if (threadIdx.x + 256 * k < kXsVec) reinterpret_cast<u32x4*>(sm.xs)[threadIdx.x + 256 * k] = xv[k];
+    __syncthreads();
+  };
+  // A routed slot waits for its expert (and the digits), requests the digit
+  // record and then the weights, so the record lands first and each weight
+  // group is used as soon as it arrives.  The shared expert's weights are
+  // requested before the digits are waited for.
+  if (routed) {
+    wait_route_xd(a, slot, true, true, sm);
+    load_xd();
+  }
   const uint8_t* blob = routed ? expert_blob(a, sm.eid) : a.shared;
   const Q4KScaleSel sel = q4k_scale_sel(g);
   for (int t = 0; t < kGuPer; ++t) {
@@ -426,13 +451,11 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
       for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     }
     if (t == 0) {
-      if (!routed) wait_route_xd(a, slot, false, true, sm);
-      // the digit record: 16-byte loads with the coherent (sc1) cache policy
-      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-          (void*)a.xd, 0, (int)sizeof(XGroup) * (kHidden / 64), 0x00020000);
-      for (int i = threadIdx.x; i < (int)sizeof(sm.xs) / 16; i += 256)
-        reinterpret_cast<u32x4*>(sm.xs)[i] = __builtin_amdgcn_raw_buffer_load_b128(r, i * 16, 0, 16);
-      __syncthreads();
+      if (!routed) {
+        wait_route_xd(a, slot, false, true, sm);
+        load_xd();
+      }
+      store_xd();
     }
     float acc = 0.0f;
     if (blob) {

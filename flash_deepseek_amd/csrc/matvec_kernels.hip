@@ -35,13 +35,6 @@ __global__ __launch_bounds__(256) void k_xdigits(const float* __restrict__ x, si
   }
 }
 
-__device__ __forceinline__ void stage_xgroups(XGroup* __restrict__ dst,
-                                              const XGroup* __restrict__ src, int n) {
-  const u32x4* s = reinterpret_cast<const u32x4*>(src);
-  u32x4* d = reinterpret_cast<u32x4*>(dst);
-  for (int i = threadIdx.x; i < n * kXGroupVec; i += blockDim.x) d[i] = s[i];
-}
-
 // GPL = groups per lane (in_dim / 1024) when known at compile time, 0 for
 // any in_dim that is a multiple of 256.
 template <int GPL>
@@ -49,31 +42,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void k
                                                     const XGroup* __restrict__ xd,
                                                     float* __restrict__ y, int rows, int gr) {
   extern __shared__ XGroup xs[];
-  stage_xgroups(xs, xd, gr);
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 16 + wave * 4 + (lane >> 4);
   const int l16 = lane & 15, g = l16 & 3;
   const Q4KScaleSel sel = q4k_scale_sel(g);
   float acc = 0.0f;
-  if (row < rows) {
-    const uint8_t* rp = W + (size_t)row * (size_t)(gr >> 2) * kQ4KBlock;
-    if constexpr (GPL > 0) {
-      u32x4 hdr[GPL], q0[GPL], q1[GPL];
+  if constexpr (GPL > 0) {
+    // the digit records first, then the weights: the records land first
+    XStage<16 * GPL> st;
+    st.load(xd, gr);
+    u32x4 hdr[GPL], q0[GPL], q1[GPL];
+    const uint8_t* rp = W + (size_t)min(row, rows - 1) * (size_t)(gr >> 2) * kQ4KBlock;
 #pragma unroll
-      for (int t = 0; t < GPL; ++t) {
-        const uint8_t* bp = rp + (size_t)(4 * t + (l16 >> 2)) * kQ4KBlock;
-        hdr[t] = *reinterpret_cast<const u32x4_a4*>(bp);
-        q0[t] = *reinterpret_cast<const u32x4_a4*>(bp + 16 + 32 * g);
-        q1[t] = *reinterpret_cast<const u32x4_a4*>(bp + 32 + 32 * g);
-      }
+    for (int t = 0; t < GPL; ++t) {
+      const uint8_t* bp = rp + (size_t)(4 * t + (l16 >> 2)) * kQ4KBlock;
+      hdr[t] = *reinterpret_cast<const u32x4_a4*>(bp);
+      q0[t] = *reinterpret_cast<const u32x4_a4*>(bp + 16 + 32 * g);
+      q1[t] = *reinterpret_cast<const u32x4_a4*>(bp + 32 + 32 * g);
+    }
+    st.store(xs, gr);
+    __syncthreads();
+    if (row < rows) {
 #pragma unroll
       for (int t = 0; t < GPL; ++t) {
         acc += q4k_group_dot(hdr[t], q0[t], q1[t], sel, &xs[16 * t + l16]);
         // keep each group's LDS reads next to its math (bounds live registers)
         __builtin_amdgcn_sched_barrier(0);
       }
-    } else {
+    }
+  } else {
+    xstage_copy(xs, xd, gr);
+    __syncthreads();
+    if (row < rows) {
+      const uint8_t* rp = W + (size_t)row * (size_t)(gr >> 2) * kQ4KBlock;
       for (int G = l16; G < gr; G += 16) {
         const uint8_t* bp = rp + (size_t)(G >> 2) * kQ4KBlock;
         const u32x4 hdr = *reinterpret_cast<const u32x4_a4*>(bp);
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(256) void k_matvec_q6k(const uint8_t* __restrict__ 
                                                     const XGroup* __restrict__ xd,
                                                     float* __restrict__ y, int rows, int gr) {
   extern __shared__ XGroup xs[];
-  stage_xgroups(xs, xd, gr);
+  xstage_copy(xs, xd, gr);
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int row = blockIdx.x * 16 + wave * 4 + (lane >> 4);

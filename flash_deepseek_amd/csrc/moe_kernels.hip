@@ -31,13 +31,6 @@ __device__ __forceinline__ const uint8_t* slot_blob(const SlotTable& t, int slot
   return t.shared;
 }
 
-__device__ __forceinline__ void stage_groups(XGroup* __restrict__ dst,
-                                             const XGroup* __restrict__ src, int n) {
-  const u32x4* s = reinterpret_cast<const u32x4*>(src);
-  u32x4* d = reinterpret_cast<u32x4*>(dst);
-  for (int i = threadIdx.x; i < n * kXGroupVec; i += blockDim.x) d[i] = s[i];
-}
-
 constexpr int kGuRows = 8;                 // rows of gate (and up) per workgroup
 constexpr int kGuTiles = kFfn / kGuRows;   // 256 tiles per slot
 
@@ -52,6 +45,10 @@ __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __res
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
   const int row = tile * kGuRows + 2 * wave + (q & 1);
+  // the digit records first, then the weights: the records land first and
+  // each weight group is used as soon as it arrives
+  XStage<kHidden / 64> st;
+  st.load(xd, kHidden / 64);
   Q4KGroupLoad ld[7];
   if (blob) {
     const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
@@ -61,7 +58,7 @@ __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __res
       ld[i] = t.rel ? rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g)
                     : q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, g);
   }
-  stage_groups(xs, xd, kHidden / 64);
+  st.store(xs, kHidden / 64);
   __syncthreads();
   float acc = 0.0f;
   if (blob) {
@@ -121,6 +118,8 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
   const int l16 = lane & 15;
   const int row = tile * kDnRows + wave * 4 + (lane >> 4);
   float acc = 0.0f;
+  XStage<kFfn / 64> st;
+  st.load(act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
   if (!Q6) {
     Q4KGroupLoad ld[2];
     if (blob) {
@@ -131,7 +130,7 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
         ld[i] = t.rel ? rel_load_group<true>(mat, row, 4 * i + (l16 >> 2), l16 & 3)
                       : q4k_load_group(rowp + (4 * i + (l16 >> 2)) * kQ4KBlock, l16 & 3);
     }
-    stage_groups(xs, act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
+    st.store(xs, kFfn / 64);
     __syncthreads();
     if (blob) {
       const Q4KScaleSel sel = q4k_scale_sel(l16 & 3);
@@ -145,7 +144,7 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
       ld = q6k_load_half(blob + 2 * (size_t)kGateBytes + (size_t)row * kQ6KRowFfn +
                              (l16 >> 1) * kQ6KBlock,
                          l16 & 1);
-    stage_groups(xs, act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
+    st.store(xs, kFfn / 64);
     __syncthreads();
     if (blob) acc = q6k_half_dot_ld(ld, &xs[2 * l16]);
   }
