@@ -78,6 +78,13 @@ def sync(stream=None):
     call("fdm_stream_sync", _stream(stream))
 
 
+def stream_release(stream):
+    """Free the workspace the library holds for `stream` (made at the stream's
+    first call; each stream has its own, so host threads on their own streams
+    may call concurrently).  No effect on the null stream's."""
+    call("fdm_stream_release", _stream(stream))
+
+
 def set_layer_spin_limit(polls):
     """Polls one wait inside moe_layer's kernel makes before giving up (0:
     the default).  Returns the previous limit."""

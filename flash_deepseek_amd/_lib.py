@@ -64,6 +64,7 @@ SIGNATURES = {
     "fdm_memcpy_h2d": [_vp, _vp, _sz, _vp],
     "fdm_memcpy_d2h": [_vp, _vp, _sz, _vp],
     "fdm_stream_sync": [_vp],
+    "fdm_stream_release": [_vp],
     "fdm_fp16_to_fp32": [_vp, _vp, _sz, _vp],
     "fdm_f32_to_f16": [_vp, _vp, _sz, _vp],
     "fdm_dense_upload": [_i, _vp, _vp, _vp, _i],

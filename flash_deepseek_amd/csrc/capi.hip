@@ -9,9 +9,13 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <atomic>
 #include <initializer_list>
 #include <math.h>
 #include <memory>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "../../include/fdm.h"
 #include "epoch_book.h"
@@ -102,6 +106,18 @@ int bind_scratch(int device) {
   return FDM_OK;
 }
 
+// Per-token scratch of the attention (grown to the largest max_seq).
+struct AttnScratch {
+  float *normed = nullptr, *q_a = nullptr, *q_a_n = nullptr, *q = nullptr, *kv_a = nullptr, *c_kv_n = nullptr;
+  float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr;
+  int seq = 0;
+  void release() {
+    for (float* p : {normed, q_a, q_a_n, q, kv_a, c_kv_n, q_abs, scores, wc, attn, part})
+      if (p) (void)hipFree(p);
+    *this = AttnScratch();
+  }
+};
+
 struct Workspace {
   XGroup* xd = nullptr;       // digits of activations (up to FDM_MAX_TOKENS x 112)
   float* logits = nullptr;    // FDM_MAX_TOKENS x 256 (the layer path: sigmoid scores)
@@ -143,6 +159,9 @@ struct Workspace {
   int* stage_idx = nullptr;   //                   exp_idx
   float* stage_w = nullptr;   //                   exp_w
   float* dense_act = nullptr; // dense FFN activations [kDenseMaxFfn]
+  AttnScratch attn;           // MLA attention, grown to the largest max_seq used
+  int* ids_h = nullptr;       // pinned host: the routed ids of a streamed call
+  int* slots_h = nullptr;     //              their cache slots
 };
 
 struct Layer {
@@ -175,7 +194,12 @@ struct StreamedLayer {
   uint8_t* shared = nullptr;
   size_t expert_size = 0;
   bool q6 = false;
+  // Calls on several streams take turns: one call at a time fills the cache,
+  // after the kernels of the previous call (on whichever stream) have read it.
+  std::mutex mu;
+  hipEvent_t done = nullptr;  // recorded after each call's kernels
   ~StreamedLayer() {
+    if (done) (void)hipEventDestroy(done);
     if (shared) (void)hipFree(shared);
   }
 };
@@ -195,22 +219,11 @@ struct AttnLayer {
   }
 };
 
-// Per-token scratch of the attention (grown to the largest max_seq).
-struct AttnScratch {
-  float *normed = nullptr, *q_a = nullptr, *q_a_n = nullptr, *q = nullptr, *kv_a = nullptr, *c_kv_n = nullptr;
-  float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr;
-  int seq = 0;
-  void release() {
-    for (float* p : {normed, q_a, q_a_n, q, kv_a, c_kv_n, q_abs, scores, wc, attn, part})
-      if (p) (void)hipFree(p);
-    *this = AttnScratch();
-  }
-};
-
 // Event pairs recorded around kernel launches when profiling is on.
 struct Prof {
   static constexpr int kPool = 8192;
-  bool on = false;
+  std::atomic<bool> on{false};
+  std::recursive_mutex mu;  // held by a ProfScope from its start event to its stop event
   hipEvent_t start[kPool], stop[kPool];
   int phase[kPool];
   int created = 0;
@@ -223,14 +236,13 @@ struct State {
   bool ready = false;
   Prof prof;
   int device = -1;
-  Workspace ws;
+  Workspace ws;  // the null stream's
+  std::mutex ws_mu;  // guards stream_ws
+  std::vector<std::pair<hipStream_t, std::unique_ptr<Workspace>>> stream_ws;  // any other stream's
   Layer layers[FDM_MAX_LAYERS];
   DenseLayer dense[FDM_MAX_LAYERS];
   std::unique_ptr<StreamedLayer> streamed[FDM_MAX_LAYERS];
   std::unique_ptr<AttnLayer> attn[FDM_MAX_LAYERS];
-  AttnScratch attn_ws;
-  int* stream_ids_h = nullptr;    // pinned host: the routed ids of a streamed call
-  int* stream_slots_h = nullptr;  // pinned host: their cache slots
 };
 
 State g;
@@ -258,8 +270,7 @@ int down_type(size_t expert_size, bool* q6) {
               expert_size, FDM_EXPERT_Q4K_BYTES, FDM_EXPERT_Q6K_BYTES);
 }
 
-void free_workspace() {
-  Workspace& w = g.ws;
+void free_workspace(Workspace& w) {
   void* ptrs[] = {w.xd,       w.logits,   w.idx,     w.w,       w.act,
                   w.act_xd,   w.gu_count, w.dn_count, w.eo,
                   w.stage_x,  w.stage_y,  w.stage_idx, w.stage_w,
@@ -268,11 +279,13 @@ void free_workspace() {
                   w.p_hpost, w.q_planes, w.q_xs, w.q_xe, w.q_chunks, w.q_nchunks, w.dense_act};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  g.ws = Workspace();
+  w.attn.release();
+  for (int* p : {w.ids_h, w.slots_h})
+    if (p) (void)hipHostFree(p);
+  w = Workspace();
 }
 
-int alloc_workspace() {
-  Workspace& w = g.ws;
+int alloc_workspace(Workspace& w) {
   FDM_HIP(hipMalloc(&w.xd, kXdGroups * sizeof(XGroup)));
   FDM_HIP(hipMalloc(&w.logits, (size_t)FDM_MAX_TOKENS * FDM_N_EXPERTS * sizeof(float)));
   FDM_HIP(hipMalloc(&w.idx, (size_t)FDM_MAX_TOKENS * FDM_MAX_K * sizeof(int)));
@@ -303,6 +316,46 @@ int alloc_workspace() {
   FDM_HIP(hipMalloc(&w.q_chunks, kQMaxChunks * sizeof(int4)));
   FDM_HIP(hipMalloc(&w.q_nchunks, sizeof(int)));
   return FDM_OK;
+}
+
+// The workspace of the calls on stream s.  Calls on one stream run in stream
+// order and share its workspace; calls on different streams use different
+// workspaces and may overlap.  The null stream's workspace is made by
+// fdm_init, any other stream's at its first call (kept until
+// fdm_stream_release or fdm_shutdown).
+constexpr size_t kMaxStreamWorkspaces = 64;
+
+int stream_workspace(hipStream_t s, Workspace** out) {
+  if (!s) {
+    *out = &g.ws;
+    return FDM_OK;
+  }
+  std::lock_guard<std::mutex> lock(g.ws_mu);
+  for (auto& e : g.stream_ws)
+    if (e.first == s) {
+      *out = e.second.get();
+      return FDM_OK;
+    }
+  if (g.stream_ws.size() >= kMaxStreamWorkspaces)
+    return fail(FDM_E_STATE, "more than %zu streams hold workspaces; fdm_stream_release the unused ones",
+                kMaxStreamWorkspaces);
+  auto w = std::make_unique<Workspace>();
+  if (int rc = alloc_workspace(*w)) {
+    free_workspace(*w);
+    return rc;
+  }
+  *out = w.get();
+  g.stream_ws.emplace_back(s, std::move(w));
+  return FDM_OK;
+}
+
+// The workspace of stream s if it has one.
+Workspace* find_workspace(hipStream_t s) {
+  if (!s) return &g.ws;
+  std::lock_guard<std::mutex> lock(g.ws_mu);
+  for (auto& e : g.stream_ws)
+    if (e.first == s) return e.second.get();
+  return nullptr;
 }
 
 void release_dense(DenseLayer& d) {
@@ -426,12 +479,16 @@ int prof_drain() {
 }
 
 // Brackets one launch with events when profiling is on.
+// Scopes on several host threads take turns (the pool's lock is held from
+// the start event to the stop event).
 struct ProfScope {
   int slot = -1;
   hipStream_t s;
+  std::unique_lock<std::recursive_mutex> lock;
   ProfScope(int phase, hipStream_t st) : s(st) {
     Prof& p = g.prof;
     if (!p.on) return;
+    lock = std::unique_lock<std::recursive_mutex>(p.mu);
     if (p.pending == Prof::kPool && prof_drain() != FDM_OK) return;
     slot = p.pending;
     p.phase[slot] = phase;
@@ -691,8 +748,8 @@ int fdm_init(int device) {
                 prop.gcnArchName);
   g_num_cus = prop.multiProcessorCount;
   if (int rc = bind_scratch(device)) return rc;
-  if (int rc = alloc_workspace()) {
-    free_workspace();
+  if (int rc = alloc_workspace(g.ws)) {
+    free_workspace(g.ws);
     return rc;
   }
   g.device = device;
@@ -707,12 +764,10 @@ int fdm_shutdown(void) {
   for (auto& d : g.dense) release_dense(d);
   for (auto& st : g.streamed) st.reset();
   for (auto& a : g.attn) a.reset();
-  g.attn_ws.release();
   release_stream_pool();
-  for (int* p : {g.stream_ids_h, g.stream_slots_h})
-    if (p) (void)hipHostFree(p);
-  g.stream_ids_h = g.stream_slots_h = nullptr;
-  free_workspace();
+  for (auto& e : g.stream_ws) free_workspace(*e.second);
+  g.stream_ws.clear();
+  free_workspace(g.ws);
   for (int i = 0; i < g.prof.created; ++i) {
     (void)hipEventDestroy(g.prof.start[i]);
     (void)hipEventDestroy(g.prof.stop[i]);
@@ -774,15 +829,37 @@ int fdm_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stream) {
 
 int fdm_stream_sync(void* stream) {
   if (int rc = check_ready()) return rc;
-  FDM_HIP(hipStreamSynchronize(as_stream(stream)));
-  if (g.ws.epochs.epoch != 0) {
+  hipStream_t s = as_stream(stream);
+  FDM_HIP(hipStreamSynchronize(s));
+  Workspace* w = find_workspace(s);
+  if (w && w->epochs.epoch != 0) {
     // the layer kernel records the epoch of a call whose waits timed out
     unsigned err = 0;
-    FDM_HIP(hipMemcpy(&err, g.ws.layer_flags + kLayerFlagErr * kLayerStride, sizeof(err),
+    FDM_HIP(hipMemcpy(&err, w->layer_flags + kLayerFlagErr * kLayerStride, sizeof(err),
                       hipMemcpyDeviceToHost));
-    if (g.ws.epochs.new_error(err))
+    if (w->epochs.new_error(err))
       return fail(FDM_E_STATE, "fdm_moe_layer call %u timed out inside the kernel", err);
   }
+  return FDM_OK;
+}
+
+int fdm_stream_release(void* stream) {
+  if (int rc = check_ready()) return rc;
+  hipStream_t s = as_stream(stream);
+  if (!s) return FDM_OK;  // the null stream keeps its workspace until fdm_shutdown
+  std::unique_ptr<Workspace> w;
+  {
+    std::lock_guard<std::mutex> lock(g.ws_mu);
+    for (size_t i = 0; i < g.stream_ws.size(); ++i)
+      if (g.stream_ws[i].first == s) {
+        w = std::move(g.stream_ws[i].second);
+        g.stream_ws.erase(g.stream_ws.begin() + i);
+        break;
+      }
+  }
+  if (!w) return FDM_OK;
+  FDM_HIP(hipDeviceSynchronize());  // the stream itself may already be destroyed
+  free_workspace(*w);
   return FDM_OK;
 }
 
@@ -836,13 +913,15 @@ int fdm_matvec_q4k(const void* d_W, const float* d_x, float* d_y, uint32_t out_d
                    uint32_t in_dim, void* stream) {
   if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 4)) return rc;
   hipStream_t s = as_stream(stream);
+  Workspace* w = nullptr;
+  if (int rc = stream_workspace(s, &w)) return rc;
   {
     ProfScope p(FDM_PROF_XDIGITS, s);
-    FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
+    FDM_HIP(launch_xdigits(d_x, in_dim / 64, w->xd, s));
   }
   {
     ProfScope p(FDM_PROF_MATVEC, s);
-    FDM_HIP(launch_matvec_q4k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
+    FDM_HIP(launch_matvec_q4k(static_cast<const uint8_t*>(d_W), w->xd, d_y, (int)out_dim,
                               (int)in_dim, s));
   }
   return FDM_OK;
@@ -852,13 +931,15 @@ int fdm_matvec_q6k(const void* d_W, const float* d_x, float* d_y, uint32_t out_d
                    uint32_t in_dim, void* stream) {
   if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 2)) return rc;
   hipStream_t s = as_stream(stream);
+  Workspace* w = nullptr;
+  if (int rc = stream_workspace(s, &w)) return rc;
   {
     ProfScope p(FDM_PROF_XDIGITS, s);
-    FDM_HIP(launch_xdigits(d_x, in_dim / 64, g.ws.xd, s));
+    FDM_HIP(launch_xdigits(d_x, in_dim / 64, w->xd, s));
   }
   {
     ProfScope p(FDM_PROF_MATVEC, s);
-    FDM_HIP(launch_matvec_q6k(static_cast<const uint8_t*>(d_W), g.ws.xd, d_y, (int)out_dim,
+    FDM_HIP(launch_matvec_q6k(static_cast<const uint8_t*>(d_W), w->xd, d_y, (int)out_dim,
                               (int)in_dim, s));
   }
   return FDM_OK;
@@ -885,21 +966,22 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   t.K = 0;
   t.n_slots = 1;
   t.rel = false;  // the caller's blob: packed layout
+  Workspace* w = nullptr;
+  if (int rc = stream_workspace(s, &w)) return rc;
   {
     ProfScope p(FDM_PROF_XDIGITS, s);
-    FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, g.ws.xd, s));
+    FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, w->xd, s));
   }
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, s));
+    FDM_HIP(launch_gateup(t, w->xd, w->act, w->act_xd, w->gu_count, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, q6, g.ws.act_xd, nullptr, d_out, nullptr, g.ws.eo,
-                                g.ws.dn_count, s));
+    FDM_HIP(launch_down_combine(t, q6, w->act_xd, nullptr, d_out, nullptr, w->eo, w->dn_count, s));
   }
   if (d_act)
-    FDM_HIP(hipMemcpyAsync(d_act, g.ws.act, FDM_MOE_FFN * sizeof(float),
+    FDM_HIP(hipMemcpyAsync(d_act, w->act, FDM_MOE_FFN * sizeof(float),
                            hipMemcpyDeviceToDevice, s));
   return FDM_OK;
 }
@@ -1130,18 +1212,20 @@ int fdm_moe_forward(int L, const float* d_h_post, const int* d_idx, const float*
   if (!d_h_post || !d_idx || !d_w || !d_moe_out) return fail(FDM_E_INVAL, "null pointer");
   hipStream_t s = as_stream(stream);
   const SlotTable t = slots_for(*y, d_idx, d_w, K, false);
+  Workspace* w = nullptr;
+  if (int rc = stream_workspace(s, &w)) return rc;
   {
     ProfScope p(FDM_PROF_XDIGITS, s);
-    FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, g.ws.xd, s));
+    FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, w->xd, s));
   }
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, g.ws.xd, g.ws.act, g.ws.act_xd, g.ws.gu_count, s));
+    FDM_HIP(launch_gateup(t, w->xd, w->act, w->act_xd, w->gu_count, s));
   }
   {
     ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, y->down_q6, g.ws.act_xd, nullptr, d_moe_out, nullptr,
-                                g.ws.eo, g.ws.dn_count, s));
+    FDM_HIP(launch_down_combine(t, y->down_q6, w->act_xd, nullptr, d_moe_out, nullptr, w->eo, w->dn_count,
+                                s));
   }
   return FDM_OK;
 }
@@ -1152,6 +1236,9 @@ int fdm_moe_forward_host(int L, const float* h_post, const int* exp_idx, const f
   if (int rc = get_layer(L, &y)) return rc;
   if (int rc = check_K(K)) return rc;
   if (!h_post || !exp_idx || !exp_w || !moe_out) return fail(FDM_E_INVAL, "null pointer");
+  // the null stream's staging buffers: host callers take turns
+  static std::mutex host_mu;
+  std::lock_guard<std::mutex> lock(host_mu);
   Workspace& w = g.ws;
   FDM_HIP(hipMemcpy(w.stage_x, h_post, FDM_HIDDEN * sizeof(float), hipMemcpyHostToDevice));
   FDM_HIP(hipMemcpy(w.stage_idx, exp_idx, K * sizeof(int), hipMemcpyHostToDevice));
@@ -1193,10 +1280,12 @@ int run_layer(int L, const float* h, const float* norm_w, float* h_post_out, con
   a.down_q6 = y->down_q6 ? 1 : 0;
   a.K = K;
   a.n_slots = K + (y->shared ? 1 : 0);
-  a.idx = idx ? idx : g.ws.idx;
-  a.w = w ? w : g.ws.w;
-  a.xd = g.ws.xd;
-  uint64_t* tg = g.ws.layer_tagged;
+  Workspace* ws = nullptr;
+  if (int rc = stream_workspace(s, &ws)) return rc;
+  a.idx = idx ? idx : ws->idx;
+  a.w = w ? w : ws->w;
+  a.xd = ws->xd;
+  uint64_t* tg = ws->layer_tagged;
   a.scores = tg;
   a.prov = tg + 256;
   a.route_w = tg + 256 + 16;
@@ -1204,9 +1293,9 @@ int run_layer(int L, const float* h, const float* norm_w, float* h_post_out, con
   a.act = tg + 256 + 48;
   a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
   a.norm_inv = tg + kLayerTagged - 16;  // its own 128-byte line
-  a.counters = g.ws.layer_cnt;
-  a.flags = g.ws.layer_flags;
-  a.epoch = g.ws.epochs.next();
+  a.counters = ws->layer_cnt;
+  a.flags = ws->layer_flags;
+  a.epoch = ws->epochs.next();
   a.spin_limit = g_layer_spin_limit;
   {
     ProfScope p(FDM_PROF_LAYER, s);
@@ -1237,8 +1326,7 @@ namespace fdm {
 namespace {
 // Per-row buffers of the batched path, grown (never shrunk) to `rows`.
 // Callers synchronise with earlier work on the stream before a reallocation.
-int ensure_batch_rows(size_t rows, hipStream_t s) {
-  Workspace& w = g.ws;
+int ensure_batch_rows(Workspace& w, size_t rows, hipStream_t s) {
   if (rows <= w.b_rows) return FDM_OK;
   FDM_HIP(hipStreamSynchronize(s));
   if (w.b_act) (void)hipFree(w.b_act);
@@ -1260,8 +1348,7 @@ int ensure_batch_rows(size_t rows, hipStream_t s) {
 namespace fdm {
 namespace {
 // The rms_norm output of prefill for T tokens (grown on demand).
-int ensure_prefill(int T, hipStream_t s) {
-  Workspace& w = g.ws;
+int ensure_prefill(Workspace& w, int T, hipStream_t s) {
   if (T > w.p_tokens) {
     FDM_HIP(hipStreamSynchronize(s));
     if (w.p_hpost) (void)hipFree(w.p_hpost);
@@ -1276,8 +1363,7 @@ int ensure_prefill(int T, hipStream_t s) {
 // Activation planes for the grouped GEMMs of T tokens and `rows` expert
 // rows: the larger of the token inputs (T x 7168) and the SwiGLU rows
 // (rows x 2048), three planes (grown on demand).
-int ensure_planes(int T, size_t rows, hipStream_t s) {
-  Workspace& w = g.ws;
+int ensure_planes(Workspace& w, int T, size_t rows, hipStream_t s) {
   const size_t elems = std::max((size_t)T * FDM_HIDDEN, rows * FDM_MOE_FFN);
   const size_t nrows = std::max((size_t)T, rows);
   if (elems <= w.q_elems && nrows <= w.q_rows) return FDM_OK;
@@ -1311,8 +1397,7 @@ struct QScratch {
   int* n_chunks;
 };
 
-QScratch workspace_q() {
-  const Workspace& w = g.ws;
+QScratch workspace_q(const Workspace& w) {
   return QScratch{w.q_planes, w.q_xs, w.q_xe, w.q_chunks, w.q_nchunks};
 }
 
@@ -1380,18 +1465,21 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     if (int rc = get_layer(layers[l], &y)) return rc;
   }
   hipStream_t s = as_stream(stream);
+  Workspace* ws = nullptr;
+  if (int rc = stream_workspace(s, &ws)) return rc;
+  Workspace& w = *ws;
   const size_t rows = (size_t)T * K + T;
-  if (int rc = ensure_prefill(T, s)) return rc;
-  if (int rc = ensure_batch_rows(rows, s)) return rc;
-  if (int rc = ensure_planes(T, rows, s)) return rc;
+  if (int rc = ensure_prefill(w, T, s)) return rc;
+  if (int rc = ensure_batch_rows(w, rows, s)) return rc;
+  if (int rc = ensure_planes(w, T, rows, s)) return rc;
   ProfScope prof(FDM_PROF_PREFILL, s);
   for (int l = 0; l < n_layers; ++l) {
     Layer* y = nullptr;
     (void)get_layer(layers[l], &y);
-    int* idx = d_idx ? d_idx + (size_t)l * T * K : g.ws.idx;
-    FDM_HIP(launch_rms_norm(d_H, d_norm_w ? d_norm_w[l] : nullptr, g.ws.p_hpost, T, FDM_HIDDEN, s));
-    FDM_HIP(launch_router_logits(y->Wg, g.ws.p_hpost, FDM_N_EXPERTS, FDM_HIDDEN, T, g.ws.logits, s));
-    FDM_HIP(launch_route(g.ws.logits, y->bias, T, K, idx, g.ws.w, s));
+    int* idx = d_idx ? d_idx + (size_t)l * T * K : w.idx;
+    FDM_HIP(launch_rms_norm(d_H, d_norm_w ? d_norm_w[l] : nullptr, w.p_hpost, T, FDM_HIDDEN, s));
+    FDM_HIP(launch_router_logits(y->Wg, w.p_hpost, FDM_N_EXPERTS, FDM_HIDDEN, T, w.logits, s));
+    FDM_HIP(launch_route(w.logits, y->bias, T, K, idx, w.w, s));
     BatchArgs b{};
     b.T = T;
     b.K = K;
@@ -1401,18 +1489,18 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     b.h_in = d_H;
     b.out = d_H;  // residual in place
     b.idx = idx;
-    b.w = g.ws.w;
-    b.act = g.ws.b_act;
-    b.act_xd = g.ws.b_act_xd;
-    b.eo = g.ws.b_eo;
-    b.seg_start = g.ws.b_seg;
-    b.pair_tok = g.ws.b_pair_tok;
-    b.pair_of = g.ws.b_pair_of;
-    b.distinct = g.ws.b_distinct;
-    b.n_distinct = g.ws.b_ndistinct;
+    b.w = w.w;
+    b.act = w.b_act;
+    b.act_xd = w.b_act_xd;
+    b.eo = w.b_eo;
+    b.seg_start = w.b_seg;
+    b.pair_tok = w.b_pair_tok;
+    b.pair_of = w.b_pair_of;
+    b.distinct = w.b_distinct;
+    b.n_distinct = w.b_ndistinct;
     FDM_HIP(launch_dispatch(b, s));
     // prefill precision: one fp16 plane of the activations (the bar is 1e-2)
-    if (int rc = run_qgemm_experts(y, b, g.ws.p_hpost, 1, workspace_q(), s)) return rc;
+    if (int rc = run_qgemm_experts(y, b, w.p_hpost, 1, workspace_q(w), s)) return rc;
     FDM_HIP(launch_combine(b, s));
   }
   return FDM_OK;
@@ -1523,15 +1611,17 @@ int fdm_moe_forward_batched(int L, const float* d_X, const float* d_H_in, int T,
   Layer* y = nullptr;
   if (int rc = check_batched_args(L, d_X, T, K, d_hidden, &y)) return rc;
   hipStream_t s = as_stream(stream);
+  Workspace* ws = nullptr;
+  if (int rc = stream_workspace(s, &ws)) return rc;
+  Workspace& w = *ws;
   const size_t rows = (size_t)T * K + (y->shared ? T : 0);
-  if (int rc = ensure_batch_rows(rows, s)) return rc;
+  if (int rc = ensure_batch_rows(w, rows, s)) return rc;
   if (batch_uses_mfma(T)) {
-    if (int rc = ensure_planes(T, rows, s)) return rc;
+    if (int rc = ensure_planes(w, T, rows, s)) return rc;
   }
-  const Workspace& w = g.ws;
   const BatchScratch sc{w.xd,         w.logits,   w.idx,      w.w,        w.b_seg,
                         w.b_pair_tok, w.b_pair_of, w.b_distinct, w.b_ndistinct, w.b_act,
-                        w.b_act_xd,   w.b_eo,      workspace_q()};
+                        w.b_act_xd,   w.b_eo,      workspace_q(w)};
   return batched_step(y, d_X, d_H_in, T, K, d_hidden, d_idx, d_w, d_n_distinct, sc, s);
 }
 
@@ -1569,6 +1659,7 @@ int fdm_set_batch_kernel(int mode, int* prev) {
 int fdm_prof_enable(int on) {
   if (int rc = check_ready()) return rc;
   Prof& p = g.prof;
+  std::lock_guard<std::recursive_mutex> lock(p.mu);
   if (on && p.created == 0) {
     for (int i = 0; i < Prof::kPool; ++i) {
       FDM_HIP(hipEventCreate(&p.start[i]));
@@ -1586,6 +1677,7 @@ int fdm_prof_enable(int on) {
 
 int fdm_prof_reset(void) {
   if (int rc = check_ready()) return rc;
+  std::lock_guard<std::recursive_mutex> lock(g.prof.mu);
   if (g.prof.created == 0) return FDM_OK;
   if (int rc = prof_drain()) return rc;
   prof_clear_stats();
@@ -1596,6 +1688,7 @@ int fdm_prof_read(int phase, int* count, double* total_ms, double* min_ms, doubl
   if (int rc = check_ready()) return rc;
   if (phase < 0 || phase >= FDM_PROF_PHASES) return fail(FDM_E_INVAL, "phase %d", phase);
   Prof& p = g.prof;
+  std::lock_guard<std::recursive_mutex> lock(p.mu);
   if (p.created == 0) {
     if (count) *count = 0;
     if (total_ms) *total_ms = 0.0;
@@ -1627,11 +1720,9 @@ int fdm_layer_stream_open(int L, const char* layer_file, size_t expert_size, int
   if (n_threads < 0 || n_threads > 64) return fail(FDM_E_INVAL, "n_threads=%d: 0 (default 8) .. 64", n_threads);
   if (!aligned(d_Wg, 16) || (d_shared && !aligned(d_shared, 16)))
     return fail(FDM_E_INVAL, "router weights and shared expert must be 16-byte aligned");
-  if (!g.stream_ids_h) {
-    FDM_HIP(hipHostMalloc(reinterpret_cast<void**>(&g.stream_ids_h), FDM_MAX_K * sizeof(int), hipHostMallocDefault));
-    FDM_HIP(hipHostMalloc(reinterpret_cast<void**>(&g.stream_slots_h), FDM_MAX_K * sizeof(int), hipHostMallocDefault));
-  }
   auto st = std::make_unique<StreamedLayer>();
+  FDM_HIP(hipEventCreateWithFlags(&st->done, hipEventDisableTiming));
+  FDM_HIP(hipEventRecord(st->done, nullptr));
   std::string err;
   if (int rc = st->es.open(layer_file, expert_size, n_experts, n_cache, n_threads ? n_threads : 8, g.device, &err))
     return fail(rc, "layer %d: %s", L, err.c_str());
@@ -1659,16 +1750,24 @@ int fdm_moe_layer_streamed(int L, const float* d_h_post, const float* d_h_in, in
   StreamedLayer& y = *g.streamed[L];
   if (K > y.es.n_cache()) return fail(FDM_E_INVAL, "K=%d exceeds the layer's %d cache slots", K, y.es.n_cache());
   hipStream_t s = as_stream(stream);
-  Workspace& w = g.ws;
+  Workspace* ws = nullptr;
+  if (int rc = stream_workspace(s, &ws)) return rc;
+  Workspace& w = *ws;
+  if (!w.ids_h) {
+    FDM_HIP(hipHostMalloc(reinterpret_cast<void**>(&w.ids_h), FDM_MAX_K * sizeof(int), hipHostMallocDefault));
+    FDM_HIP(hipHostMalloc(reinterpret_cast<void**>(&w.slots_h), FDM_MAX_K * sizeof(int), hipHostMallocDefault));
+  }
   // route on the device (infer.m:1881-1883), then the ids to the host
   FDM_HIP(launch_router_logits(y.Wg, d_h_post, FDM_N_EXPERTS, FDM_HIDDEN, 1, w.logits, s));
   FDM_HIP(launch_route(w.logits, y.bias, 1, K, w.idx, w.w, s));
-  FDM_HIP(hipMemcpyAsync(g.stream_ids_h, w.idx, K * sizeof(int), hipMemcpyDeviceToHost, s));
+  FDM_HIP(hipMemcpyAsync(w.ids_h, w.idx, K * sizeof(int), hipMemcpyDeviceToHost, s));
   FDM_HIP(hipStreamSynchronize(s));
+  std::lock_guard<std::mutex> lock(y.mu);
+  FDM_HIP(hipEventSynchronize(y.done));  // the previous call's kernels have read the cache
   // the selected experts into the cache (parallel pread, infer.m:1577-1602)
   std::string err;
-  if (int rc = y.es.fetch(g.stream_ids_h, K, g.stream_slots_h, &err)) return fail(rc, "layer %d: %s", L, err.c_str());
-  FDM_HIP(hipMemcpyAsync(w.stage_idx, g.stream_slots_h, K * sizeof(int), hipMemcpyHostToDevice, s));
+  if (int rc = y.es.fetch(w.ids_h, K, w.slots_h, &err)) return fail(rc, "layer %d: %s", L, err.c_str());
+  FDM_HIP(hipMemcpyAsync(w.stage_idx, w.slots_h, K * sizeof(int), hipMemcpyHostToDevice, s));
   SlotTable t;
   t.experts = y.es.cache();
   t.expert_size = y.expert_size;
@@ -1682,6 +1781,7 @@ int fdm_moe_layer_streamed(int L, const float* d_h_post, const float* d_h_in, in
   FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, w.xd, s));
   FDM_HIP(launch_gateup(t, w.xd, w.act, w.act_xd, w.gu_count, s));
   FDM_HIP(launch_down_combine(t, y.q6, w.act_xd, d_h_in, d_hidden, nullptr, w.eo, w.dn_count, s));
+  FDM_HIP(hipEventRecord(y.done, s));
   if (d_idx) FDM_HIP(hipMemcpyAsync(d_idx, w.idx, K * sizeof(int), hipMemcpyDeviceToDevice, s));
   if (d_w) FDM_HIP(hipMemcpyAsync(d_w, w.w, K * sizeof(float), hipMemcpyDeviceToDevice, s));
   return FDM_OK;
@@ -1724,6 +1824,27 @@ static void yarn_table(float* f) {
   }
 }
 
+// The attention scratch of workspace w for a cache of seq positions (grown,
+// never shrunk, after the stream's earlier work).
+static int ensure_attn(Workspace& w, int seq, hipStream_t s) {
+  AttnScratch& ws = w.attn;
+  if (ws.seq >= seq) return FDM_OK;
+  FDM_HIP(hipStreamSynchronize(s));
+  ws.release();
+  const size_t H = FDM_HIDDEN, QA = 1536, QB = 128 * 192, KVA = 576, O = 128 * 128;
+  const size_t n[] = {H, QA, QA, QB, KVA, 512, 128 * 512, (size_t)128 * seq, 128 * 512, O,
+                      (size_t)((seq + 63) / 64) * 128 * 512};
+  float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.kv_a, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn,
+                 &ws.part};
+  for (int i = 0; i < 11; ++i)
+    if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
+      ws.release();
+      return fail(FDM_E_NOMEM, "cannot allocate the attention scratch");
+    }
+  ws.seq = seq;
+  return FDM_OK;
+}
+
 int fdm_attn_upload(int L, const fdm_attn_weights* w, int max_seq) {
   if (int rc = check_ready()) return rc;
   if (L < 0 || L >= FDM_MAX_LAYERS) return fail(FDM_E_INVAL, "layer %d out of range", L);
@@ -1753,21 +1874,7 @@ int fdm_attn_upload(int L, const fdm_attn_weights* w, int max_seq) {
     return fail(FDM_E_NOMEM, "cannot allocate the KV cache of layer %d", L);
   FDM_HIP(hipMemcpy(a->freq, freq, sizeof freq, hipMemcpyHostToDevice));
   a->max_seq = max_seq;
-  AttnScratch& ws = g.attn_ws;
-  if (ws.seq < max_seq) {
-    (void)hipDeviceSynchronize();
-    ws.release();
-    const size_t n[] = {H, QA, QA, QB, KVA, 512, 128 * 512, (size_t)128 * max_seq, 128 * 512, O,
-                        (size_t)((max_seq + 63) / 64) * 128 * 512};
-    float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.kv_a, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn,
-                   &ws.part};
-    for (int i = 0; i < 11; ++i)
-      if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
-        ws.release();
-        return fail(FDM_E_NOMEM, "cannot allocate the attention scratch");
-      }
-    ws.seq = max_seq;
-  }
+  if (int rc = ensure_attn(g.ws, max_seq, nullptr)) return rc;  // the null stream's, made ahead
   (void)hipDeviceSynchronize();
   g.attn[L] = std::move(a);
   return FDM_OK;
@@ -1875,8 +1982,11 @@ int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
   if (pos < 0) return fail(FDM_E_INVAL, "pos %d", pos);
   AttnLayer& a = *g.attn[L];
   if (a.len >= a.max_seq) return fail(FDM_E_INVAL, "KV cache of layer %d is full (%d)", L, a.max_seq);
-  AttnScratch& ws = g.attn_ws;
   hipStream_t s = as_stream(stream);
+  Workspace* w = nullptr;
+  if (int rc = stream_workspace(s, &w)) return rc;
+  if (int rc = ensure_attn(*w, a.max_seq, s)) return rc;
+  AttnScratch& ws = w->attn;
   ProfScope prof(FDM_PROF_ATTN, s);
   FDM_HIP(launch_rms_norm(d_hidden, a.attn_norm, ws.normed, 1, FDM_HIDDEN, s));
   FDM_HIP(launch_mv_f16(a.q_a, ws.normed, nullptr, ws.q_a, 1536, FDM_HIDDEN, s));
@@ -2031,6 +2141,8 @@ int fdm_dense_ffn(int L, const float* d_h_post, const float* d_h_in, float* d_hi
   if (!d_h_post || !d_hidden) return fail(FDM_E_INVAL, "null pointer");
   if (!aligned(d_h_post, 16)) return fail(FDM_E_INVAL, "h_post must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  Workspace* w = nullptr;
+  if (int rc = stream_workspace(s, &w)) return rc;
   ProfScope prof(FDM_PROF_DENSE, s);
   DenseArgs a;
   a.gate = d.gate;
@@ -2038,7 +2150,7 @@ int fdm_dense_ffn(int L, const float* d_h_post, const float* d_h_in, float* d_hi
   a.down = d.down;
   a.x = d_h_post;
   a.h_in = d_h_in;
-  a.act = g.ws.dense_act;
+  a.act = w->dense_act;
   a.out = d_hidden;
   a.inter = d.inter;
   a.n_cus = g_num_cus;

@@ -79,6 +79,22 @@ int fdm_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, void *stream);
 int fdm_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, void *stream);
 int fdm_stream_sync(void *stream);
 
+/* ---- streams and host threads ----------------------------------------------
+ * Every call that needs scratch memory takes it from the workspace of its
+ * stream: calls on one stream run in stream order and share it, calls on
+ * different streams use different workspaces, so host threads that each use
+ * their own stream may call concurrently.  The null stream's workspace is
+ * made by fdm_init; another stream's at its first call, kept until
+ * fdm_stream_release(stream) or fdm_shutdown (at most 64 streams at a time:
+ * FDM_E_STATE beyond).  Release a stream's workspace before destroying the
+ * stream if its handle may be reused.  Shared across streams, by design:
+ * a streamed layer's expert cache (calls take turns), an attention layer's
+ * KV cache (one sequence: one stream at a time), the scratch of
+ * fdm_moe_forward_batched_noalloc, and the timing pool of fdm_prof_*.
+ * (Concurrency rule of the reference: one GPU queue per process,
+ * infer.m:1276-1400; no counterpart of fdm_stream_release.) */
+int fdm_stream_release(void *stream);
+
 /* ---- quant.h device twins (quant.h:11-15, quant.c:4-92) -------------------
  * Bit-exact with quant.c read as C with FP_CONTRACT off: every product and
  * difference rounds separately.  n must be a multiple of 256. */
