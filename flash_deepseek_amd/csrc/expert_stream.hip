@@ -19,6 +19,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 #include <thread>
 
 #include "../../include/fdm.h"
@@ -30,7 +31,8 @@ namespace {
 
 constexpr size_t kStreamChunk = 4u << 20;
 
-// Pinned staging and copy streams shared by every streamed layer.
+// Pinned staging and copy streams shared by every streamed layer, grown to
+// the largest n_threads a layer asks for.  One fetch at a time uses it.
 struct ReadPool {
   struct Worker {
     hipStream_t s = nullptr;
@@ -39,29 +41,37 @@ struct ReadPool {
   };
   std::vector<Worker> w;
   int device = -1;
+  std::mutex mu;  // held by a fetch's reads and by init
 
   hipError_t init(int n, int dev) {
-    if (!w.empty()) return hipSuccess;
+    std::lock_guard<std::mutex> lock(mu);
     device = dev;
-    w.resize(n);
-    for (Worker& k : w) {
-      if (hipError_t e = hipStreamCreateWithFlags(&k.s, hipStreamNonBlocking)) return e;
-      for (int b = 0; b < 2; ++b) {
-        if (hipError_t e = hipHostMalloc(&k.buf[b], kStreamChunk, hipHostMallocDefault)) return e;
-        if (hipError_t e = hipEventCreateWithFlags(&k.ev[b], hipEventDisableTiming)) return e;
+    while (w.size() < (size_t)n) {
+      Worker k;  // kept only when complete
+      hipError_t e = hipStreamCreateWithFlags(&k.s, hipStreamNonBlocking);
+      for (int b = 0; b < 2 && e == hipSuccess; ++b) {
+        e = hipHostMalloc(&k.buf[b], kStreamChunk, hipHostMallocDefault);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&k.ev[b], hipEventDisableTiming);
       }
+      if (e != hipSuccess) {
+        free_worker(k);
+        return e;
+      }
+      w.push_back(k);
     }
     return hipSuccess;
   }
-  void release() {
-    for (Worker& k : w) {
-      if (k.s) (void)hipStreamSynchronize(k.s);
-      for (int b = 0; b < 2; ++b) {
-        if (k.ev[b]) (void)hipEventDestroy(k.ev[b]);
-        if (k.buf[b]) (void)hipHostFree(k.buf[b]);
-      }
-      if (k.s) (void)hipStreamDestroy(k.s);
+  static void free_worker(Worker& k) {
+    if (k.s) (void)hipStreamSynchronize(k.s);
+    for (int b = 0; b < 2; ++b) {
+      if (k.ev[b]) (void)hipEventDestroy(k.ev[b]);
+      if (k.buf[b]) (void)hipHostFree(k.buf[b]);
     }
+    if (k.s) (void)hipStreamDestroy(k.s);
+  }
+  void release() {
+    std::lock_guard<std::mutex> lock(mu);
+    for (Worker& k : w) free_worker(k);
     w.clear();
   }
 };
@@ -153,6 +163,7 @@ int ExpertStream::fetch(const int* ids, int K, int* slots, std::string* err) {
   std::atomic<size_t> next{0};
   std::atomic<int> rc{FDM_OK};
   std::atomic<int> io_errno{0};
+  std::lock_guard<std::mutex> pool_lock(g_pool.mu);
   auto work = [&](int t) {
     if (hipSetDevice(g_pool.device) != hipSuccess) {
       rc = FDM_E_HIP;
@@ -176,6 +187,7 @@ int ExpertStream::fetch(const int* ids, int K, int* slots, std::string* err) {
       const off_t at = (off_t)((uint64_t)m.first * es_ + off);
       while (got < len) {
         const ssize_t r = pread(fd_, dst + got, len - got, at + (off_t)got);
+        if (r < 0 && errno == EINTR) continue;
         if (r <= 0) {
           io_errno = r < 0 ? errno : EIO;
           rc = FDM_E_IO;

@@ -3,7 +3,9 @@ GGUF (stacked expert tensors, router, bias, shared expert; sparse files so
 only 16 experts carry data) and as a packed layer file in repack_experts.c's
 layout, loaded by fdm_layer_load_gguf / fdm_layer_load_packed.  The loaded
 layers must behave bit for bit like the same bytes attached directly
-(routing and outputs of fdm_moe_layer), and the loaders must reject the
+(routing and outputs of fdm_moe_layer), match the oracle run on the bytes
+written to the files (routing bit for bit, outputs within 1e-3 relative L2
+of float64), and the loaders must reject the
 inconsistencies load_layer_weights and repack_experts.c reject."""
 import time
 
@@ -11,7 +13,7 @@ import numpy as np
 import pytest
 
 from tests import gguf_writer as W
-from tests._helpers import empty_f32, say, to_dev, to_host
+from tests._helpers import empty_f32, rel_l2, say, to_dev, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -90,6 +92,22 @@ def attach_reference(fdm, m, L, with_shared=True):
     return ex, wg, b, sh
 
 
+def check_oracle(oracle, m, with_shared, h, h_in, got, K=8):
+    """A loaded layer against the oracle on the bytes written to the files:
+    the routing of the file's router and bias bit for bit, and the output
+    within 1e-3 relative L2 of the float64 sum h_in + sum_k w_k E_k (+ S)."""
+    out, gi, gw = got
+    ri, rw = oracle.route(oracle.router_logits(m["router"].astype(np.float32), h), m["bias"], K=K)
+    assert np.array_equal(gi, ri)
+    assert np.array_equal(gw.view(np.uint32), rw.view(np.uint32))
+    want = h_in.astype(np.float64)
+    for e, wk in zip(ri.tolist(), rw.tolist()):
+        want = want + np.float64(wk) * oracle.expert_ffn(np.concatenate(m["blobs"][e]), m["q6"], h)
+    if with_shared:
+        want = want + oracle.expert_ffn(np.concatenate(m["shared"]), m["q6"], h)
+    assert rel_l2(out, want) <= 1e-3
+
+
 def run(fdm, L, h, h_in, K=8):
     import torch
     out = empty_f32(H)
@@ -123,11 +141,13 @@ def test_load_gguf_and_packed_match_attached(fdm, oracle, model, with_shared):
                 print(f"{how} ingest of {nb / 1e9:.2f} GB (sparse files): {nb / dt / 1e9:.2f} GB/s")
                 assert q6 == model["q6"]
                 assert fdm.layer_info(L) == (model["es"], model["q6"], E)
-                for (h, h_in), ref in zip(toks, refs):
+                for t, ((h, h_in), ref) in enumerate(zip(toks, refs)):
                     got = run(fdm, L, h, h_in)
                     assert np.array_equal(got[1], ref[1])
                     assert np.array_equal(got[2].view(np.uint32), ref[2].view(np.uint32))
                     assert np.array_equal(got[0].view(np.uint32), ref[0].view(np.uint32))
+                    if t == 0:
+                        check_oracle(oracle, model, with_shared, h, h_in, got)
                 fdm.release_layer(L)
     finally:
         fdm.release_layer(50)
