@@ -75,14 +75,8 @@ __device__ __forceinline__ QLane qlane_load(const uint8_t* mat, int row, int blo
   return r;
 }
 
-// Bytes 0, 1 (and 2, 3) of w into the low bytes of the two halves.
-__device__ __forceinline__ uint32_t spread01(uint32_t w) { return (w & 0xFFu) | ((w << 8) & 0x00FF0000u); }
-__device__ __forceinline__ uint32_t spread23(uint32_t w) {
-  return ((w >> 16) & 0xFFu) | ((w >> 8) & 0x00FF0000u);
-}
-
-// fp16 bits of 1024 + sc * q for the two q held in the low bytes of the
-// halves of s (q < 16, so sc * q < 1024 fits the 10-bit mantissa).
+// fp16 bits of 1024 + sc * q for the two q held in bits 0-3 of the halves
+// of q2 (the rest zero; q < 16, so sc * q < 1024 fits the 10-bit mantissa).
 __device__ __forceinline__ uint32_t magic2(uint32_t q2, u16x2 sc2) {
   const u16x2 q = __builtin_bit_cast(u16x2, q2);
   const u16x2 v = q * sc2 + (u16x2){0x6400, 0x6400};
@@ -91,21 +85,25 @@ __device__ __forceinline__ uint32_t magic2(uint32_t q2, u16x2 sc2) {
 
 // The B operands of MFMA steps m (low nibbles) and m + 4 (high nibbles):
 // bytes 8 m' .. 8 m' + 7 of the lane's group, m' = m & 3 (q0 for m' < 2).
+// Elements are taken in the order 0 2 1 3 4 6 5 7 of each 8 (the order in
+// which k_xplanes stores the activations): a dword of qs holds the low
+// nibbles of elements 0 and 2 at bits 0 and 16, so each fp16 pair costs one
+// mask (after one of three shifts per dword) and one packed multiply-add.
 struct BPair {
   f16x8 lo, hi;
 };
 
 __device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, u16x2 sc_hi) {
-  const uint32_t s0 = spread01(w0), s1 = spread23(w0), s2 = spread01(w1), s3 = spread23(w1);
+  constexpr uint32_t M = 0x000F000Fu;
   u32x4 lo, hi;
-  lo.x = magic2(s0 & 0x000F000Fu, sc_lo);
-  lo.y = magic2(s1 & 0x000F000Fu, sc_lo);
-  lo.z = magic2(s2 & 0x000F000Fu, sc_lo);
-  lo.w = magic2(s3 & 0x000F000Fu, sc_lo);
-  hi.x = magic2((s0 >> 4) & 0x000F000Fu, sc_hi);
-  hi.y = magic2((s1 >> 4) & 0x000F000Fu, sc_hi);
-  hi.z = magic2((s2 >> 4) & 0x000F000Fu, sc_hi);
-  hi.w = magic2((s3 >> 4) & 0x000F000Fu, sc_hi);
+  lo.x = magic2(w0 & M, sc_lo);
+  lo.y = magic2((w0 >> 8) & M, sc_lo);
+  lo.z = magic2(w1 & M, sc_lo);
+  lo.w = magic2((w1 >> 8) & M, sc_lo);
+  hi.x = magic2((w0 >> 4) & M, sc_hi);
+  hi.y = magic2((w0 >> 12) & M, sc_hi);
+  hi.z = magic2((w1 >> 4) & M, sc_hi);
+  hi.w = magic2((w1 >> 12) & M, sc_hi);
   BPair b;
   b.lo = __builtin_bit_cast(f16x8, lo);
   b.hi = __builtin_bit_cast(f16x8, hi);
@@ -154,7 +152,8 @@ __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::
 // the row's largest |x| in [2^13, 2^14), x' = x * 2^s split into P fp16
 // planes (round to nearest, each the rounding of what the previous planes
 // left), xs[sb] = the fp32 sum over the sub-block of the planes' values,
-// xe = 2^-s.  Planes: [P][n_rows][kd].
+// xe = 2^-s.  Planes: [P][n_rows][kd], each run of 8 elements stored in the
+// order 0 2 1 3 4 6 5 7 (the weight operand's order).
 template <int P>
 __global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, int kd, size_t n_rows,
                                                  _Float16* __restrict__ xp, float* __restrict__ xs,
@@ -201,10 +200,11 @@ __global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, in
           sum += tot;
         }
       }
+      // stored in the order 0 2 1 3 4 6 5 7 that the weight operand uses
 #pragma unroll
       for (int p = 0; p < P; ++p)
         *reinterpret_cast<f16x8*>(xp + ((size_t)p * n_rows + row) * kd + 32 * sb + 8 * q) =
-            (f16x8){h[p][0], h[p][1], h[p][2], h[p][3], h[p][4], h[p][5], h[p][6], h[p][7]};
+            (f16x8){h[p][0], h[p][2], h[p][1], h[p][3], h[p][4], h[p][6], h[p][5], h[p][7]};
     }
     xs[row * nsb + sb] = sum;
   }
