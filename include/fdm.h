@@ -14,11 +14,11 @@
  *  - Pointers named d_* are device pointers; h_* are host pointers.
  *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
  *    Launches are asynchronous on that stream unless stated otherwise.
- *  - One device per process (fdm_init).  The library keeps one workspace
- *    per device for intermediate vectors (activation digits, expert
- *    outputs, routing results), as the reference keeps one set of shared
- *    Metal buffers (infer.m:1351-1373): calls that overlap in time on
- *    different streams of the same device race on it.
+ *  - One device per process (fdm_init).  Intermediate vectors (activation
+ *    digits, expert outputs, routing results) live in a workspace per
+ *    stream, where the reference keeps one set of shared Metal buffers
+ *    (infer.m:1351-1373): calls on different streams may overlap (see
+ *    "streams and host threads" below).
  *  - Layouts are the reference's: Q4_K 144-byte and Q6_K 210-byte blocks of
  *    256 weights (quant.h:6-8), matrices row-major with in_dim/256 blocks
  *    per row, a packed expert = [gate Q4_K 2048x7168 | up Q4_K | down Q4_K
@@ -61,8 +61,8 @@ extern "C" {
 #define FDM_E_FORMAT (-8)  /* malformed GGUF or layer file                  */
 
 /* ---- lifecycle: replaces metal_init (infer.m:1276-1400) -------------------
- * fdm_init selects `device`, checks it is gfx950 and allocates the
- * workspace.  Unlike metal_init (1 = ok, 0 = unavailable) it returns FDM_OK
+ * fdm_init selects `device`, checks it is gfx950 and allocates the null
+ * stream's workspace.  Unlike metal_init (1 = ok, 0 = unavailable) it returns FDM_OK
  * or an error code; fdm_available() gives the reference's 1/0 answer. */
 int fdm_init(int device);
 int fdm_shutdown(void);
@@ -248,8 +248,8 @@ int fdm_moe_forward_host(int L, const float *h_post, const int *exp_idx, const f
  * shared expert, combine, and the residual:
  *   hidden = h_in + sum_k w[k] E_k(h_post) + S(h_post).
  * d_h_in may be NULL (no residual).  d_idx / d_w (optional) receive the
- * routing.  One cooperative launch; calls on one device must not overlap
- * (they share the library's workspace).  A launch whose internal waits
+ * routing.  One launch; its scratch is the stream's workspace, so calls on
+ * different streams may overlap.  A launch whose internal waits
  * time out (never expected; it would mean a broken device) completes with
  * an unspecified result and makes the next fdm_stream_sync return
  * FDM_E_STATE. */
@@ -351,8 +351,9 @@ int fdm_moe_prefill(const int *layers, int n_layers, float *d_H, int T, int K,
  * fdm_moe_layer_streamed computes the same layer as fdm_moe_layer: it
  * routes on the device (bit-exact), synchronises the stream to read the
  * routed ids, reads the missing experts, then runs the experts, the combine
- * and the residual on `stream`; it returns after queuing them.  Calls on one
- * device must not overlap.  Opening a layer streamed releases it as a
+ * and the residual on `stream`; it returns after queuing them.  Calls on
+ * different streams take turns on the layer's cache (a fill waits for the
+ * previous call's kernels).  Opening a layer streamed releases it as a
  * resident layer and the other way round; fdm_layer_release releases both.
  * fdm_stream_stats: cumulative cache hits and misses (routed experts) and
  * bytes read from the file. */
@@ -375,7 +376,8 @@ int fdm_stream_stats(int L, uint64_t *hits, uint64_t *misses, uint64_t *bytes_re
  * the layout LayerAttnDense holds them (infer.m:687-706), row-major; the
  * library keeps its own copy (synchronous upload).  Each fdm_attn_forward
  * appends the token at the cache's next row (fdm_attn_reset empties it);
- * max_seq <= FDM_ATTN_MAX_SEQ.  Calls on one device must not overlap. */
+ * max_seq <= FDM_ATTN_MAX_SEQ.  An attention layer holds one sequence: its
+ * calls belong on one stream (its cache length is host state). */
 #define FDM_ATTN_MAX_SEQ 16384 /* MAX_SEQ, infer.m:67 */
 typedef struct fdm_attn_weights {
   const float *attn_norm;  /* [7168]                                 */
@@ -414,8 +416,8 @@ int fdm_attn_release(int L);
  * fp32 and rounds to F16 on the device, bit-exact with the reference's
  * (__fp16) cast; *inter receives the intermediate size (may be NULL).
  * fdm_dense_ffn: d_h_post 16-byte aligned, d_h_in may be NULL (no residual),
- * d_hidden must not alias d_h_post; calls on one device must not overlap
- * (they share the activation workspace). */
+ * d_hidden must not alias d_h_post; its activations live in the stream's
+ * workspace. */
 #define FDM_DENSE_FFN 18432
 int fdm_dense_upload(int L, const uint16_t *h_gate, const uint16_t *h_up, const uint16_t *h_down,
                      int inter);
