@@ -909,40 +909,81 @@ static int matvec_common(const void* d_W, const float* d_x, float* d_y, uint32_t
   return FDM_OK;
 }
 
-int fdm_matvec_q4k(const void* d_W, const float* d_x, float* d_y, uint32_t out_dim,
-                   uint32_t in_dim, void* stream) {
-  if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 4)) return rc;
+}  // extern "C"
+
+namespace fdm {
+namespace {
+// The layer kernel's share of a stream workspace: the digit records, the
+// tagged hand-off words, counters, flags and a fresh epoch.
+void layer_workspace_args(LayerArgs& a, Workspace* ws) {
+  a.xd = ws->xd;
+  uint64_t* tg = ws->layer_tagged;
+  a.scores = tg;
+  a.prov = tg + 256;
+  a.route_w = tg + 256 + 16;
+  a.route_perm = tg + 256 + 32;
+  a.act = tg + 256 + 48;
+  a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
+  a.norm_inv = tg + kLayerTagged - 16;  // its own 128-byte line
+  a.counters = ws->layer_cnt;
+  a.flags = ws->layer_flags;
+  a.epoch = ws->epochs.next();
+  a.spin_limit = g_layer_spin_limit;
+}
+
+// One launch (digit items, then row items) where the kernel supports in_dim;
+// otherwise the digits and the matvec as two launches.
+int run_matvec(bool q6, const void* d_W, const float* d_x, float* d_y, uint32_t out_dim, uint32_t in_dim,
+               void* stream) {
   hipStream_t s = as_stream(stream);
   Workspace* w = nullptr;
   if (int rc = stream_workspace(s, &w)) return rc;
+  const uint8_t* W = static_cast<const uint8_t*>(d_W);
+  if (matvec1_supported(q6, (int)in_dim)) {
+    MatvecArgs a;
+    a.W = W;
+    a.x = d_x;
+    a.y = d_y;
+    a.rows = (int)out_dim;
+    a.gr = (int)in_dim / 64;
+    a.xd = w->xd;
+    a.counter = w->layer_cnt;  // the layer kernel's digit counter and flag: calls on a stream never overlap
+    a.flag = w->layer_flags;
+    a.err = w->layer_flags + kLayerFlagErr * kLayerStride;
+    a.epoch = w->epochs.next();
+    a.spin_limit = g_layer_spin_limit;
+    ProfScope p(FDM_PROF_MATVEC, s);
+    FDM_HIP(launch_matvec1(a, q6, s));
+    return FDM_OK;
+  }
   {
     ProfScope p(FDM_PROF_XDIGITS, s);
     FDM_HIP(launch_xdigits(d_x, in_dim / 64, w->xd, s));
   }
   {
     ProfScope p(FDM_PROF_MATVEC, s);
-    FDM_HIP(launch_matvec_q4k(static_cast<const uint8_t*>(d_W), w->xd, d_y, (int)out_dim,
-                              (int)in_dim, s));
+    if (q6)
+      FDM_HIP(launch_matvec_q6k(W, w->xd, d_y, (int)out_dim, (int)in_dim, s));
+    else
+      FDM_HIP(launch_matvec_q4k(W, w->xd, d_y, (int)out_dim, (int)in_dim, s));
   }
   return FDM_OK;
+}
+}  // namespace
+}  // namespace fdm
+
+extern "C" {
+
+int fdm_matvec_q4k(const void* d_W, const float* d_x, float* d_y, uint32_t out_dim,
+                   uint32_t in_dim, void* stream) {
+  if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 4)) return rc;
+  return run_matvec(false, d_W, d_x, d_y, out_dim, in_dim, stream);
 }
 
 int fdm_matvec_q6k(const void* d_W, const float* d_x, float* d_y, uint32_t out_dim,
                    uint32_t in_dim, void* stream) {
   if (int rc = matvec_common(d_W, d_x, d_y, out_dim, in_dim, 2)) return rc;
-  hipStream_t s = as_stream(stream);
-  Workspace* w = nullptr;
-  if (int rc = stream_workspace(s, &w)) return rc;
-  {
-    ProfScope p(FDM_PROF_XDIGITS, s);
-    FDM_HIP(launch_xdigits(d_x, in_dim / 64, w->xd, s));
-  }
-  {
-    ProfScope p(FDM_PROF_MATVEC, s);
-    FDM_HIP(launch_matvec_q6k(static_cast<const uint8_t*>(d_W), w->xd, d_y, (int)out_dim,
-                              (int)in_dim, s));
-  }
-  return FDM_OK;
+  return run_matvec(true, d_W, d_x, d_y, out_dim, in_dim, stream);
 }
 
 // ---- one expert -----------------------------------------------------------
@@ -954,35 +995,36 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   if (int rc = down_type(expert_size, &q6)) return rc;
   if (!aligned(d_blob, 4) || !aligned(d_x, 16))
     return fail(FDM_E_INVAL, "blob must be 4-byte and x 16-byte aligned");
+  if (d_act && !aligned(d_act, 4)) return fail(FDM_E_INVAL, "act must be 4-byte aligned");
   hipStream_t s = as_stream(stream);
-  // the expert runs as the "shared" slot of a zero-routed-expert table
-  SlotTable t;
-  t.experts = nullptr;
-  t.expert_size = expert_size;
-  t.n_experts = 0;
-  t.shared = static_cast<const uint8_t*>(d_blob);
-  t.idx = nullptr;
-  t.w = nullptr;
-  t.K = 0;
-  t.n_slots = 1;
-  t.rel = false;  // the caller's blob: packed layout
-  Workspace* w = nullptr;
-  if (int rc = stream_workspace(s, &w)) return rc;
-  {
-    ProfScope p(FDM_PROF_XDIGITS, s);
-    FDM_HIP(launch_xdigits(d_x, FDM_HIDDEN / 64, w->xd, s));
-  }
+  // one launch of the layer kernel's work list without router or route:
+  // the expert runs as the shared slot of a zero-routed-expert layer, read
+  // from the caller's packed blob
+  Workspace* ws = nullptr;
+  if (int rc = stream_workspace(s, &ws)) return rc;
+  LayerArgs a;
+  a.Wg = nullptr;
+  a.bias = nullptr;
+  a.h = d_x;
+  a.h_in = nullptr;
+  a.out = d_out;
+  a.moe_out = nullptr;
+  a.experts = nullptr;
+  a.expert_size = expert_size;
+  a.n_experts = 0;
+  a.shared = static_cast<const uint8_t*>(d_blob);
+  a.down_q6 = q6 ? 1 : 0;
+  a.K = 0;
+  a.n_slots = 1;
+  a.idx = ws->idx;
+  a.w = ws->w;
+  layer_workspace_args(a, ws);
+  a.expert_only = 1;
+  a.act_out = d_act;
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_gateup(t, w->xd, w->act, w->act_xd, w->gu_count, s));
+    FDM_HIP(launch_layer(a, s));
   }
-  {
-    ProfScope p(FDM_PROF_DOWN, s);
-    FDM_HIP(launch_down_combine(t, q6, w->act_xd, nullptr, d_out, nullptr, w->eo, w->dn_count, s));
-  }
-  if (d_act)
-    FDM_HIP(hipMemcpyAsync(d_act, w->act, FDM_MOE_FFN * sizeof(float),
-                           hipMemcpyDeviceToDevice, s));
   return FDM_OK;
 }
 
@@ -1284,19 +1326,7 @@ int run_layer(int L, const float* h, const float* norm_w, float* h_post_out, con
   if (int rc = stream_workspace(s, &ws)) return rc;
   a.idx = idx ? idx : ws->idx;
   a.w = w ? w : ws->w;
-  a.xd = ws->xd;
-  uint64_t* tg = ws->layer_tagged;
-  a.scores = tg;
-  a.prov = tg + 256;
-  a.route_w = tg + 256 + 16;
-  a.route_perm = tg + 256 + 32;
-  a.act = tg + 256 + 48;
-  a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
-  a.norm_inv = tg + kLayerTagged - 16;  // its own 128-byte line
-  a.counters = ws->layer_cnt;
-  a.flags = ws->layer_flags;
-  a.epoch = ws->epochs.next();
-  a.spin_limit = g_layer_spin_limit;
+  layer_workspace_args(a, ws);
   {
     ProfScope p(FDM_PROF_LAYER, s);
     FDM_HIP(launch_layer(a, s));

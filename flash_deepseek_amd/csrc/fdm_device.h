@@ -334,6 +334,59 @@ __device__ __forceinline__ float q4k_group_dot_ld(const Q4KGroupLoad& r, const Q
   return q4k_group_dot(q4k_quad_hdr(r), r.q0, r.q1, sel, x);
 }
 
+// R rows' groups (the same group position g in every row) against ONE
+// digit record in LDS: each quarter of the record (12 registers of digits)
+// is read once and applied to all R rows, so a lane's LDS traffic is one
+// record instead of R.  Sub-block by sub-block (low nibbles, then high), so
+// only one sub-block's int32 sums are live.  out[r] = the group's dot of row r,
+// the same arithmetic as q4k_group_dot.
+template <int R>
+__device__ __forceinline__ void q4k_group_dot_rows(const Q4KGroupLoad (&ld)[R], const Q4KScaleSel& sel,
+                                                   const XGroup* __restrict__ xg, float (&out)[R]) {
+  const i32x4* av = reinterpret_cast<const i32x4*>(xg->a);
+  const i32x4* bv = reinterpret_cast<const i32x4*>(xg->b);
+  const i32x4* cv = reinterpret_cast<const i32x4*>(xg->c);
+  float f0[R];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+    int A[R], B[R], C[R];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const i32x4 a = av[2 * n + h], b = bv[2 * n + h], c = cv[2 * n + h];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const u32x4 q = h ? ld[r].q1 : ld[r].q0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t v = n ? (q[i] >> 4) & 0x0F0F0F0Fu : q[i] & 0x0F0F0F0Fu;
+          const bool first = h == 0 && i == 0;
+          A[r] = sdot4(v, (uint32_t)a[i], first ? 0 : A[r]);
+          B[r] = sdot4(v, (uint32_t)b[i], first ? 0 : B[r]);
+          C[r] = sdot4(v, (uint32_t)c[i], first ? 0 : C[r]);
+        }
+      }
+    }
+    const f32x4 meta = *reinterpret_cast<const f32x4*>(xg->s);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float f = (n ? meta.y : meta.x) * digit_fold(A[r], B[r], C[r]);
+      if (n == 0) {
+        f0[r] = f;
+      } else {
+        const u32x4 hdr = q4k_quad_hdr(ld[r]);
+        int sc0, m0, sc1, m1;
+        q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, sel, sc0, m0, sc1, m1);
+        const float d = half_to_float(hdr.x);
+        const float dmin = half_to_float(hdr.x >> 16);
+        const float qx = fmaf((float)sc0, f0[r], (float)sc1 * f);
+        const float mx = fmaf((float)m0, meta.z, (float)m1 * meta.w);
+        out[r] = fmaf(d, qx, -dmin * mx);
+      }
+    }
+  }
+}
+
+
 // ---- the resident expert layout (REL) ---------------------------------------------------
 // Experts of a resident layer are stored with each Q4_K matrix permuted so
 // that every load instruction of the dot4 kernels reads whole contiguous
@@ -514,6 +567,13 @@ __device__ __forceinline__ void reset_agent(int* counter) {
   __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+__device__ __forceinline__ unsigned load_u32_agent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_u32_agent(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.0f + expf(-g)) * u; }
 
 // Reduction of v over each half-wave (lanes 0-31 and 32-63) by DPP: row
@@ -573,6 +633,32 @@ __device__ __forceinline__ void make_digits3(float v, int8_t& a_out, int8_t& b_o
   c_out = (int8_t)c;
   s_out = s;
   sum_out = sum;
+}
+
+// The digit record of one 64-element group, by the whole wave (lane l holds
+// element l), published for other workgroups: agent-scope dword stores (four
+// lanes' digits packed per dword), followed by the caller's wait for the
+// stores and its flag.
+__device__ __forceinline__ void publish_digit_group(float v, XGroup* xg) {
+  const int lane = threadIdx.x & 63;
+  int8_t da, db, dc;
+  float ds, dsum;
+  make_digits3(v, da, db, dc, ds, dsum);
+  const int l = lane & 31, sub = lane >> 5;
+  auto pack4 = [](int8_t d) {
+    const unsigned u = (uint8_t)d;
+    return u | (__shfl_down(u, 1, 32) << 8) | (__shfl_down(u, 2, 32) << 16) | (__shfl_down(u, 3, 32) << 24);
+  };
+  const unsigned wa = pack4(da), wb = pack4(db), wc = pack4(dc);
+  if ((l & 3) == 0) {
+    store_u32_agent(reinterpret_cast<unsigned*>(xg->a) + 8 * sub + l / 4, wa);
+    store_u32_agent(reinterpret_cast<unsigned*>(xg->b) + 8 * sub + l / 4, wb);
+    store_u32_agent(reinterpret_cast<unsigned*>(xg->c) + 8 * sub + l / 4, wc);
+  }
+  if (l == 0) {
+    store_agent(&xg->s[sub], ds);
+    store_agent(&xg->xsum[sub], dsum);
+  }
 }
 
 }  // namespace fdm

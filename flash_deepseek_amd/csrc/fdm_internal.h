@@ -34,6 +34,22 @@ hipError_t launch_matvec_q4k(const uint8_t* W, const XGroup* xd, float* y, int r
                              int in_dim, hipStream_t s);
 hipError_t launch_matvec_q6k(const uint8_t* W, const XGroup* xd, float* y, int rows,
                              int in_dim, hipStream_t s);
+// One launch: the digits of x, then the rows (work list, see matvec_kernels.hip).
+struct MatvecArgs {
+  const uint8_t* W;   // Q4_K or Q6_K rows, packed
+  const float* x;     // [in_dim]
+  float* y;           // [rows]
+  int rows, gr;       // output rows, 64-element groups per row (in_dim / 64)
+  XGroup* xd;         // workspace: the digit records of x [gr]
+  int* counter;       // arrivals of the digit items (zero at first use, left zero)
+  unsigned* flag;     // set to epoch by the last digit item
+  unsigned* err;      // receives epoch when a wait gives up
+  unsigned epoch, spin_limit;
+};
+// false when this in_dim has no one-launch kernel (the caller then runs
+// launch_xdigits + launch_matvec_q4k / q6k)
+bool matvec1_supported(bool q6, int in_dim);
+hipError_t launch_matvec1(const MatvecArgs& a, bool q6, hipStream_t s);
 
 // router_kernels.hip
 hipError_t launch_router_logits(const float* Wg, const float* x, int n_exp, int dim, int T,
@@ -110,6 +126,8 @@ struct LayerArgs {
   unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
   unsigned epoch;          // non-zero, different from every earlier call's
   unsigned spin_limit;     // polls before a wait gives up (kLayerSpinLimit)
+  int expert_only = 0;     // one expert from the packed blob `shared` (K = 0, no router)
+  float* act_out = nullptr;  // expert_only: receives the SwiGLU activations [2048] (or null)
 };
 constexpr unsigned kLayerSpinLimit = 1u << 17;  // polls of one wait (each >= ~1 us)
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);

@@ -101,13 +101,6 @@ constexpr int kFlagXd = 0;
 constexpr int kFlagErr = kLayerFlagErr;
 constexpr int kCntXd = 0;
 
-__device__ __forceinline__ unsigned load_u32_agent(const unsigned* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_u32_agent(unsigned* p, unsigned v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // ---- tagged words ------------------------------------------------------------------
 __device__ __forceinline__ void put_tagged(uint64_t* p, unsigned epoch, uint32_t bits) {
   __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED,
@@ -254,25 +247,7 @@ __device__ __forceinline__ void xd_item(const LayerArgs& a, int i, LayerSmem& sm
     const float w = a.norm_w[64 * G + lane];
     v = (v * wait_inv(a, sm)) * w;
   }
-  int8_t da, db, dc;
-  float ds, dsum;
-  make_digits3(v, da, db, dc, ds, dsum);
-  const int l = lane & 31, sub = lane >> 5;
-  auto pack4 = [](int8_t d) {
-    const unsigned u = (uint8_t)d;
-    return u | (__shfl_down(u, 1, 32) << 8) | (__shfl_down(u, 2, 32) << 16) | (__shfl_down(u, 3, 32) << 24);
-  };
-  const unsigned wa = pack4(da), wb = pack4(db), wc = pack4(dc);
-  XGroup* xg = a.xd + G;
-  if ((l & 3) == 0) {
-    store_u32_agent(reinterpret_cast<unsigned*>(xg->a) + 8 * sub + l / 4, wa);
-    store_u32_agent(reinterpret_cast<unsigned*>(xg->b) + 8 * sub + l / 4, wb);
-    store_u32_agent(reinterpret_cast<unsigned*>(xg->c) + 8 * sub + l / 4, wc);
-  }
-  if (l == 0) {
-    store_agent(&xg->s[sub], ds);
-    store_agent(&xg->xsum[sub], dsum);
-  }
+  publish_digit_group(v, a.xd + G);
   wait_stores_done();
   __syncthreads();
   if (threadIdx.x == 0) {
@@ -407,6 +382,7 @@ __device__ __forceinline__ void exact_item(const LayerArgs& a) {
 // 32-63 up, 16 lanes per row); SwiGLU in registers; the activations go out
 // tagged.  The route and the digits of h_post are waited for and staged
 // once per run, so their round trips are paid once for kGuPer tiles.
+template <bool PACKED>
 __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int tile0, bool routed,
                                            LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -445,10 +421,13 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
     const int row = (tile0 + t) * kGuTileRows + 2 * wave + (q & 1);
     Q4KGroupLoad ld[7];
     if (blob) {
-      // resident expert layout: each half-wave load reads one 512-byte run
+      // resident expert layout: each half-wave load reads one 512-byte run;
+      // packed layout (a caller's blob): 16-byte slices of the row's blocks
       const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
 #pragma unroll
-      for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
+      for (int i = 0; i < 7; ++i)
+        ld[i] = PACKED ? q4k_load_group(mat + (size_t)row * kQ4KRowHidden + (size_t)(4 * i + (l16 >> 2)) * kQ4KBlock, g)
+                       : rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     }
     if (t == 0) {
       if (!routed) {
@@ -467,8 +446,11 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
     }
     acc = sum16(acc);
     const float up = __shfl(acc, (lane + 32) & 63);
-    if (lane == 0 || lane == 16)
-      put_tagged(a.act + (size_t)slot * kFfn + row, a.epoch, __float_as_uint(silu_mul(acc, up)));
+    if (lane == 0 || lane == 16) {
+      const float av = silu_mul(acc, up);
+      put_tagged(a.act + (size_t)slot * kFfn + row, a.epoch, __float_as_uint(av));
+      if (PACKED && a.act_out) a.act_out[row] = av;
+    }
   }
 }
 
@@ -480,7 +462,7 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
 //  Q4_K: kDnLanesQ4 lanes per row (one 64-element group each), lane row
 //        group rr = lane / kDnLanesQ4, rows rr + 16 j (j < 7) at 8 parts.
 //  Q6_K: kDnLanesQ6 lanes per row (one 128-element half block each).
-template <bool Q6>
+template <bool Q6, bool PACKED>
 __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part, int item,
                                           bool routed, LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -516,22 +498,15 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
     if (blob) {
       // resident expert layout: a wave's load (4 rows x one block quad) reads one 1 KB run
 #pragma unroll
-      for (int j = 0; j < kDnRowsQ4L; ++j) ld[j] = rel_load_group<true>(dbase, row0 + RPW * j, blk, gl & 3);
+      for (int j = 0; j < kDnRowsQ4L; ++j)
+        ld[j] = PACKED ? q4k_load_group(dbase + (size_t)(row0 + RPW * j) * kQ4KRowFfn + (size_t)blk * kQ4KBlock, gl & 3)
+                       : rel_load_group<true>(dbase, row0 + RPW * j, blk, gl & 3);
     }
     stage_act();
     float acc[kDnRowsQ4L] = {};
-    if (blob) {
-      const Q4KScaleSel sel = q4k_scale_sel(gl & 3);
-#pragma unroll
-      for (int j = 0; j < kDnRowsQ4L; ++j) {
-        // re-read the digits per row: held across the seven rows they
-        // would take 52 more registers than the 128 of four waves per SIMD
-        int gi = gl;
-        __asm__ volatile("" : "+v"(gi));
-        acc[j] = q4k_group_dot_ld(ld[j], sel, &sm.xs[gi]);
-        __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
-      }
-    }
+    // the lane's seven rows share one digit record: each quarter of it is
+    // read from LDS once for all seven
+    if (blob) q4k_group_dot_rows<kDnRowsQ4L>(ld, q4k_scale_sel(gl & 3), &sm.xs[gl], acc);
 #pragma unroll
     for (int j = 0; j < kDnRowsQ4L; ++j) {
       float v = acc[j];
@@ -642,16 +617,19 @@ struct LayerList {
   int gup, dnp;  // gate/up and down items per (slot, part)
 };
 
-__host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6, bool norm) {
+// Expert-only lists (one expert, no router: K = 0, the expert in the shared
+// slot) have no router rows and no route items.
+__host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6, bool norm,
+                                                         bool expert = false) {
   const int hs = n_slots - K;  // 1 with a shared expert
   LayerList l;
   l.gup = kGuPerPart;
   l.dnp = dn_per_part(q6);
   l.xd = norm ? 1 : 0;  // item 0: the fused rms_norm
   l.router = l.xd + kXdItems;
-  l.route = l.router + kRows;
-  l.exact = l.route + 1;
-  l.shared = l.exact + 1;
+  l.route = l.router + (expert ? 0 : kRows);
+  l.exact = l.route + (expert ? 0 : 1);
+  l.shared = l.exact + (expert ? 0 : 1);
   l.routed = l.shared + hs * kParts * (l.gup + l.dnp);
   l.comb = l.routed + K * kParts * (l.gup + l.dnp);
   l.total = l.comb + kCombTiles;
@@ -691,34 +669,36 @@ __device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, 
 
 }  // namespace
 
-template <bool Q6>
+// EXPERT: one expert from a caller's packed blob (the shared slot, K = 0),
+// no router or route items.
+template <bool Q6, bool EXPERT>
 __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
-  const LayerList l = layer_list(a.K, a.n_slots, Q6, a.norm_w != nullptr);
+  const LayerList l = layer_list(a.K, a.n_slots, Q6, a.norm_w != nullptr, EXPERT);
   const int it = blockIdx.x;
   if (it < l.xd) {
     norm_item(a, sm);
   } else if (it < l.router) {
     xd_item(a, it - l.xd, sm);
-  } else if (it < l.route) {
+  } else if (!EXPERT && it < l.route) {
     router_row(a, it - l.router, sm);
-  } else if (it == l.route) {
+  } else if (!EXPERT && it == l.route) {
     route_item(a);
-  } else if (it == l.exact) {
+  } else if (!EXPERT && it == l.exact) {
     exact_item(a);
   } else if (it < l.routed) {
     const int off = it - l.shared;
     if (off < kParts * l.gup)
-      gateup_run(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, false, sm);
+      gateup_run<EXPERT>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, false, sm);
     else
-      down_part<Q6>(a, a.K, (off - kParts * l.gup) / l.dnp, (off - kParts * l.gup) % l.dnp, false, sm);
-  } else if (it < l.comb) {
+      down_part<Q6, EXPERT>(a, a.K, (off - kParts * l.gup) / l.dnp, (off - kParts * l.gup) % l.dnp, false, sm);
+  } else if (!EXPERT && it < l.comb) {
     bool dn;
     int slot, part, idx;
     routed_item(l, a.K, it - l.routed, dn, slot, part, idx);
     if (!dn)
-      gateup_run(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, true, sm);
+      gateup_run<false>(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, true, sm);
     else
-      down_part<Q6>(a, slot, part, idx, true, sm);
+      down_part<Q6, false>(a, slot, part, idx, true, sm);
   } else {
     combine_tile(a, it - l.comb, sm);
   }
@@ -729,20 +709,34 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_layer_q4k(
     LayerArgs a) {
   __shared__ LayerSmem sm;
-  layer_item<false>(a, sm);
+  layer_item<false, false>(a, sm);
 }
 
 __global__ __launch_bounds__(256) void k_layer_q6k(LayerArgs a) {
   __shared__ LayerSmem sm;
-  layer_item<true>(a, sm);
+  layer_item<true, false>(a, sm);
+}
+
+// One expert FFN (fdm_expert_ffn) in one launch: digits | gate/up items |
+// down parts | combine tiles, on the caller's packed blob.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_q4k(
+    LayerArgs a) {
+  __shared__ LayerSmem sm;
+  layer_item<false, true>(a, sm);
+}
+
+__global__ __launch_bounds__(256) void k_expert_q6k(LayerArgs a) {
+  __shared__ LayerSmem sm;
+  layer_item<true, true>(a, sm);
 }
 
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s) {
-  const LayerList l = layer_list(a.K, a.n_slots, a.down_q6 != 0, a.norm_w != nullptr);
+  const bool ex = a.expert_only != 0;
+  const LayerList l = layer_list(a.K, a.n_slots, a.down_q6 != 0, a.norm_w != nullptr, ex);
   if (a.down_q6)
-    hipLaunchKernelGGL(k_layer_q6k, dim3(l.total), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(ex ? k_expert_q6k : k_layer_q6k, dim3(l.total), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(k_layer_q4k, dim3(l.total), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(ex ? k_expert_q4k : k_layer_q4k, dim3(l.total), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

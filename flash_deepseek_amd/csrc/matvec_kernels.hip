@@ -180,4 +180,148 @@ hipError_t launch_matvec_q6k(const uint8_t* W, const XGroup* xd, float* y, int r
   return hipGetLastError();
 }
 
+// ---- one launch: the digits of x, then the rows ---------------------------------------
+// Work list of 128-thread workgroups: [digit items: two 64-element groups
+// each, one per wave] [row items: 8 rows each, 16 lanes per row].  A row
+// item requests its weights first, then waits for the digit flag (set by
+// the last digit item to arrive), stages the records with coherent 16-byte
+// loads and finishes; the digits' latency hides behind the weight loads and
+// no second launch is paid.  Digit items never wait, so the grid drains
+// whatever the dispatch order; the flag wait is bounded as well (a wait that
+// gives up records the epoch in the error flag, which fdm_stream_sync reports).
+
+__device__ __forceinline__ int mv_digit_items(int gr) { return (gr + 1) / 2; }
+
+__device__ __forceinline__ void mv_digit_item(const MatvecArgs& a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int G = 2 * blockIdx.x + wave;
+  if (G < a.gr) publish_digit_group(a.x[64 * G + lane], a.xd + G);
+  wait_stores_done();
+  __syncthreads();
+  if (threadIdx.x == 0 && arrive_agent(a.counter) == mv_digit_items(a.gr) - 1) {
+    reset_agent(a.counter);
+    store_u32_agent(a.flag, a.epoch);
+  }
+}
+
+// Thread 0 polls the digit flag; every thread returns after it is set (or
+// after the bounded wait gave up).
+__device__ __forceinline__ void mv_wait_digits(const MatvecArgs& a) {
+  if (threadIdx.x == 0) {
+    for (unsigned n = 0; load_u32_agent(a.flag) != a.epoch; ++n) {
+      if (n >= a.spin_limit || ((n & 63) == 63 && load_u32_agent(a.err) == a.epoch)) {
+        store_u32_agent(a.err, a.epoch);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+}
+
+// The first n records of a.xd into LDS: every 16-byte load (coherent, sc1)
+// is issued before the first store.
+template <int N>
+__device__ __forceinline__ void mv_stage(const MatvecArgs& a, XGroup* xs) {
+  constexpr int kVec = N * (int)sizeof(XGroup) / 16;
+  constexpr int kPer = (kVec + 127) / 128;
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.xd, 0, N * (int)sizeof(XGroup), 0x00020000);
+  u32x4 v[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, (threadIdx.x + 128 * k) * 16, 0, 16);
+#pragma unroll
+  for (int k = 0; k < kPer; ++k)
+    if (threadIdx.x + 128 * k < kVec) reinterpret_cast<u32x4*>(xs)[threadIdx.x + 128 * k] = v[k];
+  __syncthreads();
+}
+
+// Q4_K, in_dim = 1024 GPL: lane l16 of a row takes groups l16 + 16 t.
+template <int GPL>
+__global__ __launch_bounds__(128) void k_matvec1_q4k(MatvecArgs a) {
+  __shared__ XGroup xs[16 * GPL];
+  const int nd = mv_digit_items(a.gr);
+  if ((int)blockIdx.x < nd) {
+    mv_digit_item(a);
+    return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = 8 * ((int)blockIdx.x - nd) + 4 * wave + (lane >> 4);
+  const int l16 = lane & 15, g = l16 & 3;
+  const uint8_t* rp = a.W + (size_t)min(row, a.rows - 1) * (size_t)(a.gr / 4) * kQ4KBlock;
+  Q4KGroupLoad ld[GPL];
+#pragma unroll
+  for (int t = 0; t < GPL; ++t) ld[t] = q4k_load_group(rp + (size_t)(4 * t + (l16 >> 2)) * kQ4KBlock, g);
+  mv_wait_digits(a);
+  mv_stage<16 * GPL>(a, xs);
+  const Q4KScaleSel sel = q4k_scale_sel(g);
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < GPL; ++t) {
+    acc += q4k_group_dot_ld(ld[t], sel, &xs[16 * t + l16]);
+    __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
+  }
+  acc = sum16(acc);
+  if (row < a.rows && l16 == 0) a.y[row] = acc;
+}
+
+// Q6_K, in_dim = 2048 HPL: lane l16 of a row takes 128-element halves l16 + 16 t.
+template <int HPL>
+__global__ __launch_bounds__(128) void k_matvec1_q6k(MatvecArgs a) {
+  __shared__ XGroup xs[32 * HPL];
+  const int nd = mv_digit_items(a.gr);
+  if ((int)blockIdx.x < nd) {
+    mv_digit_item(a);
+    return;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = 8 * ((int)blockIdx.x - nd) + 4 * wave + (lane >> 4);
+  const int l16 = lane & 15;
+  const uint8_t* rp = a.W + (size_t)min(row, a.rows - 1) * (size_t)(a.gr / 4) * kQ6KBlock;
+  Q6KHalfLoad l6[HPL];
+#pragma unroll
+  for (int t = 0; t < HPL; ++t) {
+    const int hb = 16 * t + l16;
+    l6[t] = q6k_load_half(rp + (size_t)(hb >> 1) * kQ6KBlock, hb & 1);
+  }
+  mv_wait_digits(a);
+  mv_stage<32 * HPL>(a, xs);
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < HPL; ++t) {
+    acc += q6k_half_dot_ld(l6[t], &xs[2 * (16 * t + l16)]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  acc = sum16(acc);
+  if (row < a.rows && l16 == 0) a.y[row] = acc;
+}
+
+bool matvec1_supported(bool q6, int in_dim) {
+  if (q6) return in_dim % 2048 == 0 && in_dim / 2048 >= 1 && in_dim / 2048 <= 3;
+  return in_dim % 1024 == 0 && in_dim / 1024 >= 1 && in_dim / 1024 <= 7;
+}
+
+hipError_t launch_matvec1(const MatvecArgs& a, bool q6, hipStream_t s) {
+  const int in_dim = a.gr * 64;
+  const dim3 grid((unsigned)((a.gr + 1) / 2 + (a.rows + 7) / 8)), block(128);
+  if (q6) {
+    switch (in_dim / 2048) {
+      case 1: hipLaunchKernelGGL(k_matvec1_q6k<1>, grid, block, 0, s, a); break;
+      case 2: hipLaunchKernelGGL(k_matvec1_q6k<2>, grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL(k_matvec1_q6k<3>, grid, block, 0, s, a); break;
+    }
+  } else {
+    switch (in_dim / 1024) {
+      case 1: hipLaunchKernelGGL(k_matvec1_q4k<1>, grid, block, 0, s, a); break;
+      case 2: hipLaunchKernelGGL(k_matvec1_q4k<2>, grid, block, 0, s, a); break;
+      case 3: hipLaunchKernelGGL(k_matvec1_q4k<3>, grid, block, 0, s, a); break;
+      case 4: hipLaunchKernelGGL(k_matvec1_q4k<4>, grid, block, 0, s, a); break;
+      case 5: hipLaunchKernelGGL(k_matvec1_q4k<5>, grid, block, 0, s, a); break;
+      case 6: hipLaunchKernelGGL(k_matvec1_q4k<6>, grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL(k_matvec1_q4k<7>, grid, block, 0, s, a); break;
+    }
+  }
+  return hipGetLastError();
+}
+
 }  // namespace fdm
