@@ -87,42 +87,77 @@ struct Records {
 }  // namespace
 
 // ---- dispatch -------------------------------------------------------------------------
-// One workgroup.  Counts pairs per expert (LDS atomics), the segment starts
-// (exclusive scan), the ascending list of distinct experts, and each pair's
-// position in its expert's segment.  The order of pairs inside a segment
-// does not affect any result: every pair's activations and output are
-// computed from its own token only.
+// Exclusive prefix sum of v over the 256 threads of the workgroup; tot
+// receives the total in every thread.
+__device__ __forceinline__ int block_scan_excl(int v, int* wsum, int& tot) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  int base = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) base += w < wave ? wsum[w] : 0;
+  tot = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+  __syncthreads();  // wsum may be reused
+  return base + x - v;
+}
+
+// One workgroup, thread e = expert e: pair counts per expert, segment
+// starts, the ascending list of distinct experts, each pair's position in
+// its expert's segment and, with b.ch > 0, the grouped GEMMs' chunk list
+// (every distinct expert's segment in chunks of b.ch pairs, ascending, then
+// the shared expert's tokens in chunks of b.ch), all by block-wide scans.
+// The order of pairs inside a segment (LDS atomics) does not affect any
+// result: every pair's activations and output come from its own token only.
 __global__ __launch_bounds__(256) void k_dispatch(BatchArgs b) {
   __shared__ int cnt[kExperts];
   __shared__ int fill[kExperts];
-  __shared__ int start[kExperts + 1];
+  __shared__ int start[kExperts];
+  __shared__ int wsum[4];
   const int P = b.T * b.K;
-  cnt[threadIdx.x] = 0;
-  fill[threadIdx.x] = 0;
+  const int e = threadIdx.x;
+  cnt[e] = 0;
+  fill[e] = 0;
   __syncthreads();
   for (int p = threadIdx.x; p < P; p += 256) {
-    const int e = b.idx[p];
-    if (e >= 0 && e < kExperts) atomicAdd(&cnt[e], 1);
+    const int x = b.idx[p];
+    if (x >= 0 && x < kExperts) atomicAdd(&cnt[x], 1);
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int s = 0, d = 0;
-    for (int e = 0; e < kExperts; ++e) {
-      start[e] = s;
-      s += cnt[e];
-      if (cnt[e]) b.distinct[d++] = e;
-    }
-    start[kExperts] = s;
-    *b.n_distinct = d;
+  const int c = cnt[e];
+  int tot, nd;
+  const int st = block_scan_excl(c, wsum, tot);
+  const int dpos = block_scan_excl(c > 0 ? 1 : 0, wsum, nd);
+  start[e] = st;
+  b.seg_start[e] = st;
+  if (c > 0) b.distinct[dpos] = e;
+  if (e == 0) {
+    b.seg_start[kExperts] = tot;
+    *b.n_distinct = nd;
+  }
+  if (b.ch > 0) {
+    const int ch = b.ch;
+    const int nch = (c + ch - 1) / ch;
+    int nr;
+    const int cpos = block_scan_excl(nch, wsum, nr);
+    for (int q = 0; q < nch; ++q)
+      b.chunks[cpos + q] = make_int4(e, st + q * ch, min(ch, c - q * ch), cpos | (nch << 16));
+    const int ns = b.shared ? (b.T + ch - 1) / ch : 0;
+    for (int q = threadIdx.x; q < ns; q += 256)
+      b.chunks[nr + q] = make_int4(-1, q * ch, min(ch, b.T - q * ch), nr | (ns << 16));
+    if (e == 0) *b.n_chunks = nr + ns;
   }
   __syncthreads();
-  b.seg_start[threadIdx.x] = start[threadIdx.x];
-  if (threadIdx.x == 0) b.seg_start[kExperts] = start[kExperts];
   for (int p = threadIdx.x; p < P; p += 256) {
-    const int e = b.idx[p];
+    const int x = b.idx[p];
     int pos = -1;
-    if (e >= 0 && e < kExperts) {
-      pos = start[e] + atomicAdd(&fill[e], 1);
+    if (x >= 0 && x < kExperts) {
+      pos = start[x] + atomicAdd(&fill[x], 1);
       b.pair_tok[pos] = p / b.K;
     }
     b.pair_of[p] = pos;  // -1: invalid expert id, contributes 0

@@ -1435,15 +1435,18 @@ QScratch workspace_q(const Workspace& w) {
 // chunk list, planes of the token rows, gate/up + SwiGLU into b.act, then
 // a Q4_K down on the GEMM (planes of b.act first) or a Q6_K down on the
 // dot4 kernels, into b.eo.  x: the fp32 token rows [T][7168].
-int run_qgemm_experts(const Layer* y, const BatchArgs& b, const float* x, int planes, const QScratch& w,
+int run_qgemm_experts(const Layer* y, const BatchArgs& b0, const float* x, int planes, const QScratch& w,
                       hipStream_t s) {
+  BatchArgs b = b0;
   const int T = b.T, K = b.K;
   const size_t rows = (size_t)T * K + (y->shared ? T : 0);
   const int ch = qgemm_chunk_tokens(planes);
   const int mc = max_chunks(T, K, ch);
   if (mc > kQMaxChunks) return fail(FDM_E_INVAL, "chunk list of %d entries exceeds %d", mc, kQMaxChunks);
-  FDM_HIP(launch_qchunks(b.seg_start, b.distinct, b.n_distinct, T, y->shared != nullptr, ch, w.chunks,
-                         w.n_chunks, s));
+  b.ch = ch;
+  b.chunks = w.chunks;
+  b.n_chunks = w.n_chunks;
+  FDM_HIP(launch_dispatch(b, s));  // with the chunk list
   FDM_HIP(launch_xplanes(x, FDM_HIDDEN, (size_t)T, planes, w.planes, w.xs, w.xe, s));
   QGemmArgs q;
   q.T = T;
@@ -1528,7 +1531,6 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     b.pair_of = w.b_pair_of;
     b.distinct = w.b_distinct;
     b.n_distinct = w.b_ndistinct;
-    FDM_HIP(launch_dispatch(b, s));
     // prefill precision: one fp16 plane of the activations (the bar is 1e-2)
     if (int rc = run_qgemm_experts(y, b, w.p_hpost, 1, workspace_q(w), s)) return rc;
     FDM_HIP(launch_combine(b, s));
@@ -1595,7 +1597,6 @@ int batched_step(const Layer* y, const float* d_X, const float* d_H_in, int T, i
     return FDM_OK;
   }
   // grouped MFMA GEMMs at fp32 grade (three fp16 planes of the activations)
-  FDM_HIP(launch_dispatch(b, s));
   if (int rc = run_qgemm_experts(y, b, d_X, 3, sc.q, s)) return rc;
   FDM_HIP(launch_combine(b, s));
   return FDM_OK;

@@ -155,6 +155,10 @@ struct BatchArgs {
   int* pair_of;            // workspace: [T*K] position of pair (t, k), -1 if invalid id
   int* distinct;           // workspace: [256] distinct experts, ascending
   int* n_distinct;         // out: number of distinct experts (device int)
+  // optional: the dispatch also writes the grouped GEMMs' chunk list (ch > 0)
+  int ch = 0;              // tokens per chunk
+  int4* chunks = nullptr;  // {expert or -1 (shared), first pair / token, count, first chunk | count << 16}
+  int* n_chunks = nullptr;
 };
 hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t s);
 // The grouped down (digits of b.act, then the dot4 down kernel) on its own.
@@ -187,9 +191,6 @@ struct QGemmArgs {
 // sub-block sums and 2^-s per row.
 hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
                           hipStream_t s);
-// The chunk list of one step from the dispatch (chunks of `ch` tokens).
-hipError_t launch_qchunks(const int* seg_start, const int* distinct, const int* n_distinct, int T, bool with_shared,
-                          int ch, int4* chunks, int* n_chunks, hipStream_t s);
 int qgemm_chunk_tokens(int planes);
 constexpr int kQMaxChunks = 1024;  // >= 256 + 512 * 16 / 16 + 512 / 16
 // Q4_K gate/up + SwiGLU (down = false) or Q4_K down (down = true) over the

@@ -210,29 +210,6 @@ __global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, in
   }
 }
 
-// ---- the chunk list -------------------------------------------------------------------
-// One thread: every distinct routed expert's pair segment in chunks of `ch`
-// pairs, then the shared expert's tokens in chunks of `ch`.  Entry:
-// {expert (-1: shared), first pair position (or token), count, group}, where
-// group = first chunk of the expert | (the expert's chunk count << 16).
-__global__ void k_qchunks(const int* __restrict__ seg_start, const int* __restrict__ distinct,
-                          const int* __restrict__ n_distinct, int T, int with_shared, int ch,
-                          int4* __restrict__ chunks, int* __restrict__ n_chunks) {
-  if (threadIdx.x != 0) return;
-  int n = 0;
-  auto group = [&](int e, int a, int b) {
-    const int first = n, cnt = (b - a + ch - 1) / ch;
-    for (int f = a; f < b; f += ch) chunks[n++] = make_int4(e, f, min(ch, b - f), first | (cnt << 16));
-  };
-  const int D = *n_distinct;
-  for (int d = 0; d < D; ++d) {
-    const int e = distinct[d];
-    group(e, seg_start[e], seg_start[e + 1]);
-  }
-  if (with_shared) group(-1, 0, T);
-  *n_chunks = n;
-}
-
 // ---- the grouped GEMM ------------------------------------------------------------------
 template <int P, int NB, bool DOWN>
 __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int* rows, int chunk, int rg) {
@@ -436,13 +413,6 @@ hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Fl
     hipLaunchKernelGGL(k_xplanes<3>, dim3((unsigned)n_rows), dim3(256), 0, s, x, kd, n_rows, xp, xs, xe);
   else
     hipLaunchKernelGGL(k_xplanes<1>, dim3((unsigned)n_rows), dim3(256), 0, s, x, kd, n_rows, xp, xs, xe);
-  return hipGetLastError();
-}
-
-hipError_t launch_qchunks(const int* seg_start, const int* distinct, const int* n_distinct, int T, bool with_shared,
-                          int ch, int4* chunks, int* n_chunks, hipStream_t s) {
-  hipLaunchKernelGGL(k_qchunks, dim3(1), dim3(64), 0, s, seg_start, distinct, n_distinct, T, with_shared ? 1 : 0,
-                     ch, chunks, n_chunks);
   return hipGetLastError();
 }
 
