@@ -109,7 +109,10 @@ int fdm_dequant_q6k(const void *d_src, float *d_dst, size_t n, void *stream);
  * dequant_matvec_q4k / dequant_matvec_q6k kernels (infer.m:1525-1540,
  * shaders.metal:43-179).  y[r] = sum_c deq(W[r,c]) * x[c]; W is out_dim rows
  * of in_dim/256 blocks; in_dim must be a multiple of 256 and at most
- * FDM_HIDDEN * 4. */
+ * FDM_HIDDEN * 4.  One launch (the digits of x and the rows) when in_dim is
+ * 1024 n <= 7168 (Q4_K) or 2048 n <= 6144 (Q6_K), two otherwise; a bounded
+ * wait inside the one-launch kernel that gives up is reported by
+ * fdm_stream_sync (FDM_E_STATE). */
 int fdm_matvec_q4k(const void *d_W, const float *d_x, float *d_y, uint32_t out_dim,
                    uint32_t in_dim, void *stream);
 int fdm_matvec_q6k(const void *d_W, const float *d_x, float *d_y, uint32_t out_dim,
@@ -118,7 +121,9 @@ int fdm_matvec_q6k(const void *d_W, const float *d_x, float *d_y, uint32_t out_d
 /* ---- one SwiGLU expert: replaces encode_expert (infer.m:1559-1575), i.e.
  * gate and up matvecs, swiglu_fused (shaders.metal:210-220) and the down
  * matvec.  expert_size selects the down type exactly as infer.m:1810-1821.
- * d_act (optional, 2048 floats) receives silu(gate) * up. */
+ * d_act (optional, 2048 floats) receives silu(gate) * up.  One launch (the
+ * batch-1 layer kernel's work list without router; waits reported as for
+ * fdm_moe_layer). */
 int fdm_expert_ffn(const void *d_blob, size_t expert_size, const float *d_x, float *d_out,
                    float *d_act, void *stream);
 
@@ -434,7 +439,7 @@ int fdm_dense_ffn(int L, const float *d_h_post, const float *d_h_in, float *d_hi
  * the recorded events and returns the count, total, min and max duration
  * (milliseconds) of one phase since the last reset. */
 #define FDM_PROF_ROUTER 0   /* fdm_router_logits / fdm_route kernels    */
-#define FDM_PROF_GATEUP 1   /* gate/up matvecs + SwiGLU (routing given) */
+#define FDM_PROF_GATEUP 1   /* gate/up matvecs + SwiGLU (routing given); fdm_expert_ffn */
 #define FDM_PROF_DOWN 2     /* down matvecs + combine (routing given)   */
 #define FDM_PROF_XDIGITS 3  /* activation digits (routing given)        */
 #define FDM_PROF_MATVEC 4   /* fdm_matvec_q4k / _q6k kernel             */
