@@ -939,6 +939,22 @@ int run_matvec(bool q6, const void* d_W, const float* d_x, float* d_y, uint32_t 
   Workspace* w = nullptr;
   if (int rc = stream_workspace(s, &w)) return rc;
   const uint8_t* W = static_cast<const uint8_t*>(d_W);
+  // the layer kernel's tagged expert-output words hold the partial sums
+  const size_t part_words = (size_t)kLayerMaxSlots * kLayerMaxParts * FDM_HIDDEN;
+  if (!q6 && matvec2_supported((int)in_dim, (int)out_dim, part_words)) {
+    Matvec2Args a;
+    a.W = W;
+    a.x = d_x;
+    a.y = d_y;
+    a.rows = (int)out_dim;
+    a.part = w->layer_tagged + 256 + 48 + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
+    a.err = w->layer_flags + kLayerFlagErr * kLayerStride;
+    a.epoch = w->epochs.next();
+    a.spin_limit = g_layer_spin_limit;
+    ProfScope p(FDM_PROF_MATVEC, s);
+    FDM_HIP(launch_matvec2_q4k(a, (int)in_dim, s));
+    return FDM_OK;
+  }
   if (matvec1_supported(q6, (int)in_dim)) {
     MatvecArgs a;
     a.W = W;

@@ -661,4 +661,38 @@ __device__ __forceinline__ void publish_digit_group(float v, XGroup* xg) {
   }
 }
 
+// ---- tagged words -------------------------------------------------------------------------
+// {epoch, payload} in one 64-bit word written by one agent-scope store: a
+// reader's load is its own readiness check (tag == this call's epoch) and
+// nothing is ever cleared.
+__device__ __forceinline__ void put_tagged(uint64_t* p, unsigned epoch, uint32_t bits) {
+  __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get_tagged(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool tag_is(uint64_t v, unsigned epoch) {
+  return (unsigned)(v >> 32) == epoch;
+}
+__device__ __forceinline__ float tagged_f(uint64_t v) { return __uint_as_float((uint32_t)v); }
+__device__ __forceinline__ int tagged_i(uint64_t v) { return (int)(uint32_t)v; }
+
+
+// Digits of the 64 elements held by one wave (lane l: element l) into LDS
+// record g (two sub-blocks of 32, one per half-wave).
+__device__ __forceinline__ void digits_to_lds(float v, XGroup& g) {
+  const int lane = threadIdx.x & 63;
+  int8_t da, db, dc;
+  float ds, dsum;
+  make_digits3(v, da, db, dc, ds, dsum);
+  g.a[lane] = da;
+  g.b[lane] = db;
+  g.c[lane] = dc;
+  if ((lane & 31) == 0) {
+    g.s[lane >> 5] = ds;
+    g.xsum[lane >> 5] = dsum;
+  }
+}
+
 }  // namespace fdm

@@ -48,6 +48,19 @@ struct MatvecArgs {
 };
 // false when this in_dim has no one-launch kernel (the caller then runs
 // launch_xdigits + launch_matvec_q4k / q6k)
+// Q4_K by column parts of 1024 (see matvec_kernels.hip): in_dim = 1024 P,
+// P <= 7; part holds (P - 1) x rows tagged partial sums.
+struct Matvec2Args {
+  const uint8_t* W;
+  const float* x;
+  float* y;
+  int rows;
+  uint64_t* part;   // workspace: tagged partial sums [P - 1][rows]
+  unsigned* err;    // receives epoch when a wait gives up
+  unsigned epoch, spin_limit;
+};
+bool matvec2_supported(int in_dim, int rows, size_t part_words);
+hipError_t launch_matvec2_q4k(const Matvec2Args& a, int in_dim, hipStream_t s);
 bool matvec1_supported(bool q6, int in_dim);
 hipError_t launch_matvec1(const MatvecArgs& a, bool q6, hipStream_t s);
 

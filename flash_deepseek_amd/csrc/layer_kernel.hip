@@ -101,20 +101,6 @@ constexpr int kFlagXd = 0;
 constexpr int kFlagErr = kLayerFlagErr;
 constexpr int kCntXd = 0;
 
-// ---- tagged words ------------------------------------------------------------------
-__device__ __forceinline__ void put_tagged(uint64_t* p, unsigned epoch, uint32_t bits) {
-  __hip_atomic_store(p, ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t get_tagged(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ bool tag_is(uint64_t v, unsigned epoch) {
-  return (unsigned)(v >> 32) == epoch;
-}
-__device__ __forceinline__ float tagged_f(uint64_t v) { return __uint_as_float((uint32_t)v); }
-__device__ __forceinline__ int tagged_i(uint64_t v) { return (int)(uint32_t)v; }
-
 struct LayerSmem {
   union {
     XGroup xs[kHidden / 64];  // digits of h_post (gate/up) or of a part's activations (down)
@@ -171,21 +157,6 @@ __device__ __forceinline__ void wait_route_xd(const LayerArgs& a, int slot, bool
   });
 }
 
-// Digits of the 64 elements held by one wave (lane l: element l) into LDS
-// record g (two sub-blocks of 32, one per half-wave).
-__device__ __forceinline__ void digits_to_lds(float v, XGroup& g) {
-  const int lane = threadIdx.x & 63;
-  int8_t da, db, dc;
-  float ds, dsum;
-  make_digits3(v, da, db, dc, ds, dsum);
-  g.a[lane] = da;
-  g.b[lane] = db;
-  g.c[lane] = dc;
-  if ((lane & 31) == 0) {
-    g.s[lane >> 5] = ds;
-    g.xsum[lane >> 5] = dsum;
-  }
-}
 
 // ---- the fused rms_norm --------------------------------------------------------------
 // The first item of the list computes 1 / sqrt(sum h^2 / 7168 + 1e-6) of the

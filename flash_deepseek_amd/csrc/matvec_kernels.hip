@@ -180,7 +180,7 @@ hipError_t launch_matvec_q6k(const uint8_t* W, const XGroup* xd, float* y, int r
   return hipGetLastError();
 }
 
-// ---- one launch: the digits of x, then the rows ---------------------------------------
+// ---- one launch (Q6_K): the digits of x, then the rows -------------------------------
 // Work list of 128-thread workgroups: [digit items: two 64-element groups
 // each, one per wave] [row items: 8 rows each, 16 lanes per row].  A row
 // item requests its weights first, then waits for the digit flag (set by
@@ -236,35 +236,6 @@ __device__ __forceinline__ void mv_stage(const MatvecArgs& a, XGroup* xs) {
   __syncthreads();
 }
 
-// Q4_K, in_dim = 1024 GPL: lane l16 of a row takes groups l16 + 16 t.
-template <int GPL>
-__global__ __launch_bounds__(128) void k_matvec1_q4k(MatvecArgs a) {
-  __shared__ XGroup xs[16 * GPL];
-  const int nd = mv_digit_items(a.gr);
-  if ((int)blockIdx.x < nd) {
-    mv_digit_item(a);
-    return;
-  }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int row = 8 * ((int)blockIdx.x - nd) + 4 * wave + (lane >> 4);
-  const int l16 = lane & 15, g = l16 & 3;
-  const uint8_t* rp = a.W + (size_t)min(row, a.rows - 1) * (size_t)(a.gr / 4) * kQ4KBlock;
-  Q4KGroupLoad ld[GPL];
-#pragma unroll
-  for (int t = 0; t < GPL; ++t) ld[t] = q4k_load_group(rp + (size_t)(4 * t + (l16 >> 2)) * kQ4KBlock, g);
-  mv_wait_digits(a);
-  mv_stage<16 * GPL>(a, xs);
-  const Q4KScaleSel sel = q4k_scale_sel(g);
-  float acc = 0.0f;
-#pragma unroll
-  for (int t = 0; t < GPL; ++t) {
-    acc += q4k_group_dot_ld(ld[t], sel, &xs[16 * t + l16]);
-    __builtin_amdgcn_sched_barrier(0);  // one group's LDS reads at a time
-  }
-  acc = sum16(acc);
-  if (row < a.rows && l16 == 0) a.y[row] = acc;
-}
-
 // Q6_K, in_dim = 2048 HPL: lane l16 of a row takes 128-element halves l16 + 16 t.
 template <int HPL>
 __global__ __launch_bounds__(128) void k_matvec1_q6k(MatvecArgs a) {
@@ -297,29 +268,87 @@ __global__ __launch_bounds__(128) void k_matvec1_q6k(MatvecArgs a) {
 }
 
 bool matvec1_supported(bool q6, int in_dim) {
-  if (q6) return in_dim % 2048 == 0 && in_dim / 2048 >= 1 && in_dim / 2048 <= 3;
-  return in_dim % 1024 == 0 && in_dim / 1024 >= 1 && in_dim / 1024 <= 7;
+  return q6 && in_dim % 2048 == 0 && in_dim / 2048 >= 1 && in_dim / 2048 <= 3;
 }
 
 hipError_t launch_matvec1(const MatvecArgs& a, bool q6, hipStream_t s) {
-  const int in_dim = a.gr * 64;
+  if (!q6) return hipErrorInvalidValue;  // Q4_K takes the column-part kernel below
   const dim3 grid((unsigned)((a.gr + 1) / 2 + (a.rows + 7) / 8)), block(128);
-  if (q6) {
-    switch (in_dim / 2048) {
-      case 1: hipLaunchKernelGGL(k_matvec1_q6k<1>, grid, block, 0, s, a); break;
-      case 2: hipLaunchKernelGGL(k_matvec1_q6k<2>, grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL(k_matvec1_q6k<3>, grid, block, 0, s, a); break;
+  switch (a.gr * 64 / 2048) {
+    case 1: hipLaunchKernelGGL(k_matvec1_q6k<1>, grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(k_matvec1_q6k<2>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(k_matvec1_q6k<3>, grid, block, 0, s, a); break;
+  }
+  return hipGetLastError();
+}
+
+// ---- one launch by column parts (Q4_K, in_dim = 1024 P) -------------------------------
+// Items of 256 threads, part-major: (part p, 16-row block).  An item turns its
+// part's 1024 activations into digit records itself (4 KB of x: no hand-off
+// before the math), contracts its 16 rows x 4 blocks (16 lanes per row, one
+// 64-element group each) and publishes each row's partial sum as a tagged
+// word.  The items of the last part then take the earlier parts' partials of
+// their rows (bounded waits; those items precede them in the list) and write
+// y = ((p_0 + p_1) + ...) + p_(P-1).
+template <int P>
+__global__ __launch_bounds__(256) void k_matvec2_q4k(Matvec2Args a) {
+  __shared__ XGroup xs[16];
+  __shared__ float own[16];
+  const int nb = (a.rows + 15) / 16;
+  const int p = blockIdx.x / nb, rb = blockIdx.x - p * nb;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = 16 * rb + 4 * wave + (lane >> 4);
+  const int l16 = lane & 15, g = l16 & 3;
+  const uint8_t* bp = a.W + ((size_t)min(row, a.rows - 1) * (4 * P) + 4 * p + (l16 >> 2)) * kQ4KBlock;
+  const Q4KGroupLoad ld = q4k_load_group(bp, g);
+  float xv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) xv[i] = a.x[1024 * p + 64 * (4 * wave + i) + lane];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) digits_to_lds(xv[i], xs[4 * wave + i]);
+  __syncthreads();
+  const float acc = sum16(q4k_group_dot_ld(ld, q4k_scale_sel(g), &xs[l16]));
+  if (p < P - 1) {
+    if (l16 == 0 && row < a.rows) put_tagged(a.part + (size_t)p * a.rows + row, a.epoch, __float_as_uint(acc));
+    return;
+  }
+  if (l16 == 0) own[4 * wave + (lane >> 4)] = acc;
+  __syncthreads();
+  const int r = 16 * rb + (int)threadIdx.x;
+  if (threadIdx.x >= 16 || r >= a.rows) return;
+  float sum = 0.0f;
+#pragma unroll
+  for (int q = 0; q < P - 1; ++q) {
+    uint64_t v = get_tagged(a.part + (size_t)q * a.rows + r);
+    for (unsigned n = 0; !tag_is(v, a.epoch); ++n) {
+      if (n >= a.spin_limit || ((n & 63) == 63 && load_u32_agent(a.err) == a.epoch)) {
+        store_u32_agent(a.err, a.epoch);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+      v = get_tagged(a.part + (size_t)q * a.rows + r);
     }
-  } else {
-    switch (in_dim / 1024) {
-      case 1: hipLaunchKernelGGL(k_matvec1_q4k<1>, grid, block, 0, s, a); break;
-      case 2: hipLaunchKernelGGL(k_matvec1_q4k<2>, grid, block, 0, s, a); break;
-      case 3: hipLaunchKernelGGL(k_matvec1_q4k<3>, grid, block, 0, s, a); break;
-      case 4: hipLaunchKernelGGL(k_matvec1_q4k<4>, grid, block, 0, s, a); break;
-      case 5: hipLaunchKernelGGL(k_matvec1_q4k<5>, grid, block, 0, s, a); break;
-      case 6: hipLaunchKernelGGL(k_matvec1_q4k<6>, grid, block, 0, s, a); break;
-      default: hipLaunchKernelGGL(k_matvec1_q4k<7>, grid, block, 0, s, a); break;
-    }
+    sum = q == 0 ? tagged_f(v) : sum + tagged_f(v);
+  }
+  a.y[r] = P == 1 ? own[threadIdx.x] : sum + own[threadIdx.x];
+}
+
+bool matvec2_supported(int in_dim, int rows, size_t part_words) {
+  const int P = in_dim / 1024;
+  return in_dim % 1024 == 0 && P >= 1 && P <= 7 && (size_t)(P - 1) * (size_t)rows <= part_words;
+}
+
+hipError_t launch_matvec2_q4k(const Matvec2Args& a, int in_dim, hipStream_t s) {
+  const int P = in_dim / 1024;
+  const dim3 grid((unsigned)(P * ((a.rows + 15) / 16))), block(256);
+  switch (P) {
+    case 1: hipLaunchKernelGGL(k_matvec2_q4k<1>, grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(k_matvec2_q4k<2>, grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL(k_matvec2_q4k<3>, grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(k_matvec2_q4k<4>, grid, block, 0, s, a); break;
+    case 5: hipLaunchKernelGGL(k_matvec2_q4k<5>, grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL(k_matvec2_q4k<6>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(k_matvec2_q4k<7>, grid, block, 0, s, a); break;
   }
   return hipGetLastError();
 }

@@ -27,9 +27,11 @@ def run(fdm, q6, raw, x, rows, cols):
     (False, 21, 1280),     # generic path (5 blocks per row)
     (True, 19, 7168),      # Q6_K generic path (56 halves per row)
     (True, 33, 512),
-    (False, 37, 1024),     # one-launch path, one group per lane, ragged rows
-    (False, 9, 3072),      # one-launch path, three groups per lane
+    (False, 37, 1024),     # one-launch column-part path, one part, ragged rows
+    (False, 9, 3072),      # three parts
     (False, 100, 5120),
+    (False, 45, 7168),     # seven parts, ragged rows
+    (False, 3, 2048),
     (True, 5, 4096),       # one-launch Q6_K path, two halves per lane
     (True, 13, 6144),
 ])
