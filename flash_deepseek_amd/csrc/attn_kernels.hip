@@ -6,14 +6,14 @@
 //
 // Launch sequence of one token (fdm_attn_forward):
 //   rms_norm(hidden, attn_norm)                        (bit-exact, shared kernel)
-//   q_a = W_qa . normed; rms_norm(q_a, q_a_norm)       k_mv_f16, rms_norm
+//   [q_a; kv_a] = [W_qa; W_kva] . normed  [1536 + 576]  k_mv_f16 (the two stacked)
+//   rms_norm(q_a, q_a_norm), rms_norm(kv_a[:512])        k_rms_norm_pair
 //   q = W_qb . q_a_n  [128][192]                        k_mv_f16
-//   kv_a = W_kva . normed [576]; rms_norm(kv_a[:512])   k_mv_f16, rms_norm
 //   YaRN RoPE of q_rope and k_rope at pos, cache append k_mla_rope_append
 //   Q_abs[h] = k_b[h] . q_nope[h]  [128][512]           k_mv_f16_heads
-//   scores[h][s] = scale (Q_abs[h].c_kv[s] + q_rope[h].k_rope[s])   k_mla_scores
+//   scores[h][s] = scale (Q_abs[h].c_kv[s] + q_rope[h].k_rope[s])   k_mla_scores_mfma
 //   p = softmax(scores[h]) in place                                  k_mla_softmax
-//   wc[h] = sum_s p[h][s] c_kv[s] (per 64-position chunk, then summed) k_mla_wsum_part/_reduce
+//   wc[h] = sum_s p[h][s] c_kv[s] (per 256-position chunk, summed)  k_mla_wsum_mfma/_reduce
 //   attn[h] = v_b[h] . wc[h]  [128][128]                k_mv_f16_heads
 //   hidden = residual + W_o . attn                      k_mv_f16 (+ residual)
 // The matvecs stream F16 weights (375 MB per R1 layer) once and bound the
@@ -137,63 +137,55 @@ __global__ __launch_bounds__(256) void k_mla_rope_append(float* __restrict__ q, 
 }
 
 // scores[h][s] = scale * (Q_abs[h] . c_kv[s]) + scale * (q_rope[h] . k_rope[s])
-// for s < S (the reference's two sgemm calls, infer.m:829-838), as a tiled
-// product: workgroup (position block of 64, head block of 8); the 576 dims
-// go through LDS in 9 tiles of 64 (8 latent, 1 rope), the cache tile
-// transposed so the 64 lanes of a wave read 64 consecutive positions.
-// Thread (wave w, lane p): position p of the block, heads 2 w, 2 w + 1.
-__global__ __launch_bounds__(256) void k_mla_scores(const float* __restrict__ q_abs, const float* __restrict__ q,
-                                                    const float* __restrict__ cache_c,
-                                                    const float* __restrict__ cache_k, int S, float scale,
-                                                    float* __restrict__ scores) {
-  __shared__ float ct[64][65];  // [dim][position], padded
-  __shared__ float qt[8][64];  // [head][dim]
-  const int s0 = blockIdx.x * 64, h0 = blockIdx.y * 8;
+// for s < S (the reference's two sgemm calls, infer.m:829-838) on fp32 MFMA
+// (v_mfma_f32_16x16x4f32: fp32 products, fp32 accumulation, as the sgemm): one wave per tile of 16 heads x 16
+// positions, heads as rows and positions as columns.  MFMA step e of a group
+// of 16 dims takes from lane l the dim 16 m + 4 (l / 16) + e of its row, so
+// both operands are read as float4 along the dims (the contraction order is
+// the same permutation on both sides); four accumulators (one per step)
+// keep four independent chains.  Workgroup: 4 position tiles of one head tile.
+__device__ __forceinline__ f32x4 mfma_f32x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void k_mla_scores_mfma(const float* __restrict__ q_abs, const float* __restrict__ q,
+                                                         const float* __restrict__ cache_c,
+                                                         const float* __restrict__ cache_k, int S, float scale,
+                                                         float* __restrict__ scores) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float a[2] = {}, b[2] = {};
-  for (int tile = 0; tile < 9; ++tile) {
-    const bool rope = tile == 8;
-    __syncthreads();
-    // cache tile: positions s0 .. s0 + 63, dims 64 tile .. + 63 (coalesced
-    // rows); every load of the tile is issued before the first LDS store
-    float cv[16], qv[2];
+  const int r = lane & 15, q4 = lane >> 4;
+  const int h0 = 16 * blockIdx.y, s0 = 64 * blockIdx.x + 16 * wave;
+  const int sp = min(s0 + r, S - 1);  // past the cache: a valid row, result not written
+  const float* qa = q_abs + (size_t)(h0 + r) * 512 + 4 * q4;
+  const float* cc = cache_c + (size_t)sp * 512 + 4 * q4;
+  f32x4 a[4], b[4];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int i = threadIdx.x + 256 * k, sp = i >> 6, d = i & 63, s = s0 + sp;
-      cv[k] = s < S ? (rope ? cache_k[(size_t)s * 64 + d] : cache_c[(size_t)s * 512 + 64 * tile + d]) : 0.0f;
-    }
+  for (int e = 0; e < 4; ++e) a[e] = b[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+  for (int m = 0; m < 32; ++m) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(qa + 16 * m);
+    const f32x4 y = *reinterpret_cast<const f32x4*>(cc + 16 * m);
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int i = threadIdx.x + 256 * k, h = h0 + (i >> 6), d = i & 63;
-      qv[k] = rope ? q[(size_t)h * 192 + 128 + d] : q_abs[(size_t)h * 512 + 64 * tile + d];
-    }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      ct[i & 63][i >> 6] = cv[k];
-    }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int i = threadIdx.x + 256 * k;
-      qt[i >> 6][i & 63] = qv[k];
-    }
-    __syncthreads();
-#pragma unroll 8
-    for (int d = 0; d < 64; ++d) {
-      const float c = ct[d][lane];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (rope)
-          b[j] = fmaf(qt[2 * wave + j][d], c, b[j]);
-        else
-          a[j] = fmaf(qt[2 * wave + j][d], c, a[j]);
-      }
-    }
+    for (int e = 0; e < 4; ++e) a[e] = mfma_f32x4(x[e], y[e], a[e]);
   }
-  const int s = s0 + lane;
+  const float* qr = q + (size_t)(h0 + r) * 192 + 128 + 4 * q4;
+  const float* kr = cache_k + (size_t)sp * 64 + 4 * q4;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(qr + 16 * m);
+    const f32x4 y = *reinterpret_cast<const f32x4*>(kr + 16 * m);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) b[e] = mfma_f32x4(x[e], y[e], b[e]);
+  }
+  // D: lane l holds heads h0 + 4 (l / 16) + v, position s0 + l % 16
+  const int s = s0 + r;
   if (s < S) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) scores[(size_t)(h0 + 2 * wave + j) * S + s] = scale * a[j] + scale * b[j];
+    for (int v = 0; v < 4; ++v) {
+      const float av = (a[0][v] + a[1][v]) + (a[2][v] + a[3][v]);
+      const float bv = (b[0][v] + b[1][v]) + (b[2][v] + b[3][v]);
+      scores[(size_t)(h0 + 4 * q4 + v) * S + s] = scale * av + scale * bv;
+    }
   }
 }
 
@@ -228,48 +220,39 @@ __global__ __launch_bounds__(256) void k_mla_softmax(float* __restrict__ scores,
   for (int s = threadIdx.x; s < S; s += 256) sc[s] *= inv;
 }
 
-// Partial latent sums (infer.m:862-867 as a tiled product): workgroup
-// (chunk c of 64 positions, block of 64 latent dims) reads its cache tile
-// and the 128 heads' probabilities once; thread t: dim 64 b + (t & 63),
-// heads (t >> 6) + 4 j, j < 32.  part[c][h][d] = sum over the chunk.
-__global__ __launch_bounds__(256) void k_mla_wsum_part(const float* __restrict__ p, int S,
+// Partial latent sums on fp32 MFMA: part[c][h][d] = sum over the positions
+// of chunk c (kMlaChunk of them) of p[h][s] c_kv[s][d] (infer.m:862-867).  One
+// wave per tile of 16 heads (rows) x 16 latent dims (columns); step e of a
+// group of 16 positions takes from lane l the position 16 m + 4 (l / 16) + e.
+// Workgroup: 4 dim tiles of one head tile and one chunk.
+constexpr int kMlaChunk = 256;
+
+__global__ __launch_bounds__(256) void k_mla_wsum_mfma(const float* __restrict__ p, int S,
                                                        const float* __restrict__ cache_c,
                                                        float* __restrict__ part) {
-  __shared__ float ct[64][64];    // [position][dim]
-  __shared__ float pt[128][65];   // [head][position], padded
-  const int c = blockIdx.x, d0 = blockIdx.y * 64, s0 = c * 64, ns = min(64, S - s0);
-  const int lane = threadIdx.x & 63, hq = threadIdx.x >> 6;
-  float cv[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, q4 = lane >> 4;
+  const int c = blockIdx.x, h0 = 16 * (blockIdx.y >> 3), d0 = 64 * (blockIdx.y & 7) + 16 * wave;
+  const int base = c * kMlaChunk, end = min(S, base + kMlaChunk);
+  const float* pr = p + (size_t)(h0 + r) * S;
+  f32x4 acc[4];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int i = threadIdx.x + 256 * k, sp = i >> 6;
-    cv[k] = sp < ns ? cache_c[(size_t)(s0 + sp) * 512 + d0 + (i & 63)] : 0.0f;
-  }
-  float pv[32];
+  for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int g = base; g < end; g += 16) {
+    const int s = g + 4 * q4;
+    float x[4], y[4];
 #pragma unroll
-  for (int k = 0; k < 32; ++k) {
-    const int i = threadIdx.x + 256 * k, h = i >> 6, sp = i & 63;
-    pv[k] = sp < ns ? p[(size_t)h * S + s0 + sp] : 0.0f;
-  }
+    for (int e = 0; e < 4; ++e) {
+      const bool in = s + e < end;
+      x[e] = in ? pr[s + e] : 0.0f;
+      y[e] = in ? cache_c[(size_t)(s + e) * 512 + d0 + r] : 0.0f;
+    }
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    ct[i >> 6][i & 63] = cv[k];
-  }
-#pragma unroll
-  for (int k = 0; k < 32; ++k) {
-    const int i = threadIdx.x + 256 * k;
-    pt[i >> 6][i & 63] = pv[k];
-  }
-  __syncthreads();
-  float acc[32] = {};
-  for (int sp = 0; sp < 64; ++sp) {
-    const float cval = ct[sp][lane];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) acc[j] = fmaf(pt[hq + 4 * j][sp], cval, acc[j]);
+    for (int e = 0; e < 4; ++e) acc[e] = mfma_f32x4(x[e], y[e], acc[e]);
   }
 #pragma unroll
-  for (int j = 0; j < 32; ++j) part[((size_t)c * 128 + hq + 4 * j) * 512 + d0 + lane] = acc[j];
+  for (int v = 0; v < 4; ++v)
+    part[((size_t)c * 128 + h0 + 4 * q4 + v) * 512 + d0 + r] = (acc[0][v] + acc[1][v]) + (acc[2][v] + acc[3][v]);
 }
 
 // wc[h][d] = sum over chunks c = 0, 1, ... of part[c][h][d] (fixed order).
@@ -304,13 +287,13 @@ hipError_t launch_mla_attend(const MlaArgs& a, hipStream_t s) {
   // Q_abs[h] = k_b[h] (512 x 128) . q_nope[h]
   if (hipError_t e = launch_mv_f16_heads(a.k_b, a.q, 192, a.q_abs, 128, 512, 128, s)) return e;
   const int S = a.len + 1;
-  k_mla_scores<<<dim3((S + 63) / 64, 128 / 8), 256, 0, s>>>(a.q_abs, a.q, a.cache_c, a.cache_k, S, a.scale,
-                                                             a.scores);
+  k_mla_scores_mfma<<<dim3((S + 63) / 64, 128 / 16), 256, 0, s>>>(a.q_abs, a.q, a.cache_c, a.cache_k, S, a.scale,
+                                                                  a.scores);
   if (hipError_t e = hipGetLastError()) return e;
   k_mla_softmax<<<128, 256, 0, s>>>(a.scores, S);
   if (hipError_t e = hipGetLastError()) return e;
-  const int n_chunks = (S + 63) / 64;
-  k_mla_wsum_part<<<dim3(n_chunks, 512 / 64), 256, 0, s>>>(a.scores, S, a.cache_c, a.part);
+  const int n_chunks = (S + kMlaChunk - 1) / kMlaChunk;
+  k_mla_wsum_mfma<<<dim3(n_chunks, (128 / 16) * 8), 256, 0, s>>>(a.scores, S, a.cache_c, a.part);
   if (hipError_t e = hipGetLastError()) return e;
   k_mla_wsum_reduce<<<128 * 512 / 256, 256, 0, s>>>(a.part, n_chunks, a.wc);
   if (hipError_t e = hipGetLastError()) return e;

@@ -112,7 +112,8 @@ struct AttnScratch {
   float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr;
   int seq = 0;
   void release() {
-    for (float* p : {normed, q_a, q_a_n, q, kv_a, c_kv_n, q_abs, scores, wc, attn, part})
+    // kv_a lives in q_a's allocation (the two projections run as one matvec)
+    for (float* p : {normed, q_a, q_a_n, q, c_kv_n, q_abs, scores, wc, attn, part})
       if (p) (void)hipFree(p);
     *this = AttnScratch();
   }
@@ -213,8 +214,9 @@ struct AttnLayer {
   float *cache_c = nullptr, *cache_k = nullptr;
   int max_seq = 0, len = 0;
   ~AttnLayer() {
+    // kv_a lives in q_a's allocation: rows 1536 .. 2111 of one stacked matrix
     for (void* p : {(void*)attn_norm, (void*)q_a_norm, (void*)kv_a_norm, (void*)freq, (void*)q_a, (void*)q_b,
-                    (void*)kv_a, (void*)k_b, (void*)v_b, (void*)o_proj, (void*)cache_c, (void*)cache_k})
+                    (void*)k_b, (void*)v_b, (void*)o_proj, (void*)cache_c, (void*)cache_k})
       if (p) (void)hipFree(p);
   }
 };
@@ -1879,15 +1881,16 @@ static int ensure_attn(Workspace& w, int seq, hipStream_t s) {
   FDM_HIP(hipStreamSynchronize(s));
   ws.release();
   const size_t H = FDM_HIDDEN, QA = 1536, QB = 128 * 192, KVA = 576, O = 128 * 128;
-  const size_t n[] = {H, QA, QA, QB, KVA, 512, 128 * 512, (size_t)128 * seq, 128 * 512, O,
+  const size_t n[] = {H, QA + KVA, QA, QB, 512, 128 * 512, (size_t)128 * seq, 128 * 512, O,
                       (size_t)((seq + 63) / 64) * 128 * 512};
-  float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.kv_a, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn,
+  float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn,
                  &ws.part};
-  for (int i = 0; i < 11; ++i)
+  for (int i = 0; i < 10; ++i)
     if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
       ws.release();
       return fail(FDM_E_NOMEM, "cannot allocate the attention scratch");
     }
+  ws.kv_a = ws.q_a + QA;  // q_a and kv_a: one [1536 + 576] output
   ws.seq = seq;
   return FDM_OK;
 }
@@ -1906,13 +1909,19 @@ int fdm_attn_upload(int L, const fdm_attn_weights* w, int max_seq) {
     const void* src;
     size_t bytes;
   } m[] = {{(void**)&a->attn_norm, w->attn_norm, H * 4}, {(void**)&a->q_a_norm, w->q_a_norm, QA * 4},
-           {(void**)&a->kv_a_norm, w->kv_a_norm, 512 * 4}, {(void**)&a->q_a, w->q_a, QA * H * 2},
-           {(void**)&a->q_b, w->q_b, QB * QA * 2}, {(void**)&a->kv_a, w->kv_a, KVA * H * 2},
+           {(void**)&a->kv_a_norm, w->kv_a_norm, 512 * 4}, {(void**)&a->q_b, w->q_b, QB * QA * 2},
            {(void**)&a->k_b, w->k_b, KB * 2}, {(void**)&a->v_b, w->v_b, KB * 2}, {(void**)&a->o_proj, w->o_proj, H * O * 2}};
   for (const M& x : m) {
     if (hipMalloc(x.dst, x.bytes) != hipSuccess) return fail(FDM_E_NOMEM, "cannot allocate attention layer %d", L);
     FDM_HIP(hipMemcpy(*x.dst, x.src, x.bytes, hipMemcpyHostToDevice));
   }
+  // q_a and kv_a stacked in one allocation ([1536 + 576][7168]): the forward
+  // runs both projections, which read the same input, as one matvec
+  if (hipMalloc(&a->q_a, (QA + KVA) * H * 2) != hipSuccess)
+    return fail(FDM_E_NOMEM, "cannot allocate attention layer %d", L);
+  a->kv_a = a->q_a + QA * H;
+  FDM_HIP(hipMemcpy(a->q_a, w->q_a, QA * H * 2, hipMemcpyHostToDevice));
+  FDM_HIP(hipMemcpy(a->kv_a, w->kv_a, KVA * H * 2, hipMemcpyHostToDevice));
   float freq[32];
   yarn_table(freq);
   if (hipMalloc(&a->freq, sizeof freq) != hipSuccess ||
@@ -2036,11 +2045,11 @@ int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
   AttnScratch& ws = w->attn;
   ProfScope prof(FDM_PROF_ATTN, s);
   FDM_HIP(launch_rms_norm(d_hidden, a.attn_norm, ws.normed, 1, FDM_HIDDEN, s));
-  FDM_HIP(launch_mv_f16(a.q_a, ws.normed, nullptr, ws.q_a, 1536, FDM_HIDDEN, s));
-  FDM_HIP(launch_rms_norm(ws.q_a, a.q_a_norm, ws.q_a_n, 1, 1536, s));
+  // q_a and kv_a (infer.m:781-789) read the same input: one matvec over the
+  // stacked [1536 + 576] rows, then both rms_norms in one launch
+  FDM_HIP(launch_mv_f16(a.q_a, ws.normed, nullptr, ws.q_a, 1536 + 576, FDM_HIDDEN, s));
+  FDM_HIP(launch_rms_norm_pair(ws.q_a, a.q_a_norm, ws.q_a_n, 1536, ws.kv_a, a.kv_a_norm, ws.c_kv_n, 512, s));
   FDM_HIP(launch_mv_f16(a.q_b, ws.q_a_n, nullptr, ws.q, 128 * 192, 1536, s));
-  FDM_HIP(launch_mv_f16(a.kv_a, ws.normed, nullptr, ws.kv_a, 576, FDM_HIDDEN, s));
-  FDM_HIP(launch_rms_norm(ws.kv_a, a.kv_a_norm, ws.c_kv_n, 1, 512, s));
   // softmax scale with the YaRN mscale (infer.m:802-815), in float as there
   const float mscale = 0.1f * logf(40.0f) + 1.0f;
   MlaArgs m;

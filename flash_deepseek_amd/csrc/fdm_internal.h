@@ -183,6 +183,9 @@ hipError_t launch_combine(const BatchArgs& b, hipStream_t s);
 // prefill_kernels.hip
 // rms_norm per token (infer.m:369-374), bit-exact: o = x * inv * w.  d <= 7168.
 hipError_t launch_rms_norm(const float* x, const float* w, float* o, int T, int d, hipStream_t s);
+// Two rows of widths d0, d1 (<= 7168) in one launch, each as launch_rms_norm.
+hipError_t launch_rms_norm_pair(const float* x0, const float* w0, float* o0, int d0, const float* x1,
+                                const float* w1, float* o1, int d1, hipStream_t s);
 
 // gemm_kernels.hip: grouped expert GEMMs (batched decode, prefill) on MFMA.
 // Rows: pair position p (routed), T*K + t (shared expert of token t).

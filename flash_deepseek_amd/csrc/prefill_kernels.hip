@@ -13,11 +13,8 @@ namespace fdm {
 // in order); sqrt and division are IEEE; o = (x * inv) * w as infer.m:372.
 // At d = 7168 (16-byte aligned rows) every load is a 16-byte vector load
 // issued before the sum, so the row's latency is paid once.
-__global__ __launch_bounds__(kRmsThreads) void k_rms_norm(const float* __restrict__ x,
-                                                          const float* __restrict__ w, float* o, int d) {
-  __shared__ RmsSmem sm;
-  const float* xr = x + (size_t)blockIdx.x * d;
-  float* orow = o + (size_t)blockIdx.x * d;
+__device__ __forceinline__ void rms_norm_row(const float* __restrict__ xr, const float* __restrict__ w,
+                                             float* orow, int d, RmsSmem& sm) {
   const int n = (d + kRmsThreads - 1) / kRmsThreads;
   const int i0 = threadIdx.x * n;
   const bool vec = d == kHidden && (reinterpret_cast<uintptr_t>(xr) & 15) == 0 &&
@@ -66,6 +63,31 @@ __global__ __launch_bounds__(kRmsThreads) void k_rms_norm(const float* __restric
     const float v = xr[i] * inv;
     orow[i] = w ? v * w[i] : v;
   }
+}
+
+__global__ __launch_bounds__(kRmsThreads) void k_rms_norm(const float* __restrict__ x,
+                                                          const float* __restrict__ w, float* o, int d) {
+  __shared__ RmsSmem sm;
+  rms_norm_row(x + (size_t)blockIdx.x * d, w, o + (size_t)blockIdx.x * d, d, sm);
+}
+
+// Two independent rows of different widths in one launch (the attention's
+// q_a and kv_a norms): workgroup 0 and 1.
+__global__ __launch_bounds__(kRmsThreads) void k_rms_norm_pair(const float* __restrict__ x0,
+                                                               const float* __restrict__ w0, float* o0, int d0,
+                                                               const float* __restrict__ x1,
+                                                               const float* __restrict__ w1, float* o1, int d1) {
+  __shared__ RmsSmem sm;
+  if (blockIdx.x == 0)
+    rms_norm_row(x0, w0, o0, d0, sm);
+  else
+    rms_norm_row(x1, w1, o1, d1, sm);
+}
+
+hipError_t launch_rms_norm_pair(const float* x0, const float* w0, float* o0, int d0, const float* x1,
+                                const float* w1, float* o1, int d1, hipStream_t s) {
+  hipLaunchKernelGGL(k_rms_norm_pair, dim3(2), dim3(kRmsThreads), 0, s, x0, w0, o0, d0, x1, w1, o1, d1);
+  return hipGetLastError();
 }
 
 hipError_t launch_rms_norm(const float* x, const float* w, float* o, int T, int d, hipStream_t s) {
