@@ -43,8 +43,15 @@ typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kQWaves = 4;            // waves per workgroup
 constexpr int kQRowB = kQK * 2;       // LDS token row: one block of fp16 (512 B)
-constexpr int kQGuRows = 16 * kQWaves;   // gate (and up) rows per workgroup: 128
-constexpr int kQDnRows = 32 * kQWaves;   // down rows per workgroup: 256
+// Weight tiles of 16 rows per wave (TL): a gate/up GEMM holds TL / 2 tiles of
+// gate and as many of up (SwiGLU pairs tile t with tile t + TL / 2), a down
+// GEMM TL tiles; every token operand read from LDS serves all of them.  Four
+// tiles for the fp32-grade gate/up (three planes: twice the weights per token
+// operand read, 238 VGPRs, 2 waves per SIMD), two elsewhere (3 waves per SIMD).
+__host__ __device__ constexpr int qgemm_tiles(int planes, bool down) { return (planes == 3 && !down) ? 4 : 2; }
+__host__ __device__ constexpr int qgemm_rows(int tiles, bool down) {  // rows per workgroup (of gate for gate/up)
+  return (down ? 16 : 8) * tiles * kQWaves;
+}
 
 // One lane's share of one block of one weight row (resident expert layout):
 // its group's 32 qs bytes and the 16-byte block header.
@@ -211,7 +218,7 @@ __global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, in
 }
 
 // ---- the grouped GEMM ------------------------------------------------------------------
-template <int P, int NB, bool DOWN>
+template <int P, int NB, bool DOWN, int TL>
 __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int* rows, int chunk, int rg) {
   constexpr int KD = DOWN ? kFfn : kHidden;  // contraction length
   constexpr int NBLK = KD / kQK;             // 8 or 28 (even)
@@ -235,17 +242,19 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
   }
   __syncthreads();
   const uint8_t* blob = shared ? g.shared : g.experts + (size_t)ck.x * g.expert_size;
-  const uint8_t* mat0;
-  const uint8_t* mat1;
-  int row0, row1;
-  if (DOWN) {
-    mat0 = mat1 = blob + 2 * (size_t)kGateBytes;
-    row0 = rg * kQDnRows + 32 * wave + c16;
-    row1 = row0 + 16;
-  } else {
-    mat0 = blob;
-    mat1 = blob + kGateBytes;
-    row0 = row1 = rg * kQGuRows + 16 * wave + c16;
+  constexpr int ROWS = qgemm_rows(TL, DOWN);
+  const uint8_t* mat[TL];
+  int row[TL];
+#pragma unroll
+  for (int t = 0; t < TL; ++t) {
+    if (DOWN) {
+      mat[t] = blob + 2 * (size_t)kGateBytes;
+      row[t] = rg * ROWS + 16 * TL * wave + 16 * t + c16;
+    } else {
+      // tiles 0 .. TL/2 - 1: gate rows, TL/2 .. TL - 1: the same rows of up
+      mat[t] = blob + (t < TL / 2 ? 0 : (size_t)kGateBytes);
+      row[t] = rg * ROWS + 8 * TL * wave + 16 * (t % (TL / 2)) + c16;
+    }
   }
   // direct-load sources: round k of wave w fills LDS rows 2 (w + 8 k), +1 of
   // the buffer (row rho = plane * NT + token); lane i: row rho0 + i / 32,
@@ -273,63 +282,92 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
     const float2 v = *reinterpret_cast<const float2*>(g.xs + (size_t)rin[16 * nb + c16] * (KD / 32) + 8 * b + 2 * j);
     return v;
   };
-  f32x4 acc[2][NB];
+  f32x4 acc[TL][NB];
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
+  for (int tt = 0; tt < TL; ++tt)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[tt][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // One block: both tiles' B operands are built per MFMA step and share
-  // every token operand read from LDS.
-  auto block = [&](int buf, const QLane& w0, const QLane& w1, const float2 (&xsv)[NB]) {
+  // One block: the token operands of an MFMA step are read from LDS once and
+  // serve every tile, whose B operands are built per step.
+  auto block = [&](int buf, const QLane (&w)[TL], const float2 (&xsv)[NB]) {
     const uint8_t* base = lds + buf * BUF;
-    const QScale s0 = qscale(w0.hdr, sel), s1 = qscale(w1.hdr, sel);
-    f32x4 C0[NB], C1[NB];
+    QScale sc[TL];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      C0[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      C1[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
+    for (int t = 0; t < TL; ++t) sc[t] = qscale(w[t].hdr, sel);
+    f32x4 C[TL][NB];
+#pragma unroll
+    for (int t = 0; t < TL; ++t)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) C[t][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int i0 = 2 * (m & 1);
-      const u32x4& qa = m < 2 ? w0.q0 : w0.q1;
-      const u32x4& qb = m < 2 ? w1.q0 : w1.q1;
-      const BPair B0 = build_b(qa[i0], qa[i0 + 1], s0.sc_lo, s0.sc_hi);
-      const BPair B1 = build_b(qb[i0], qb[i0 + 1], s1.sc_lo, s1.sc_hi);
+      if constexpr (TL == 2) {
+        // both tiles' B operands first, then each token operand read once
+        // and used by both (the order that keeps two tiles at 3 waves per SIMD)
+        const u32x4& qa = m < 2 ? w[0].q0 : w[0].q1;
+        const u32x4& qb = m < 2 ? w[1].q0 : w[1].q1;
+        const BPair B0 = build_b(qa[i0], qa[i0 + 1], sc[0].sc_lo, sc[0].sc_hi);
+        const BPair B1 = build_b(qb[i0], qb[i0 + 1], sc[1].sc_lo, sc[1].sc_hi);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
+        for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            const uint8_t* r = base + (p * NT + 16 * nb + c16) * kQRowB;
+            const f16x8 alo = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ c16));
+            const f16x8 ahi = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ c16));
+            C[0][nb] = mfma_h(alo, B0.lo, C[0][nb]);
+            C[1][nb] = mfma_h(alo, B1.lo, C[1][nb]);
+            C[0][nb] = mfma_h(ahi, B0.hi, C[0][nb]);
+            C[1][nb] = mfma_h(ahi, B1.hi, C[1][nb]);
+          }
+        }
+        continue;
+      }
+      f16x8 alo[NB][P], ahi[NB][P];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int p = 0; p < P; ++p) {
           const uint8_t* r = base + (p * NT + 16 * nb + c16) * kQRowB;
-          const f16x8 alo = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ c16));
-          const f16x8 ahi = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ c16));
-          C0[nb] = mfma_h(alo, B0.lo, C0[nb]);
-          C1[nb] = mfma_h(alo, B1.lo, C1[nb]);
-          C0[nb] = mfma_h(ahi, B0.hi, C0[nb]);
-          C1[nb] = mfma_h(ahi, B1.hi, C1[nb]);
+          alo[nb][p] = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ c16));
+          ahi[nb][p] = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ c16));
         }
+#pragma unroll
+      for (int t = 0; t < TL; ++t) {
+        const u32x4& qa = m < 2 ? w[t].q0 : w[t].q1;
+        const BPair B = build_b(qa[i0], qa[i0 + 1], sc[t].sc_lo, sc[t].sc_hi);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            C[t][nb] = mfma_h(alo[nb][p], B.lo, C[t][nb]);
+            C[t][nb] = mfma_h(ahi[nb][p], B.hi, C[t][nb]);
+          }
       }
     }
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      f32x4 a0 = acc[0][nb], a1 = acc[1][nb];
+    for (int t = 0; t < TL; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a0[i] = fmaf(s0.d, C0[nb][i], a0[i]);
-        a1[i] = fmaf(s1.d, C1[nb][i], a1[i]);
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x4 a = acc[t][nb];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = fmaf(sc[t].d, C[t][nb][i], a[i]);
+        a = mfma_f(xsv[nb].x, sc[t].bc_lo, a);
+        a = mfma_f(xsv[nb].y, sc[t].bc_hi, a);
+        acc[t][nb] = a;
       }
-      a0 = mfma_f(xsv[nb].x, s0.bc_lo, a0);
-      a0 = mfma_f(xsv[nb].y, s0.bc_hi, a0);
-      a1 = mfma_f(xsv[nb].x, s1.bc_lo, a1);
-      a1 = mfma_f(xsv[nb].y, s1.bc_hi, a1);
-      acc[0][nb] = a0;
-      acc[1][nb] = a1;
-    }
+  };
+  auto load_w = [&](QLane (&w)[TL], int b, bool last) {
+#pragma unroll
+    for (int t = 0; t < TL; ++t)
+      w[t] = last ? qlane_load<DOWN, true>(mat[t], row[t], b, j) : qlane_load<DOWN, false>(mat[t], row[t], b, j);
   };
 
   dma(0, 0);
-  QLane wa0 = qlane_load<DOWN, false>(mat0, row0, 0, j), wa1 = qlane_load<DOWN, false>(mat1, row1, 0, j);
+  QLane wa[TL], wb[TL];
+  load_w(wa, 0, false);
   float2 xa[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) xa[nb] = load_xs(0, nb);
@@ -341,20 +379,19 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
     wait_vm();
     __syncthreads();  // block b staged by every wave; buffer 1 read by all (block b - 1)
     dma(b + 1, 1);
-    QLane wb0 = qlane_load<DOWN, true>(mat0, row0, b + 1, j), wb1 = qlane_load<DOWN, true>(mat1, row1, b + 1, j);
+    load_w(wb, b + 1, true);
     float2 xb[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) xb[nb] = load_xs(b + 1, nb);
-    block(0, wa0, wa1, xa);
+    block(0, wa, xa);
     const int b2 = min(b + 2, NBLK - 1);
     wait_vm();
     __syncthreads();  // block b + 1 staged; buffer 0 read by all (block b)
     dma(b2, 0);
-    wa0 = qlane_load<DOWN, false>(mat0, row0, b2, j);
-    wa1 = qlane_load<DOWN, false>(mat1, row1, b2, j);
+    load_w(wa, b2, false);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) xa[nb] = load_xs(b2, nb);
-    block(1, wb0, wb1, xb);
+    block(1, wb, xb);
   }
   wait_vm();  // the re-staged copy has landed before the LDS is released
   // D of a 16x16 MFMA: lane (c16, j) holds row (column) c16 of the tile and
@@ -368,10 +405,12 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
       const float e = g.xe[rin[t]];
       if (DOWN) {
         float* o = g.out + (size_t)rout[t] * kHidden;
-        o[row0] = acc[0][nb][i] * e;
-        o[row1] = acc[1][nb][i] * e;
+#pragma unroll
+        for (int tt = 0; tt < TL; ++tt) o[row[tt]] = acc[tt][nb][i] * e;
       } else {
-        g.out[(size_t)rout[t] * kFfn + row0] = silu_mul(acc[0][nb][i] * e, acc[1][nb][i] * e);
+#pragma unroll
+        for (int tt = 0; tt < TL / 2; ++tt)
+          g.out[(size_t)rout[t] * kFfn + row[tt]] = silu_mul(acc[tt][nb][i] * e, acc[tt + TL / 2][nb][i] * e);
       }
     }
   }
@@ -389,7 +428,8 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 // from that XCD's L2 to its other chunks; every XCD does the same work.
 template <int P, int NB, bool DOWN>
 __global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(QGemmArgs g) {
-  constexpr int RG = DOWN ? kHidden / kQDnRows : kFfn / kQGuRows;
+  constexpr int TL = qgemm_tiles(P, DOWN);
+  constexpr int RG = (DOWN ? kHidden : kFfn) / qgemm_rows(TL, DOWN);
   constexpr int Q = RG / 8;
   static_assert(Q * 8 == RG, "row groups split evenly over the XCDs");
   const int id = blockIdx.x, xcd = id & 7, k = id >> 3;
@@ -402,9 +442,9 @@ __global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2)
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * P * NT * kQRowB];
   __shared__ int rows[2 * NT];
   if (NB > 1 && g.chunks[chunk].z > 16)
-    qgemm_body<P, NB, DOWN>(g, lds, rows, chunk, rg);
+    qgemm_body<P, NB, DOWN, TL>(g, lds, rows, chunk, rg);
   else
-    qgemm_body<P, 1, DOWN>(g, lds, rows, chunk, rg);
+    qgemm_body<P, 1, DOWN, TL>(g, lds, rows, chunk, rg);
 }
 
 hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
@@ -420,7 +460,7 @@ int qgemm_chunk_tokens(int planes) { return planes == 3 ? 16 : 32; }
 
 hipError_t launch_qgemm(const QGemmArgs& g, int planes, bool down, int max_chunks, hipStream_t s) {
   const dim3 blk(kQWaves * 64);
-  const int RG = down ? kHidden / kQDnRows : kFfn / kQGuRows;
+  const int RG = (down ? kHidden : kFfn) / qgemm_rows(qgemm_tiles(planes, down), down);
   const dim3 grid((unsigned)(RG * max_chunks));
   if (planes == 3) {
     if (down)
