@@ -19,10 +19,11 @@
 // grade; P = 1 carries 11 bits -- prefill, whose bar is 1e-2.  X_sb is the
 // fp32 sum of the planes, so the 1024 X part of C cancels against it.
 //
-// Mapping.  A workgroup of 8 waves owns 128 gate and 128 up rows (wave w:
-// rows 16 w .. 16 w + 15 of both, so SwiGLU is applied in registers) or 256
-// down rows (wave w: two tiles of 16), for one chunk of <= 16 NB tokens of
-// one expert.  Weight rows are the MFMA columns (B operand): lane (c, j)
+// Mapping.  A workgroup of 4 waves owns 64 gate and 64 up rows (wave w:
+// rows 16 w .. 16 w + 15 of both, so SwiGLU is applied in registers) or 128
+// down rows (wave w: two tiles of 16) -- the three-plane gate/up GEMM twice
+// that, 32 rows of gate and of up per wave -- for one chunk of <= 16 NB
+// tokens of one expert.  Weight rows are the MFMA columns (B operand): lane (c, j)
 // holds row c and group j (qs bytes 32 j .. 32 j + 31, sub-blocks 2j, 2j+1)
 // of every block, read as two whole 16-byte pieces of the resident expert
 // layout, so the four lanes of a row read one 64-byte line per load and
@@ -40,6 +41,7 @@ namespace {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kQWaves = 4;            // waves per workgroup
 constexpr int kQRowB = kQK * 2;       // LDS token row: one block of fp16 (512 B)
@@ -90,27 +92,43 @@ __device__ __forceinline__ uint32_t magic2(uint32_t q2, u16x2 sc2) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// The same halves for the two q held in bits 4-7 of the halves of w (the
+// rest of w arbitrary): 0x6400 | 16 q is the half 1024 + 16 q, and one fused
+// multiply-add per half, (1024 + 16 q) (sc / 16) + (1024 - 64 sc), gives
+// 1024 + sc q exactly (the exact result is a half: a single rounding keeps
+// it), with no shift to bring the nibble down.
+__device__ __forceinline__ uint32_t magic2_hi(uint32_t w, f16x2 sc16, f16x2 off) {
+  // one v_and_or_b32 (mask from an SGPR, 0x64006400 from a VGPR: a VOP3
+  // takes no literal and one SGPR), which the compiler otherwise splits
+  uint32_t m;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(m) : "v"(w), "s"(0x00F000F0u), "v"(0x64006400u));
+  const f16x2 v = __builtin_bit_cast(f16x2, m);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, sc16, off));
+}
+
 // The B operands of MFMA steps m (low nibbles) and m + 4 (high nibbles):
 // bytes 8 m' .. 8 m' + 7 of the lane's group, m' = m & 3 (q0 for m' < 2).
 // Elements are taken in the order 0 2 1 3 4 6 5 7 of each 8 (the order in
 // which k_xplanes stores the activations): a dword of qs holds the low
-// nibbles of elements 0 and 2 at bits 0 and 16, so each fp16 pair costs one
-// mask (after one of three shifts per dword) and one packed multiply-add.
+// nibbles of elements 0 and 2 at bits 0 and 16 and their high nibbles at
+// bits 4 and 20, elements 1 and 3 eight bits higher, so one shift per dword
+// and per fp16 pair one mask and one packed multiply-add suffice.
 struct BPair {
   f16x8 lo, hi;
 };
 
-__device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, u16x2 sc_hi) {
+__device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, f16x2 sc16_hi, f16x2 off_hi) {
   constexpr uint32_t M = 0x000F000Fu;
+  const uint32_t v0 = w0 >> 8, v1 = w1 >> 8;
   u32x4 lo, hi;
   lo.x = magic2(w0 & M, sc_lo);
-  lo.y = magic2((w0 >> 8) & M, sc_lo);
+  lo.y = magic2(v0 & M, sc_lo);
   lo.z = magic2(w1 & M, sc_lo);
-  lo.w = magic2((w1 >> 8) & M, sc_lo);
-  hi.x = magic2((w0 >> 4) & M, sc_hi);
-  hi.y = magic2((w0 >> 12) & M, sc_hi);
-  hi.z = magic2((w1 >> 4) & M, sc_hi);
-  hi.w = magic2((w1 >> 12) & M, sc_hi);
+  lo.w = magic2(v1 & M, sc_lo);
+  hi.x = magic2_hi(w0, sc16_hi, off_hi);
+  hi.y = magic2_hi(v0, sc16_hi, off_hi);
+  hi.z = magic2_hi(w1, sc16_hi, off_hi);
+  hi.w = magic2_hi(v1, sc16_hi, off_hi);
   BPair b;
   b.lo = __builtin_bit_cast(f16x8, lo);
   b.hi = __builtin_bit_cast(f16x8, hi);
@@ -120,7 +138,8 @@ __device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, 
 // Per-block constants of the lane's row and group.
 struct QScale {
   float d;
-  u16x2 sc_lo, sc_hi;  // sc of sub-blocks 2j, 2j+1, in both halves
+  u16x2 sc_lo;         // sc of sub-block 2j, in both halves
+  f16x2 sc16_hi, off_hi;  // sc / 16 and 1024 - 64 sc of sub-block 2j+1 (halves)
   float bc_lo, bc_hi;  // -(1024 d + dmin m) of sub-blocks 2j, 2j+1
 };
 
@@ -131,7 +150,12 @@ __device__ __forceinline__ QScale qscale(const u32x4 hdr, const Q4KScaleSel& sel
   s.d = half_to_float(hdr.x);
   const float dmin = half_to_float(hdr.x >> 16);
   s.sc_lo = (u16x2){(unsigned short)sc0, (unsigned short)sc0};
-  s.sc_hi = (u16x2){(unsigned short)sc1, (unsigned short)sc1};
+  // the halves 1024 + sc1, then sc1 / 16 and 1024 - 64 sc1, all exact
+  const f16x2 h = __builtin_bit_cast(f16x2, (uint32_t)sc1 * 0x10001u + 0x64006400u);
+  s.sc16_hi = __builtin_elementwise_fma(h, (f16x2){(_Float16)0.0625f, (_Float16)0.0625f},
+                                        (f16x2){(_Float16)-64.0f, (_Float16)-64.0f});
+  s.off_hi = __builtin_elementwise_fma(s.sc16_hi, (f16x2){(_Float16)-1024.0f, (_Float16)-1024.0f},
+                                       (f16x2){(_Float16)1024.0f, (_Float16)1024.0f});
   const float off = 1024.0f * s.d;  // exact: a power-of-two multiple of a half
   s.bc_lo = -fmaf(dmin, (float)m0, off);
   s.bc_hi = -fmaf(dmin, (float)m1, off);
@@ -308,8 +332,8 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
         // and used by both (the order that keeps two tiles at 3 waves per SIMD)
         const u32x4& qa = m < 2 ? w[0].q0 : w[0].q1;
         const u32x4& qb = m < 2 ? w[1].q0 : w[1].q1;
-        const BPair B0 = build_b(qa[i0], qa[i0 + 1], sc[0].sc_lo, sc[0].sc_hi);
-        const BPair B1 = build_b(qb[i0], qb[i0 + 1], sc[1].sc_lo, sc[1].sc_hi);
+        const BPair B0 = build_b(qa[i0], qa[i0 + 1], sc[0].sc_lo, sc[0].sc16_hi, sc[0].off_hi);
+        const BPair B1 = build_b(qb[i0], qb[i0 + 1], sc[1].sc_lo, sc[1].sc16_hi, sc[1].off_hi);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -337,7 +361,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 #pragma unroll
       for (int t = 0; t < TL; ++t) {
         const u32x4& qa = m < 2 ? w[t].q0 : w[t].q1;
-        const BPair B = build_b(qa[i0], qa[i0 + 1], sc[t].sc_lo, sc[t].sc_hi);
+        const BPair B = build_b(qa[i0], qa[i0 + 1], sc[t].sc_lo, sc[t].sc16_hi, sc[t].off_hi);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -427,7 +451,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 // An expert's weights are then read from HBM once per row group and served
 // from that XCD's L2 to its other chunks; every XCD does the same work.
 template <int P, int NB, bool DOWN>
-__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(QGemmArgs g) {
+__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(qgemm_tiles(P, DOWN) == 4 ? 2 : 3))) void k_qgemm(QGemmArgs g) {
   constexpr int TL = qgemm_tiles(P, DOWN);
   constexpr int RG = (DOWN ? kHidden : kFfn) / qgemm_rows(TL, DOWN);
   constexpr int Q = RG / 8;
