@@ -274,20 +274,30 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
 // hidden[t] = (h_in[t] + sum_k w[t][k] E_{idx[t][k]}) + S[t], slots in route()
 // order (infer.m:1689-1695, 1922).  out may alias h_in (each element is read
 // before it is written, by the same thread).
+// V consecutive outputs per thread (V = 4 when h_in and out are 16-byte
+// aligned: every load and store a 16-byte vector), each the same chain
+// (h_in + sum_k w_k E_k) + S in slot order.
+template <int V>
 __global__ __launch_bounds__(256) void k_bcombine(BatchArgs b) {
+  typedef float vf __attribute__((ext_vector_type(V)));
   const int t = blockIdx.y;
-  const int r = blockIdx.x * 256 + threadIdx.x;
+  const int r = (blockIdx.x * 256 + threadIdx.x) * V;
   if (r >= kHidden) return;
   const int P = b.T * b.K;
-  float moe = 0.0f;
+  vf moe = (vf)0.0f;
   for (int k = 0; k < b.K; ++k) {
     const int pos = b.pair_of[t * b.K + k];
-    const float ev = pos >= 0 ? b.eo[(size_t)pos * kHidden + r] : 0.0f;
-    moe = fmaf(b.w[t * b.K + k], ev, moe);
+    const vf ev = pos >= 0 ? *reinterpret_cast<const vf*>(b.eo + (size_t)pos * kHidden + r) : (vf)0.0f;
+    const float wk = b.w[t * b.K + k];
+#pragma unroll
+    for (int i = 0; i < V; ++i) moe[i] = fmaf(wk, ev[i], moe[i]);
   }
-  const float sd = b.shared ? b.eo[(size_t)(P + t) * kHidden + r] : 0.0f;
-  const float hin = b.h_in ? b.h_in[(size_t)t * kHidden + r] : 0.0f;
-  b.out[(size_t)t * kHidden + r] = (hin + moe) + sd;
+  const vf sd = b.shared ? *reinterpret_cast<const vf*>(b.eo + (size_t)(P + t) * kHidden + r) : (vf)0.0f;
+  const vf hin = b.h_in ? *reinterpret_cast<const vf*>(b.h_in + (size_t)t * kHidden + r) : (vf)0.0f;
+  vf o;
+#pragma unroll
+  for (int i = 0; i < V; ++i) o[i] = (hin[i] + moe[i]) + sd[i];
+  *reinterpret_cast<vf*>(b.out + (size_t)t * kHidden + r) = o;
 }
 
 hipError_t launch_dispatch(const BatchArgs& b, hipStream_t s) {
@@ -296,7 +306,11 @@ hipError_t launch_dispatch(const BatchArgs& b, hipStream_t s) {
 }
 
 hipError_t launch_combine(const BatchArgs& b, hipStream_t s) {
-  hipLaunchKernelGGL(k_bcombine, dim3(kHidden / 256, b.T), dim3(256), 0, s, b);
+  const bool vec = (reinterpret_cast<uintptr_t>(b.out) & 15) == 0 && (reinterpret_cast<uintptr_t>(b.h_in) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL(k_bcombine<4>, dim3(kHidden / 1024, b.T), dim3(256), 0, s, b);
+  else
+    hipLaunchKernelGGL(k_bcombine<1>, dim3(kHidden / 256, b.T), dim3(256), 0, s, b);
   return hipGetLastError();
 }
 
@@ -330,8 +344,7 @@ hipError_t launch_batched_experts(const BatchArgs& b, bool down_q6, hipStream_t 
   else
     hipLaunchKernelGGL(k_bdown<false>, dim3(kBDnTiles, gy), dim3(256), 0, s, b);
   if (hipError_t e = hipGetLastError()) return e;
-  hipLaunchKernelGGL(k_bcombine, dim3(kHidden / 256, b.T), dim3(256), 0, s, b);
-  return hipGetLastError();
+  return launch_combine(b, s);
 }
 
 }  // namespace fdm

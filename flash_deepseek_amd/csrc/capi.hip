@@ -1450,11 +1450,12 @@ QScratch workspace_q(const Workspace& w) {
 }
 
 // The expert half of one step on the grouped GEMMs, after the dispatch:
-// chunk list, planes of the token rows, gate/up + SwiGLU into b.act, then
-// a Q4_K down on the GEMM (planes of b.act first) or a Q6_K down on the
-// dot4 kernels, into b.eo.  x: the fp32 token rows [T][7168].
+// chunk list, planes of the token rows (unless x_planes_ready: the caller
+// has written them), gate/up + SwiGLU into b.act, then a Q4_K down on the
+// GEMM (planes of b.act first) or a Q6_K down on the dot4 kernels, into
+// b.eo.  x: the fp32 token rows [T][7168].
 int run_qgemm_experts(const Layer* y, const BatchArgs& b0, const float* x, int planes, const QScratch& w,
-                      hipStream_t s) {
+                      hipStream_t s, bool x_planes_ready = false) {
   BatchArgs b = b0;
   const int T = b.T, K = b.K;
   const size_t rows = (size_t)T * K + (y->shared ? T : 0);
@@ -1465,7 +1466,7 @@ int run_qgemm_experts(const Layer* y, const BatchArgs& b0, const float* x, int p
   b.chunks = w.chunks;
   b.n_chunks = w.n_chunks;
   FDM_HIP(launch_dispatch(b, s));  // with the chunk list
-  FDM_HIP(launch_xplanes(x, FDM_HIDDEN, (size_t)T, planes, w.planes, w.xs, w.xe, s));
+  if (!x_planes_ready) FDM_HIP(launch_xplanes(x, FDM_HIDDEN, (size_t)T, planes, w.planes, w.xs, w.xe, s));
   QGemmArgs q;
   q.T = T;
   q.K = K;
@@ -1528,7 +1529,9 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     Layer* y = nullptr;
     (void)get_layer(layers[l], &y);
     int* idx = d_idx ? d_idx + (size_t)l * T * K : w.idx;
-    FDM_HIP(launch_rms_norm(d_H, d_norm_w ? d_norm_w[l] : nullptr, w.p_hpost, T, FDM_HIDDEN, s));
+    // the normalised tokens and their one fp16 plane for the expert GEMMs
+    FDM_HIP(launch_rms_norm_planes(d_H, d_norm_w ? d_norm_w[l] : nullptr, w.p_hpost, T, w.q_planes, w.q_xs,
+                                   w.q_xe, s));
     FDM_HIP(launch_router_logits(y->Wg, w.p_hpost, FDM_N_EXPERTS, FDM_HIDDEN, T, w.logits, s));
     FDM_HIP(launch_route(w.logits, y->bias, T, K, idx, w.w, s));
     BatchArgs b{};
@@ -1550,7 +1553,7 @@ int fdm_moe_prefill(const int* layers, int n_layers, float* d_H, int T, int K,
     b.distinct = w.b_distinct;
     b.n_distinct = w.b_ndistinct;
     // prefill precision: one fp16 plane of the activations (the bar is 1e-2)
-    if (int rc = run_qgemm_experts(y, b, w.p_hpost, 1, workspace_q(w), s)) return rc;
+    if (int rc = run_qgemm_experts(y, b, w.p_hpost, 1, workspace_q(w), s, true)) return rc;
     FDM_HIP(launch_combine(b, s));
   }
   return FDM_OK;

@@ -184,6 +184,10 @@ hipError_t launch_combine(const BatchArgs& b, hipStream_t s);
 // rms_norm per token (infer.m:369-374), bit-exact: o = x * inv * w.  d <= 7168.
 hipError_t launch_rms_norm(const float* x, const float* w, float* o, int T, int d, hipStream_t s);
 // Two rows of widths d0, d1 (<= 7168) in one launch, each as launch_rms_norm.
+// rms_norm of T tokens of 7168 (o, as launch_rms_norm) and the one-plane
+// activation planes of o for the grouped GEMMs (launch_xplanes, planes = 1).
+hipError_t launch_rms_norm_planes(const float* x, const float* w, float* o, int T, _Float16* xp, float* xs,
+                                  float* xe, hipStream_t s);
 hipError_t launch_rms_norm_pair(const float* x0, const float* w0, float* o0, int d0, const float* x1,
                                 const float* w1, float* o1, int d1, hipStream_t s);
 

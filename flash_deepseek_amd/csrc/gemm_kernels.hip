@@ -34,12 +34,12 @@
 // copied global -> LDS by direct loads into one of two buffers, so block
 // b + 1 streams in while block b is contracted.
 #include "fdm_internal.h"
+#include "planes_device.h"
 
 namespace fdm {
 
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
@@ -179,66 +179,42 @@ __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::
 }  // namespace
 
 // ---- activation planes ---------------------------------------------------------------
-// One workgroup per row of n_rows x [kd] fp32: s = the power of two that puts
-// the row's largest |x| in [2^13, 2^14), x' = x * 2^s split into P fp16
-// planes (round to nearest, each the rounding of what the previous planes
-// left), xs[sb] = the fp32 sum over the sub-block of the planes' values,
-// xe = 2^-s.  Planes: [P][n_rows][kd], each run of 8 elements stored in the
-// order 0 2 1 3 4 6 5 7 (the weight operand's order).
-template <int P>
-__global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, int kd, size_t n_rows,
+// Rows of KD fp32 into the planes (planes_device.h).  One thread per
+// 32-element sub-block holds it in registers: the row is read once, its
+// largest |x| reduced across the row's threads, then converted.  KD = 2048:
+// one wave per row, four rows per workgroup; KD = 7168: one workgroup per
+// row (224 of its 256 threads hold a sub-block).
+template <int P, int KD>
+__global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, size_t n_rows,
                                                  _Float16* __restrict__ xp, float* __restrict__ xs,
                                                  float* __restrict__ xe) {
+  constexpr int NSB = KD / 32;
+  constexpr int TPR = NSB <= 64 ? 64 : 256;  // threads per row
+  static_assert(NSB * 32 == KD && NSB <= TPR, "sub-blocks of a row fit its threads");
+  constexpr int RPB = 256 / TPR;
   __shared__ float red[4];
-  const size_t row = blockIdx.x;
-  const float* xr = x + row * kd;
+  const size_t row = (size_t)blockIdx.x * RPB + threadIdx.x / TPR;
+  const int sb = threadIdx.x % TPR;
+  const bool live = row < n_rows && sb < NSB;
+  f32x4 v[8];
   float m = 0.0f;
-  for (int i = threadIdx.x; i < kd; i += 256) m = fmaxf(m, fabsf(xr[i]));
+  if (live) {
+    const f32x4* src = reinterpret_cast<const f32x4*>(x + row * KD + 32 * sb);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = src[i];
+    m = subblock_absmax(v);
+  }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  const float amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int s = 0;
-  if (amax > 0.0f && amax <= 3.4028234e38f) {
-    int E;
-    (void)frexpf(amax, &E);  // amax in [2^(E-1), 2^E)
-    s = 14 - E;
+  if constexpr (TPR == 256) {
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   }
-  if (threadIdx.x == 0) xe[row] = ldexpf(1.0f, -s);
-  const int nsb = kd / 32;
-  for (int sb = threadIdx.x; sb < nsb; sb += 256) {
-    const f32x4* src = reinterpret_cast<const f32x4*>(xr + 32 * sb);
-    float sum = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      // 8 elements: one 16-byte store per plane
-      _Float16 h[P][8];
-#pragma unroll
-      for (int v = 0; v < 2; ++v) {
-        const f32x4 a = src[2 * q + v];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float r = ldexpf(a[e], s);
-          float tot = 0.0f;
-#pragma unroll
-          for (int p = 0; p < P; ++p) {
-            const _Float16 hp = (_Float16)r;
-            h[p][4 * v + e] = hp;
-            r -= (float)hp;
-            tot += (float)hp;
-          }
-          sum += tot;
-        }
-      }
-      // stored in the order 0 2 1 3 4 6 5 7 that the weight operand uses
-#pragma unroll
-      for (int p = 0; p < P; ++p)
-        *reinterpret_cast<f16x8*>(xp + ((size_t)p * n_rows + row) * kd + 32 * sb + 8 * q) =
-            (f16x8){h[p][0], h[p][2], h[p][1], h[p][3], h[p][4], h[p][6], h[p][5], h[p][7]};
-    }
-    xs[row * nsb + sb] = sum;
-  }
+  if (!live) return;
+  const int s = planes_shift(m);
+  if (sb == 0) xe[row] = ldexpf(1.0f, -s);
+  xs[row * NSB + sb] = planes_subblock<P>(v, s, xp + row * KD + 32 * sb, n_rows * KD);
 }
 
 // ---- the grouped GEMM ------------------------------------------------------------------
@@ -473,10 +449,20 @@ __global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(qg
 
 hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
                           hipStream_t s) {
-  if (planes == 3)
-    hipLaunchKernelGGL(k_xplanes<3>, dim3((unsigned)n_rows), dim3(256), 0, s, x, kd, n_rows, xp, xs, xe);
-  else
-    hipLaunchKernelGGL(k_xplanes<1>, dim3((unsigned)n_rows), dim3(256), 0, s, x, kd, n_rows, xp, xs, xe);
+  if (kd != kHidden && kd != kFfn) return hipErrorInvalidValue;
+  const dim3 blk(256);
+  const unsigned wide = (unsigned)n_rows, narrow = (unsigned)((n_rows + 3) / 4);
+  if (planes == 3) {
+    if (kd == kHidden)
+      hipLaunchKernelGGL((k_xplanes<3, kHidden>), dim3(wide), blk, 0, s, x, n_rows, xp, xs, xe);
+    else
+      hipLaunchKernelGGL((k_xplanes<3, kFfn>), dim3(narrow), blk, 0, s, x, n_rows, xp, xs, xe);
+  } else {
+    if (kd == kHidden)
+      hipLaunchKernelGGL((k_xplanes<1, kHidden>), dim3(wide), blk, 0, s, x, n_rows, xp, xs, xe);
+    else
+      hipLaunchKernelGGL((k_xplanes<1, kFfn>), dim3(narrow), blk, 0, s, x, n_rows, xp, xs, xe);
+  }
   return hipGetLastError();
 }
 
