@@ -402,8 +402,12 @@ __device__ __forceinline__ void q4k_group_dot_rows(const Q4KGroupLoad (&ld)[R], 
 //    N = 64 pieces, at ((block / 4) * 1792 + row / 4) * 2304.
 //  Inside a step (36 N bytes): the first 16 qs bytes of group g of each
 //  piece at 16 L, the last 16 at 16 N + 16 L, header dword g at 32 N + 4 L,
-//  where L = (row % R) * 16 + (block % 4) * 4 + g (R = 2 for gate / up, 4
-//  for down).  A Q6_K down matrix keeps the packed layout.
+//  where L = (block % 4) * 4 R + (row % R) * 4 + g (R = 2 rows for gate /
+//  up, 4 for down): one block of a step's rows fills whole 128-byte lines of
+//  q0 and of q1, so a kernel that walks the blocks one at a time (the
+//  grouped GEMMs) reads every line at once instead of half of it now and
+//  the other half a block later, after the L2 may have dropped it.  A Q6_K
+//  down matrix keeps the packed layout.
 constexpr int kRelGuPieces = 32;
 constexpr int kRelDnPieces = 64;
 
@@ -416,7 +420,7 @@ __device__ __forceinline__ const uint8_t* rel_step(const uint8_t* mat, int row, 
 
 template <bool DOWN>
 __device__ __forceinline__ int rel_piece(int row, int block, int g) {
-  return (row & (DOWN ? 3 : 1)) * 16 + (block & 3) * 4 + g;
+  return DOWN ? (block & 3) * 16 + (row & 3) * 4 + g : (block & 3) * 8 + (row & 1) * 4 + g;
 }
 
 // Group g of block `block` of row `row` of a REL matrix, by nontemporal loads.

@@ -49,7 +49,8 @@ constexpr int kQRowB = kQK * 2;       // LDS token row: one block of fp16 (512 B
 // gate and as many of up (SwiGLU pairs tile t with tile t + TL / 2), a down
 // GEMM TL tiles; every token operand read from LDS serves all of them.  Four
 // tiles for the fp32-grade gate/up (three planes: twice the weights per token
-// operand read, 238 VGPRs, 2 waves per SIMD), two elsewhere (3 waves per SIMD).
+// operand read, 252 VGPRs), two elsewhere (168 VGPRs for the three-plane down:
+// 3 waves per SIMD; 213-229 for one plane: 2 waves per SIMD, no spills).
 __host__ __device__ constexpr int qgemm_tiles(int planes, bool down) { return (planes == 3 && !down) ? 4 : 2; }
 __host__ __device__ constexpr int qgemm_rows(int tiles, bool down) {  // rows per workgroup (of gate for gate/up)
   return (down ? 16 : 8) * tiles * kQWaves;
@@ -61,10 +62,12 @@ struct QLane {
   u32x4 q0, q1, hdr;
 };
 
-// In the resident layout the q0 (and q1) pieces of blocks 2i and 2i + 1 of a
-// row share one 128-byte line: block 2i reads its half with the default
-// policy (the line stays in L2 for the next iteration), block 2i + 1 the
-// other half as its last use (nontemporal).
+// A block's q0 (and q1) pieces of a row pair (gate / up) or quad (down) fill
+// whole 128-byte lines of the resident layout, read once per chunk of the
+// expert.  Odd blocks are read with the nontemporal policy, even ones with
+// the default policy: measured a little faster than either policy for every
+// block (the default lines stay in the L2 for the expert's other chunks,
+// the streamed half leaves room).
 template <bool DOWN, bool LAST>
 __device__ __forceinline__ QLane qlane_load(const uint8_t* mat, int row, int block, int j) {
   constexpr int N = DOWN ? kRelDnPieces : kRelGuPieces;
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(256) void k_xplanes(const float* __restrict__ x, si
 
 // ---- the grouped GEMM ------------------------------------------------------------------
 template <int P, int NB, bool DOWN, int TL>
-__device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int* rows, int chunk, int rg) {
+__device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds0, uint8_t* lds1, int* rows, int chunk, int rg) {
   constexpr int KD = DOWN ? kFfn : kHidden;  // contraction length
   constexpr int NBLK = KD / kQK;             // 8 or 28 (even)
   constexpr int NT = 16 * NB;                // token rows per buffer and plane
@@ -257,18 +260,21 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
     }
   }
   // direct-load sources: round k of wave w fills LDS rows 2 (w + 8 k), +1 of
-  // the buffer (row rho = plane * NT + token); lane i: row rho0 + i / 32,
-  // slot i % 32 holds piece (i % 32) ^ (rho & 15) of that row's block
+  // the buffer (row rho = plane * NT + token t); lane i: row rho0 + i / 32,
+  // slot i % 32 holds piece (i % 32) ^ (t & 7) of that row's block.  The
+  // token operand's 16-byte reads (lane (c16, j): row c16, piece
+  // (8 j + m) ^ (c16 & 7)) are then free of bank conflicts; an XOR with all
+  // four bits of c16 measured twice the cycles per read (2-way conflicts).
   uint32_t src[ROUNDS];
 #pragma unroll
   for (int k = 0; k < ROUNDS; ++k) {
     const int rho = 2 * (wave + kQWaves * k) + (lane >> 5);
     const int p = rho / NT, t = rho - p * NT;
-    const uint32_t piece = (uint32_t)((lane & 31) ^ (t & 15));
+    const uint32_t piece = (uint32_t)((lane & 31) ^ (t & 7));
     src[k] = (uint32_t)((size_t)rin[t] * KD) + 8u * piece;  // element offset inside plane p
   }
   auto dma = [&](int b, int buf) {
-    uint8_t* base = lds + buf * BUF;
+    uint8_t* base = buf ? lds1 : lds0;
 #pragma unroll
     for (int k = 0; k < ROUNDS; ++k) {
       const int rho0 = 2 * (wave + kQWaves * k);
@@ -291,7 +297,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
   // One block: the token operands of an MFMA step are read from LDS once and
   // serve every tile, whose B operands are built per step.
   auto block = [&](int buf, const QLane (&w)[TL], const float2 (&xsv)[NB]) {
-    const uint8_t* base = lds + buf * BUF;
+    const uint8_t* base = buf ? lds1 : lds0;
     QScale sc[TL];
 #pragma unroll
     for (int t = 0; t < TL; ++t) sc[t] = qscale(w[t].hdr, sel);
@@ -305,7 +311,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
       const int i0 = 2 * (m & 1);
       if constexpr (TL == 2) {
         // both tiles' B operands first, then each token operand read once
-        // and used by both (the order that keeps two tiles at 3 waves per SIMD)
+        // and used by both
         const u32x4& qa = m < 2 ? w[0].q0 : w[0].q1;
         const u32x4& qb = m < 2 ? w[1].q0 : w[1].q1;
         const BPair B0 = build_b(qa[i0], qa[i0 + 1], sc[0].sc_lo, sc[0].sc16_hi, sc[0].off_hi);
@@ -315,8 +321,8 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 #pragma unroll
           for (int p = 0; p < P; ++p) {
             const uint8_t* r = base + (p * NT + 16 * nb + c16) * kQRowB;
-            const f16x8 alo = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ c16));
-            const f16x8 ahi = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ c16));
+            const f16x8 alo = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ (c16 & 7)));
+            const f16x8 ahi = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ (c16 & 7)));
             C[0][nb] = mfma_h(alo, B0.lo, C[0][nb]);
             C[1][nb] = mfma_h(alo, B1.lo, C[1][nb]);
             C[0][nb] = mfma_h(ahi, B0.hi, C[0][nb]);
@@ -331,8 +337,8 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 #pragma unroll
         for (int p = 0; p < P; ++p) {
           const uint8_t* r = base + (p * NT + 16 * nb + c16) * kQRowB;
-          alo[nb][p] = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ c16));
-          ahi[nb][p] = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ c16));
+          alo[nb][p] = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m) ^ (c16 & 7)));
+          ahi[nb][p] = *reinterpret_cast<const f16x8*>(r + 16 * ((8 * j + m + 4) ^ (c16 & 7)));
         }
 #pragma unroll
       for (int t = 0; t < TL; ++t) {
@@ -383,6 +389,10 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
     float2 xb[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) xb[nb] = load_xs(b + 1, nb);
+    // keep the next block's loads ahead of this block's contraction (the
+    // scheduler otherwise sinks them to just before the wait, to save
+    // registers, and the stream is no longer a block ahead)
+    __builtin_amdgcn_sched_barrier(0);
     block(0, wa, xa);
     const int b2 = min(b + 2, NBLK - 1);
     wait_vm();
@@ -391,6 +401,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
     load_w(wa, b2, false);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) xa[nb] = load_xs(b2, nb);
+    __builtin_amdgcn_sched_barrier(0);
     block(1, wb, xb);
   }
   wait_vm();  // the re-staged copy has landed before the LDS is released
@@ -427,7 +438,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds, int
 // An expert's weights are then read from HBM once per row group and served
 // from that XCD's L2 to its other chunks; every XCD does the same work.
 template <int P, int NB, bool DOWN>
-__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(qgemm_tiles(P, DOWN) == 4 ? 2 : 3))) void k_qgemm(QGemmArgs g) {
+__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(QGemmArgs g) {
   constexpr int TL = qgemm_tiles(P, DOWN);
   constexpr int RG = (DOWN ? kHidden : kFfn) / qgemm_rows(TL, DOWN);
   constexpr int Q = RG / 8;
@@ -439,12 +450,16 @@ __global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(qg
   const int off = k - Q * f;
   const int chunk = f + off % c, rg = 8 * (off / c) + xcd;
   constexpr int NT = 16 * NB;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * P * NT * kQRowB];
+  // two arrays, not one: the compiler then sees that the direct loads into
+  // one buffer cannot alias the reads of the other, and does not wait for
+  // them (with all outstanding loads) before the contraction
+  __shared__ __attribute__((aligned(16))) uint8_t lds0[P * NT * kQRowB];
+  __shared__ __attribute__((aligned(16))) uint8_t lds1[P * NT * kQRowB];
   __shared__ int rows[2 * NT];
   if (NB > 1 && g.chunks[chunk].z > 16)
-    qgemm_body<P, NB, DOWN, TL>(g, lds, rows, chunk, rg);
+    qgemm_body<P, NB, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
   else
-    qgemm_body<P, 1, DOWN, TL>(g, lds, rows, chunk, rg);
+    qgemm_body<P, 1, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
 }
 
 hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
