@@ -448,8 +448,9 @@ def main():
                     help="also time the single matvec, the single expert (Q4_K and Q6_K down) "
                          "and the Q6_K-down layer (0 to skip)")
     ap.add_argument("--pmc-workload", action="store_true",
-                    help="counter-collection run: a few layer steps, then plain 256 MiB "
-                         "copies (read + write of known size) that calibrate the counters")
+                    help="counter-collection run: a few layer steps, 8 batched-decode steps "
+                         "of 256 tokens, then plain 256 MiB copies (read + write of known size) "
+                         "that calibrate the counters")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -488,6 +489,16 @@ def main():
     if args.pmc_workload:
         for i in range(min(n_tok, 40)):
             step(i)
+        # batched decode at 256 tokens (the grouped GEMMs' traffic), 8 steps
+        # over the rotated layers, with each step's distinct-expert count
+        bT, bsteps = 256, 8
+        bX = make_tokens(bsteps * bT, 8356).reshape(bsteps, bT, HIDDEN)
+        bH = make_tokens(bsteps * bT, 8357).reshape(bsteps, bT, HIDDEN)
+        bY = torch.empty((bT, HIDDEN), dtype=torch.float32, device="cuda")
+        bnd = torch.zeros(bsteps, dtype=torch.int32, device="cuda")
+        for i in range(bsteps):
+            F.moe_forward_batched(3 + i % args.layers, bX[i], bH[i], bT, K, bY, n_distinct=bnd[i:i + 1],
+                                  stream=stream)
         n = COPY_BYTES // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -495,6 +506,8 @@ def main():
             torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes 256 MiB
         torch.cuda.synchronize()
         print(json.dumps({"pmc_workload": True, "layer_steps": min(n_tok, 40),
+                          "batched_T": bT, "batched_distinct_experts": bnd.tolist(),
+                          "expert_size": layers[0].expert_size,
                           "copy_bytes": COPY_BYTES, "copies": 3}), flush=True)
         return
 
