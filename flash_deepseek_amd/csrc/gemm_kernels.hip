@@ -427,8 +427,11 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds0, ui
   }
 }
 
-// NB: the largest token block count of a chunk; a chunk of <= 16 tokens
-// runs the one-block body.  One-dimensional grid, mapped so that all the
+// NB: the largest token block count of a chunk (1 for the 16-token chunks
+// of batched decode, 4 for the 64-token chunks of prefill); a chunk runs the
+// body of the fewest 16-token blocks that hold its tokens, so its weight
+// operands are built once for up to 64 tokens and no MFMA runs on an empty
+// block.  One-dimensional grid, mapped so that all the
 // chunks of one expert that share a row group run on the same XCD, back to
 // back: workgroups are handed to the eight XCDs in turn (id % 8), so
 // id -> (xcd = id % 8, k = id / 8); XCD x owns row groups x, x + 8, ...
@@ -456,10 +459,15 @@ __global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2)
   __shared__ __attribute__((aligned(16))) uint8_t lds0[P * NT * kQRowB];
   __shared__ __attribute__((aligned(16))) uint8_t lds1[P * NT * kQRowB];
   __shared__ int rows[2 * NT];
-  if (NB > 1 && g.chunks[chunk].z > 16)
-    qgemm_body<P, NB, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
-  else
-    qgemm_body<P, 1, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
+  const int n = g.chunks[chunk].z;
+  if constexpr (NB == 4) {
+    if (n > 48) return qgemm_body<P, 4, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
+    if (n > 32) return qgemm_body<P, 3, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
+  }
+  if constexpr (NB >= 2) {
+    if (n > 16) return qgemm_body<P, 2, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
+  }
+  qgemm_body<P, 1, DOWN, TL>(g, lds0, lds1, rows, chunk, rg);
 }
 
 hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Float16* xp, float* xs, float* xe,
@@ -481,7 +489,7 @@ hipError_t launch_xplanes(const float* x, int kd, size_t n_rows, int planes, _Fl
   return hipGetLastError();
 }
 
-int qgemm_chunk_tokens(int planes) { return planes == 3 ? 16 : 32; }
+int qgemm_chunk_tokens(int planes) { return planes == 3 ? 16 : 64; }
 
 hipError_t launch_qgemm(const QGemmArgs& g, int planes, bool down, int max_chunks, hipStream_t s) {
   const dim3 blk(kQWaves * 64);
@@ -494,9 +502,9 @@ hipError_t launch_qgemm(const QGemmArgs& g, int planes, bool down, int max_chunk
       hipLaunchKernelGGL((k_qgemm<3, 1, false>), grid, blk, 0, s, g);
   } else {
     if (down)
-      hipLaunchKernelGGL((k_qgemm<1, 2, true>), grid, blk, 0, s, g);
+      hipLaunchKernelGGL((k_qgemm<1, 4, true>), grid, blk, 0, s, g);
     else
-      hipLaunchKernelGGL((k_qgemm<1, 2, false>), grid, blk, 0, s, g);
+      hipLaunchKernelGGL((k_qgemm<1, 4, false>), grid, blk, 0, s, g);
   }
   return hipGetLastError();
 }
