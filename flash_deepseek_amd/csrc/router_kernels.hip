@@ -44,11 +44,12 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int q = 0; q < TPW; ++q) {
-    float v = acc[q];
+  for (int m = 32; m >= 1; m >>= 1)
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
-    if (lane == 0) red[wave][q] = v;
+    for (int q = 0; q < TPW; ++q) acc[q] = acc[q] + __shfl_xor(acc[q], m);
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < TPW; ++q) red[wave][q] = acc[q];
   }
   __syncthreads();
   if (threadIdx.x < TPW && t0 + (int)threadIdx.x < T) {
@@ -97,15 +98,20 @@ __global__ __launch_bounds__(256) void k_router_logits_blk(const float* __restri
     }
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // every logit's butterfly, one step at a time across all of them: the
+  // same adds in the same order per logit, but EPB * TPW independent lane
+  // exchanges in flight per step instead of one
 #pragma unroll
-  for (int k = 0; k < EPB; ++k) {
+  for (int m = 32; m >= 1; m >>= 1)
 #pragma unroll
-    for (int q = 0; q < TPW; ++q) {
-      float v = acc[k][q];
+    for (int k = 0; k < EPB; ++k)
 #pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) v = v + __shfl_xor(v, m);
-      if (lane == 0) red[wave][k][q] = v;
-    }
+      for (int q = 0; q < TPW; ++q) acc[k][q] = acc[k][q] + __shfl_xor(acc[k][q], m);
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < EPB; ++k)
+#pragma unroll
+      for (int q = 0; q < TPW; ++q) red[wave][k][q] = acc[k][q];
   }
   __syncthreads();
   if (threadIdx.x < EPB * TPW) {
