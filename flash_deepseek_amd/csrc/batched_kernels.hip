@@ -114,6 +114,9 @@ __device__ __forceinline__ int block_scan_excl(int v, int* wsum, int& tot) {
 // the shared expert's tokens in chunks of b.ch), all by block-wide scans.
 // The order of pairs inside a segment (LDS atomics) does not affect any
 // result: every pair's activations and output come from its own token only.
+// The first 256 kDispHeld pairs are loaded once, all at a time, and held in
+// registers for both passes (their loads no longer wait one by one).
+constexpr int kDispHeld = 16;
 __global__ __launch_bounds__(256) void k_dispatch(BatchArgs b) {
   __shared__ int cnt[kExperts];
   __shared__ int fill[kExperts];
@@ -123,8 +126,17 @@ __global__ __launch_bounds__(256) void k_dispatch(BatchArgs b) {
   const int e = threadIdx.x;
   cnt[e] = 0;
   fill[e] = 0;
+  int held[kDispHeld];
+#pragma unroll
+  for (int i = 0; i < kDispHeld; ++i) {
+    const int p = threadIdx.x + 256 * i;
+    held[i] = p < P ? b.idx[p] : -1;
+  }
   __syncthreads();
-  for (int p = threadIdx.x; p < P; p += 256) {
+#pragma unroll
+  for (int i = 0; i < kDispHeld; ++i)
+    if (held[i] >= 0 && held[i] < kExperts) atomicAdd(&cnt[held[i]], 1);
+  for (int p = threadIdx.x + 256 * kDispHeld; p < P; p += 256) {
     const int x = b.idx[p];
     if (x >= 0 && x < kExperts) atomicAdd(&cnt[x], 1);
   }
@@ -153,15 +165,20 @@ __global__ __launch_bounds__(256) void k_dispatch(BatchArgs b) {
     if (e == 0) *b.n_chunks = nr + ns;
   }
   __syncthreads();
-  for (int p = threadIdx.x; p < P; p += 256) {
-    const int x = b.idx[p];
+  auto place = [&](int p, int x) {
     int pos = -1;
     if (x >= 0 && x < kExperts) {
       pos = start[x] + atomicAdd(&fill[x], 1);
       b.pair_tok[pos] = p / b.K;
     }
     b.pair_of[p] = pos;  // -1: invalid expert id, contributes 0
+  };
+#pragma unroll
+  for (int i = 0; i < kDispHeld; ++i) {
+    const int p = threadIdx.x + 256 * i;
+    if (p < P) place(p, held[i]);
   }
+  for (int p = threadIdx.x + 256 * kDispHeld; p < P; p += 256) place(p, b.idx[p]);
 }
 
 // ---- grouped gate/up ----------------------------------------------------------------------
