@@ -541,6 +541,32 @@ __device__ __forceinline__ float q6k_half_dot_ld(const Q6KHalfLoad& r,
   return half_to_float(r.d) * q6k_half_dot(ql, qh, r.sc, xg, xg + 1);
 }
 
+// v of lane i + N of the same 16-lane row (DPP row_shl:N; 0 past the row).
+template <int N>
+__device__ __forceinline__ float dpp_row_shl(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + N, 0xF, 0xF, true));
+}
+
+// The sum of v over the 64 lanes of a wave, in lane 0: at each step m = 32,
+// 16, 8, 4, 2, 1 lane i < m adds lane i + m, so lane 0 adds exactly the pairs,
+// in the same order, that the xor butterfly v += shfl_xor(v, m) adds in its
+// lane 0 (the same bits).  m = 32 and 16 by v_permlane32_swap /
+// v_permlane16_swap (element 1 of the swap of v with itself holds lane i + 32
+// in lanes 0-31, lane i + 16 in lanes 0-15), the rest by DPP row shifts: VALU
+// only, no lane exchange through the LDS crossbar.  Other lanes hold partial
+// sums.
+__device__ __forceinline__ float wave_sum_lane0(float v) {
+  const uint32_t u32 = __float_as_uint(v);
+  v = v + __uint_as_float(__builtin_amdgcn_permlane32_swap(u32, u32, false, false)[1]);
+  const uint32_t u16 = __float_as_uint(v);
+  v = v + __uint_as_float(__builtin_amdgcn_permlane16_swap(u16, u16, false, false)[1]);
+  v = v + dpp_row_shl<8>(v);
+  v = v + dpp_row_shl<4>(v);
+  v = v + dpp_row_shl<2>(v);
+  v = v + dpp_row_shl<1>(v);
+  return v;
+}
+
 // Sum over the 16 lanes of a row group (lanes 16r..16r+15); every lane of
 // the group receives the total.
 __device__ __forceinline__ float sum16(float v) {

@@ -271,8 +271,7 @@ __device__ __forceinline__ void router_row(const LayerArgs& a, int e, LayerSmem&
     acc = fmaf(__uint_as_float(wv[i].z), xv[i].z, acc);
     acc = fmaf(__uint_as_float(wv[i].w), xv[i].w, acc);
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) acc = acc + __shfl_xor(acc, m);
+  acc = wave_sum_lane0(acc);  // the butterfly's lane-0 sum, VALU only
   if (lane == 0) sm.red[wave] = acc;
   __syncthreads();
   if (threadIdx.x == 0)

@@ -4,8 +4,9 @@
 // Exactness.  Indices must match the reference bit for bit, so the logits
 // are defined operation by operation: partial t of 256 accumulates float4
 // chunks t, t+256, ... with one fma per element; the partials are reduced
-// by an xor butterfly per wave and the four wave sums combined as
-// (s0 + s1) + (s2 + s3).  The C restatement (oracle) sums in this same
+// as by an xor butterfly per wave (lane 0 adds the same pairs in the same
+// order, through lane permutes and DPP shifts: wave_sum_lane0) and the four
+// wave sums combined as (s0 + s1) + (s2 + s3).  The C restatement (oracle) sums in this same
 // order.  route() itself is in route_device.h.
 #include "fdm_internal.h"
 #include "route_device.h"
@@ -44,9 +45,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const float* __restrict__
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1)
-#pragma unroll
-    for (int q = 0; q < TPW; ++q) acc[q] = acc[q] + __shfl_xor(acc[q], m);
+  for (int q = 0; q < TPW; ++q) acc[q] = wave_sum_lane0(acc[q]);
   if (lane == 0) {
 #pragma unroll
     for (int q = 0; q < TPW; ++q) red[wave][q] = acc[q];
@@ -98,15 +97,12 @@ __global__ __launch_bounds__(256) void k_router_logits_blk(const float* __restri
     }
   }
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  // every logit's butterfly, one step at a time across all of them: the
-  // same adds in the same order per logit, but EPB * TPW independent lane
-  // exchanges in flight per step instead of one
+  // every logit's butterfly sum into lane 0 (the same adds in the same
+  // order), without lane exchanges through the LDS crossbar
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1)
+  for (int k = 0; k < EPB; ++k)
 #pragma unroll
-    for (int k = 0; k < EPB; ++k)
-#pragma unroll
-      for (int q = 0; q < TPW; ++q) acc[k][q] = acc[k][q] + __shfl_xor(acc[k][q], m);
+    for (int q = 0; q < TPW; ++q) acc[k][q] = wave_sum_lane0(acc[k][q]);
   if (lane == 0) {
 #pragma unroll
     for (int k = 0; k < EPB; ++k)
