@@ -109,6 +109,32 @@ def test_batched_paths_agree(fdm, layer):
         assert rel_l2(outs[1][0][t], outs[0][0][t].astype(np.float64)) <= 1e-4, t
 
 
+def test_batched_unaligned_residual_and_output(fdm, layer, batch_kernel):
+    """h_in and hidden need no 16-byte alignment: the same step with both
+    pointers 4 bytes past an aligned address (the combine's one-value-per-
+    thread variant) gives the same bits as with aligned ones (its 16-byte
+    vector variant)."""
+    import torch
+    from flash_deepseek_amd.synthetic import make_tokens
+    L, _ = layer
+    T, K = 24, 8
+    X = make_tokens(T, 5150)
+    Hin = make_tokens(T, 5151).reshape(-1)
+    n = T * 7168
+    out_a = empty_f32(n)
+    say(f"moe_forward_batched L={L} T={T} aligned")
+    fdm.moe_forward_batched(L, X, Hin, T, K, out_a)
+    hbuf = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    hbuf[1:1 + n].copy_(Hin)
+    obuf = torch.zeros(n + 4, dtype=torch.float32, device="cuda")
+    h_off, o_off = hbuf[1:1 + n], obuf[1:1 + n]
+    assert h_off.data_ptr() % 16 != 0 and o_off.data_ptr() % 16 != 0
+    say(f"moe_forward_batched L={L} T={T} unaligned h_in / hidden")
+    fdm.moe_forward_batched(L, X, h_off, T, K, o_off)
+    assert np.array_equal(to_host(out_a).view(np.uint32), to_host(o_off).view(np.uint32))
+    assert float(obuf[0]) == 0.0 and float(obuf[1 + n]) == 0.0  # nothing written outside
+
+
 def test_batched_equals_single_token_layer(fdm, oracle, layer, batch_kernel):
     """Each token of a batch gets the same routing as fdm_moe_layer and an
     output within 1e-4 of it."""
