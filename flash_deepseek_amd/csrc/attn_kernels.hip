@@ -54,12 +54,14 @@ __device__ __forceinline__ float lane_sum(float v, int width) {
 }  // namespace
 
 // y[r] = (res ? res[r] : 0) + W[r] . x for rows r < rows; cols % 512 == 0,
-// cols <= 16384.  One wave per row (grid-stride), x staged in LDS.
+// cols <= 16384.  One wave per row (grid-stride), x staged in LDS (cols
+// floats of dynamic LDS: the narrow projections keep more workgroups per CU
+// than a fixed 64 KB would allow).
 __global__ __launch_bounds__(kMvWaves * 64) void k_mv_f16(const uint16_t* __restrict__ W,
                                                           const float* __restrict__ x,
                                                           const float* __restrict__ res,
                                                           float* __restrict__ y, int rows, int cols) {
-  __shared__ float xs[kMvMaxCols];  // 64 KB
+  extern __shared__ float xs[];  // cols floats
   for (int i = threadIdx.x; i < cols / 4; i += blockDim.x)
     reinterpret_cast<f32x4*>(xs)[i] = reinterpret_cast<const f32x4*>(x)[i];
   __syncthreads();
@@ -78,7 +80,7 @@ __global__ __launch_bounds__(kMvWaves * 64) void k_mv_f16(const uint16_t* __rest
       for (int i = 0; i < kMvBatch; ++i)
         if (b + i < chunks) acc = mv_dot8(w[i], xs + (b + i) * kMvChunk + 8 * lane, acc);
     }
-    acc = lane_sum(acc, 64);
+    acc = wave_sum_lane0(acc);  // the butterfly's lane-0 sum, VALU only
     if (lane == 0) y[r] = (res ? res[r] : 0.0f) + acc;
   }
 }
@@ -266,8 +268,11 @@ __global__ __launch_bounds__(256) void k_mla_wsum_reduce(const float* __restrict
 
 hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, float* y, int rows, int cols,
                          hipStream_t s) {
-  const int wgs = min((rows + kMvWaves - 1) / kMvWaves, 2 * g_num_cus);
-  k_mv_f16<<<wgs, kMvWaves * 64, 0, s>>>(W, x, res, y, rows, cols);
+  if (cols < 512 || cols % 512 != 0 || cols > kMvMaxCols) return hipErrorInvalidValue;
+  const size_t lds = (size_t)cols * sizeof(float);
+  const int per_cu = max(1, min(8, (int)((160u << 10) / lds)));  // workgroups per CU the LDS allows
+  const int wgs = min((rows + kMvWaves - 1) / kMvWaves, per_cu * g_num_cus);
+  k_mv_f16<<<wgs, kMvWaves * 64, lds, s>>>(W, x, res, y, rows, cols);
   return hipGetLastError();
 }
 
