@@ -105,7 +105,8 @@ __global__ __launch_bounds__(256) void k_mv_f16_heads(const uint16_t* __restrict
       const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + (size_t)r * cols + 8 * l));
       acc = mv_dot8(w, x + (size_t)h * x_stride + 8 * l, 0.0f);
     }
-    acc = lane_sum(acc, lpr);
+    // the group's butterfly sum into its first lane (the same bits), VALU only
+    acc = lpr == 64 ? wave_sum_lane0(acc) : group_sum_first<16>(acc);
     if (l == 0 && r < total) y[r] = acc;
   }
 }
@@ -278,6 +279,7 @@ hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, fl
 
 hipError_t launch_mv_f16_heads(const uint16_t* W, const float* x, int x_stride, float* y, int heads, int rows_h,
                                int cols, hipStream_t s) {
+  if (cols != 128 && cols != 512) return hipErrorInvalidValue;  // 16 or 64 lanes per row
   const int rows = heads * rows_h, rpw = 64 / (cols / 8);
   const int waves = (rows + rpw - 1) / rpw;
   const int wgs = min((waves + 3) / 4, 4 * g_num_cus);

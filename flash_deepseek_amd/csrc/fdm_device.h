@@ -547,6 +547,20 @@ __device__ __forceinline__ float dpp_row_shl(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x100 + N, 0xF, 0xF, true));
 }
 
+// Sum of v over an aligned group of L lanes (L = 2, 4, 8 or 16, inside one
+// 16-lane row) into the group's first lane by DPP row shifts: lane i adds
+// lane i + m, m = L/2 .. 1, so the first lane gets exactly what the xor
+// butterfly gives it (the same pairs, in the same order).
+template <int L>
+__device__ __forceinline__ float group_sum_first(float v) {
+  static_assert(L == 2 || L == 4 || L == 8 || L == 16, "a power of two inside a DPP row");
+  if constexpr (L >= 16) v = v + dpp_row_shl<8>(v);
+  if constexpr (L >= 8) v = v + dpp_row_shl<4>(v);
+  if constexpr (L >= 4) v = v + dpp_row_shl<2>(v);
+  v = v + dpp_row_shl<1>(v);
+  return v;
+}
+
 // The sum of v over the 64 lanes of a wave, in lane 0: at each step m = 32,
 // 16, 8, 4, 2, 1 lane i < m adds lane i + m, so lane 0 adds exactly the pairs,
 // in the same order, that the xor butterfly v += shfl_xor(v, m) adds in its
