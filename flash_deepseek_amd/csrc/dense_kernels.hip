@@ -68,11 +68,9 @@ __device__ __forceinline__ float dot8(u32x4 w, f32x4 x0, f32x4 x1, float acc) {
   return acc;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-  return v;
-}
+// The xor butterfly's lane-0 sum (the same bits), through lane permutes and
+// DPP shifts; only lane 0 reads it.
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_lane0(v); }
 
 }  // namespace
 
