@@ -581,15 +581,11 @@ __device__ __forceinline__ float wave_sum_lane0(float v) {
   return v;
 }
 
-// Sum over the 16 lanes of a row group (lanes 16r..16r+15); every lane of
-// the group receives the total.
-__device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 8);
-  v += __shfl_xor(v, 4);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 1);
-  return v;
-}
+// Sum over the 16 lanes of a row group (lanes 16r..16r+15) into the group's
+// first lane (lane 16r), the value the xor butterfly over 8, 4, 2, 1 gives it
+// (group_sum_first); the other lanes hold partial sums, so callers read the
+// first lanes only.
+__device__ __forceinline__ float sum16(float v) { return group_sum_first<16>(v); }
 
 // Cross-workgroup hand-off inside one kernel (arrival counters).  The few
 // values handed over are written with agent-scope stores (written through
