@@ -840,7 +840,10 @@ int fdm_stream_sync(void* stream) {
     FDM_HIP(hipMemcpy(&err, w->layer_flags + kLayerFlagErr * kLayerStride, sizeof(err),
                       hipMemcpyDeviceToHost));
     if (w->epochs.new_error(err))
-      return fail(FDM_E_STATE, "fdm_moe_layer call %u timed out inside the kernel", err);
+      return fail(FDM_E_STATE,
+                  "a bounded wait inside a one-launch kernel (batch-1 layer, expert FFN or matvec) gave up "
+                  "in the call of epoch %u on this stream",
+                  err);
   }
   return FDM_OK;
 }
@@ -926,6 +929,7 @@ void layer_workspace_args(LayerArgs& a, Workspace* ws) {
   a.route_perm = tg + 256 + 32;
   a.act = tg + 256 + 48;
   a.eo = a.act + (size_t)kLayerMaxSlots * FDM_MOE_FFN;
+  a.act_xd = a.eo + (size_t)kLayerMaxSlots * kLayerMaxParts * FDM_HIDDEN;
   a.norm_inv = tg + kLayerTagged - 16;  // its own 128-byte line
   a.counters = ws->layer_cnt;
   a.flags = ws->layer_flags;
@@ -1364,6 +1368,10 @@ int fdm_moe_layer(int L, const float* d_h_post, const float* d_h_in, int K, floa
 int fdm_moe_layer_norm(int L, const float* d_h, const float* d_norm_w, int K, float* d_hidden,
                        float* d_h_post, int* d_idx, float* d_w, void* stream) {
   if (!d_norm_w) return fail(FDM_E_INVAL, "null norm weight");
+  // the norm item writes h_post while router rows and digit items may still
+  // read h: an h_post that overlaps h would feed them normalised values
+  if (d_h_post && d_h && d_h_post < d_h + FDM_HIDDEN && d_h < d_h_post + FDM_HIDDEN)
+    return fail(FDM_E_INVAL, "h_post must not overlap h");
   return run_layer(L, d_h, d_norm_w, d_h_post, d_h, K, d_hidden, d_idx, d_w, stream);
 }
 

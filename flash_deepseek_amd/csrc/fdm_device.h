@@ -55,6 +55,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  if (__builtin_constant_p(c) && c == 0) {
+    // the first product of a chain: the three-operand form with an inline
+    // zero accumulator (the compiler otherwise picks the two-operand
+    // accumulating form and first moves 0 into its destination)
+    int r;
+    __asm__("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+  }
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 

@@ -106,9 +106,12 @@ constexpr int kLayerFlags = 4;                   // digits ready, -, error, -
 constexpr int kLayerFlagErr = 2;                 // flag slot of the timed-out epoch
 constexpr int kLayerMaxParts = 8;               // down matrices split in <= 8 column parts
 // tagged words: scores 256, prov 16, route_w 16, route_perm 16,
-// act 17 x 2048, eo 17 x 8 x 7168 (per-part down outputs)
-constexpr size_t kLayerTagged =
-    256 + 3 * 16 + (size_t)kLayerMaxSlots * (2048 + (size_t)kLayerMaxParts * 7168) + 16;  // + the rms line
+// act 17 x 2048, eo 17 x 8 x 7168 (per-part down outputs), act_xd 17 x 32 x 52
+// (the words of the activations' digit records)
+constexpr size_t kLayerActXdWords = (size_t)kLayerMaxSlots * 32 * (sizeof(XGroup) / 4);
+constexpr size_t kLayerTagged = 256 + 3 * 16 +
+                                (size_t)kLayerMaxSlots * (2048 + (size_t)kLayerMaxParts * 7168) +
+                                kLayerActXdWords + 16;  // + the rms line
 struct LayerArgs {
   const float* Wg;         // router weights [256][7168] fp32
   const float* bias;       // [256] or null
@@ -135,6 +138,7 @@ struct LayerArgs {
   uint64_t* route_perm;    // tagged: slot running the k-th expert of that order [K]
   uint64_t* act;           // tagged: [kLayerMaxSlots][2048]
   uint64_t* eo;            // tagged: [kLayerMaxSlots][kLayerMaxParts][7168] down partial sums
+  uint64_t* act_xd;        // tagged: [kLayerMaxSlots][32][52] words of the activations' digit records
   int* counters;           // kLayerCounters x kLayerStride ints, zero at first use
   unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
   unsigned epoch;          // non-zero, different from every earlier call's

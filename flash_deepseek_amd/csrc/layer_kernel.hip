@@ -15,20 +15,25 @@
 //   digits of h_post (28: four 64-element groups each)
 //   router row e (256)
 //   route: the expert set (1);  the exact route() (1)
-//   shared expert: gate/up items of every column part, then its down parts
-//   routed experts, part-major: gate/up items of part q of every slot,
-//     then the down items of part q - lag of every slot, q = 0, 1, ...
-//   combine tiles (224)
+//   shared expert: gate/up items of both column parts, then the digit
+//     records of its activations (one item per part)
+//   routed experts, part-major: gate/up items of part q of every slot and
+//     the digit records of part q of every slot, then the down items of
+//     part q - lag of every slot, q = 0, 1, ...
+//   final items: the shared expert's down rows and the combine of the
+//     same rows (224)
 //
-// Every down matrix is split into column parts (2 by default): down part p
-// of a slot needs only the slot's activations of part p, so the downs of
-// part 0 stream alongside the gate/up items of part 1 instead of waiting
-// for the slot's last activation.  The combine sums a slot's parts in part
-// order.  (Measured on MI355X: 2 parts beat 1, 4 and 8; finer parts read
-// 144-byte row slices that share 64-byte sectors with the neighbour part.)
-// (The shared expert's gate/up items request their weights before they
-// wait for the digits: they fill the front of the launch while the router
-// rows, the route and -- with the fused rms_norm -- the norm are in flight.)
+// Every routed down matrix is split into two column parts: down part p of a
+// slot needs only the slot's activations of part p, so the downs of part 0
+// stream alongside the gate/up items of part 1 instead of waiting for the
+// slot's last activation.  A slot's expert output is its part sums added in
+// part order.  (Measured on MI355X: 2 parts, lag 1 beat 1, 4 and 8 parts and
+// lags 0 and 2.)  The shared expert's down rows are the last bytes of the
+// list: its activations are ready long before, so the final items contract
+// them while the last routed down items finish, then combine.  (The shared
+// expert's gate/up items request their weights before they wait for the
+// digits: they fill the front of the launch while the router rows, the
+// route and -- with the fused rms_norm -- the norm are in flight.)
 //
 // Items only wait for items earlier in the list, and a waiting item has
 // already issued every weight load it can (down tiles load their weights
@@ -46,9 +51,23 @@
 // therefore TAGGED: a 64-bit word {epoch, payload} written with one
 // agent-scope store and read with agent-scope loads; the reader's load is
 // its own readiness check (tag == this call's epoch), the writer never
-// waits, and nothing is ever cleared.  Only the 16 KB digit record of
+// waits, and nothing is ever cleared.  Only the 23 KB digit record of
 // h_post is published untagged, behind a flag set by the last of its 28
 // producers, and staged with 16-byte coherent loads.
+//
+// Memory ordering.  Every hand-off is a relaxed agent-scope store read by
+// relaxed agent-scope loads; there is no release/acquire pair.  What makes
+// a tagged word safe is that payload and tag are one 64-bit store, which
+// the memory system performs as a single access: a reader that sees the
+// tag sees the payload written with it.  The untagged digit record relies
+// on two properties of gfx950's memory pipeline instead: a wave's stores
+// are complete (acknowledged by the coherence point) once s_waitcnt has
+// counted them down, which the producers wait for before they bump the
+// arrival counter, and a wave's loads return in issue order, so the
+// readers' record loads, issued after the flag load saw the epoch, cannot
+// return data older than the flag.  The agent-scope (sc1) cache policy of
+// all these accesses bypasses the non-coherent per-XCD caches, so no stale
+// line of an earlier launch is read.
 #include "fdm_internal.h"
 #include "rms_device.h"
 #include "route_device.h"
@@ -85,16 +104,17 @@ constexpr int kGuPerPart = kPartCols / kGuTileRows / kGuPer;  // gate/up items p
 static_assert(kGuPerPart * kGuTileRows * kGuPer == kPartCols, "gate/up items tile a part");
 // Q4_K down item: one lane per 64-element group of a row's part, kDnRowsQ4L
 // rows per lane.  Q6_K down item: one lane per 128-element half block.
+#ifndef FDM_LAYER_DNROWS
+#define FDM_LAYER_DNROWS 7
+#endif
 constexpr int kDnLanesQ4 = kPartGroups;                     // lanes per row
-constexpr int kDnRowsQ4L = 7;                               // rows per lane
+constexpr int kDnRowsQ4L = FDM_LAYER_DNROWS;                // rows per lane
 constexpr int kDnRowsQ4 = 4 * kDnRowsQ4L * (64 / kDnLanesQ4);  // rows per item (448)
 constexpr int kDnLanesQ6 = kPartCols / 128;
 constexpr int kDnRowsQ6L = 2;
 constexpr int kDnRowsQ6 = 4 * kDnRowsQ6L * (64 / kDnLanesQ6);  // 256
 static_assert(kHidden % kDnRowsQ4 == 0 && kHidden % kDnRowsQ6 == 0, "down items tile the rows");
 __host__ __device__ constexpr int dn_per_part(bool q6) { return kHidden / (q6 ? kDnRowsQ6 : kDnRowsQ4); }
-constexpr int kCombRows = 32;                // rows per combine tile
-constexpr int kCombTiles = kHidden / kCombRows;       // 224
 
 // flag and counter slots (units of kStride)
 constexpr int kFlagXd = 0;
@@ -104,7 +124,11 @@ constexpr int kCntXd = 0;
 struct LayerSmem {
   union {
     XGroup xs[kHidden / 64];  // digits of h_post (gate/up) or of a part's activations (down)
-    float part[kLayerMaxSlots][kParts][kCombRows];  // combine: per-part down outputs
+    struct {
+      XGroup xs[kFfn / 64];                          // the shared activations' digit records
+      float v[2 * (kLayerMaxSlots - 1) * 32];        // the routed part outputs of the item's rows
+      float esh[32];                                 // the shared expert's output of each row
+    } fin;                                           // final items
     RmsSmem rms;              // the fused rms_norm (router rows and digit items)
   };
   float red[4];
@@ -424,41 +448,87 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
   }
 }
 
-// ---- down item: rows of one column part of one slot's down matrix --------------------
-// Part p covers columns kPartCols p .. kPartCols (p+1) - 1.  The weights are
-// loaded before the part's tagged activations (one per thread at 8 parts)
-// are waited for and turned into digits in LDS; each row's partial sum goes
-// out tagged into eo[slot][p][row].
-//  Q4_K: kDnLanesQ4 lanes per row (one 64-element group each), lane row
-//        group rr = lane / kDnLanesQ4, rows rr + 16 j (j < 7) at 8 parts.
-//  Q6_K: kDnLanesQ6 lanes per row (one 128-element half block each).
-template <bool Q6, bool PACKED>
-__device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part, int item,
-                                          bool routed, LayerSmem& sm) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (routed) wait_route_xd(a, slot, true, false, sm);
-  const uint8_t* blob = routed ? expert_blob(a, sm.eid) : a.shared;
-  const uint8_t* dbase = blob ? blob + 2 * (size_t)kGateBytes : nullptr;
+// ---- activation digits of one (slot, part) --------------------------------------------
+// Every down item of a slot's part contracts against the digit records of the
+// same 1024 activations, so they are made once, here, instead of once per
+// down item: the item waits for the part's tagged activations, turns them
+// into kPartGroups records in LDS and publishes the records' 32-bit words as
+// tagged words (act_xd[slot][group][word]); the down items stage them with
+// their own loads, whose tags are their readiness check.
+constexpr int kXgWords = (int)sizeof(XGroup) / 4;            // 52 words per record
+constexpr int kPartXdWords = kPartGroups * kXgWords;         // words of a part's records
+__device__ __forceinline__ uint64_t* act_xd_words(const LayerArgs& a, int slot, int group) {
+  return a.act_xd + ((size_t)slot * (kFfn / 64) + group) * kXgWords;
+}
+
+__device__ __forceinline__ void adg_item(const LayerArgs& a, int slot, int part, LayerSmem& sm) {
+  const int wave = threadIdx.x >> 6;
   const uint64_t* act = a.act + (size_t)slot * kFfn + part * kPartCols;
-  uint64_t* eo = a.eo + ((size_t)slot * kLayerMaxParts + part) * kHidden;
-  auto stage_act = [&] {
-    constexpr int kPer = kPartCols / 256;
-    float v[kPer];
-    poll_all(a, [&] {
-      bool ok = true;
+  constexpr int kPer = kPartCols / 256;
+  float v[kPer];
+  poll_all(a, [&] {
+    bool ok = true;
 #pragma unroll
-      for (int i = 0; i < kPer; ++i) {
-        const uint64_t t = get_tagged(act + threadIdx.x + 256 * i);
+    for (int i = 0; i < kPer; ++i) {
+      const uint64_t t = get_tagged(act + threadIdx.x + 256 * i);
+      ok = ok && tag_is(t, a.epoch);
+      v[i] = tagged_f(t);
+    }
+    return ok;
+  });
+  // element 256 i + 64 w + lane lives in wave w's lanes: record 4 i + w
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) digits_to_lds(v[i], sm.xs[4 * i + wave]);
+  __syncthreads();
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(sm.xs);
+  uint64_t* dst = act_xd_words(a, slot, part * kPartGroups);
+  for (int i = threadIdx.x; i < kPartXdWords; i += 256) put_tagged(dst + i, a.epoch, src[i]);
+}
+
+// The records of `n_groups` consecutive groups of a slot's activations into
+// sm.xs[0 ..): every thread loads its words (after the caller's weight loads,
+// so the first poll returns with them) until all carry this call's tag.
+template <int NG>
+__device__ __forceinline__ void stage_act_digits(const LayerArgs& a, int slot, int group0, LayerSmem& sm) {
+  constexpr int kW = NG * kXgWords, kPer = (kW + 255) / 256;
+  const uint64_t* src = act_xd_words(a, slot, group0);
+  uint32_t w[kPer];
+  poll_all(a, [&] {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int k = threadIdx.x + 256 * i;
+      if (k < kW) {
+        const uint64_t t = get_tagged(src + k);
         ok = ok && tag_is(t, a.epoch);
-        v[i] = tagged_f(t);
+        w[i] = (uint32_t)t;
       }
-      return ok;
-    });
-    // element 256 i + 64 w + lane lives in wave w's lanes: record 4 i + w
+    }
+    return ok;
+  });
+  uint32_t* dst = reinterpret_cast<uint32_t*>(sm.xs);
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) digits_to_lds(v[i], sm.xs[4 * i + wave]);
-    __syncthreads();
-  };
+  for (int i = 0; i < kPer; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    if (k < kW) dst[k] = w[i];
+  }
+  __syncthreads();
+}
+
+// ---- down item: rows of one column part of one routed slot's down matrix --------------
+// Part p covers columns kPartCols p .. kPartCols (p+1) - 1.  The weights are
+// loaded before the part's digit records are waited for and staged; each
+// row's partial sum goes out tagged into eo[slot][p][row] for the final items.
+//  Q4_K: kDnLanesQ4 lanes per row (one 64-element group each), lane row
+//        group rr = lane / kDnLanesQ4, rows rr + 4 j (j < kDnRowsQ4L).
+//  Q6_K: kDnLanesQ6 lanes per row (one 128-element half block each).
+template <bool Q6>
+__device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part, int item, LayerSmem& sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  wait_route_xd(a, slot, true, false, sm);
+  const uint8_t* blob = expert_blob(a, sm.eid);
+  const uint8_t* dbase = blob ? blob + 2 * (size_t)kGateBytes : nullptr;
+  uint64_t* eo = a.eo + ((size_t)slot * kLayerMaxParts + part) * kHidden;
   if (!Q6) {
     constexpr int LR = kDnLanesQ4, RPW = 64 / LR;
     const int gl = lane % LR;  // group of the row's part
@@ -468,14 +538,12 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
     if (blob) {
       // resident expert layout: a wave's load (4 rows x one block quad) reads one 1 KB run
 #pragma unroll
-      for (int j = 0; j < kDnRowsQ4L; ++j)
-        ld[j] = PACKED ? q4k_load_group(dbase + (size_t)(row0 + RPW * j) * kQ4KRowFfn + (size_t)blk * kQ4KBlock, gl & 3)
-                       : rel_load_group<true>(dbase, row0 + RPW * j, blk, gl & 3);
+      for (int j = 0; j < kDnRowsQ4L; ++j) ld[j] = rel_load_group<true>(dbase, row0 + RPW * j, blk, gl & 3);
     }
-    stage_act();
+    stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
     float acc[kDnRowsQ4L] = {};
-    // the lane's seven rows share one digit record: each quarter of it is
-    // read from LDS once for all seven
+    // the lane's rows share one digit record: each quarter of it is read
+    // from LDS once for all of them
     if (blob) q4k_group_dot_rows<kDnRowsQ4L>(ld, q4k_scale_sel(gl & 3), &sm.xs[gl], acc);
 #pragma unroll
     for (int j = 0; j < kDnRowsQ4L; ++j) {
@@ -493,10 +561,9 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
     if (blob) {
 #pragma unroll
       for (int j = 0; j < kDnRowsQ6L; ++j)
-        l6[j] = q6k_load_half(dbase + (size_t)(row0 + RPW * j) * kQ6KRowFfn + (H >> 1) * kQ6KBlock,
-                              H & 1);
+        l6[j] = q6k_load_half(dbase + (size_t)(row0 + RPW * j) * kQ6KRowFfn + (H >> 1) * kQ6KBlock, H & 1);
     }
-    stage_act();
+    stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
     float acc[kDnRowsQ6L] = {};
     if (blob) {
 #pragma unroll
@@ -517,73 +584,207 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
   }
 }
 
-// ---- combine tile: rows 32*tile .. 32*tile+31 ------------------------------------------
-// Thread (part p = t / 32, row r = t % 32) waits for every slot's part-p
-// output of its row; the parts of a slot are summed p = 0, 1, ... in LDS;
-// then the routed experts are summed in the reference's slot order and the
-// shared expert and the residual added.
-__device__ __forceinline__ void combine_tile(const LayerArgs& a, int tile, LayerSmem& sm) {
-  const int rr = threadIdx.x & (kCombRows - 1), p = threadIdx.x / kCombRows;
-  const int r = tile * kCombRows + rr;
-  const bool mine = p < kParts;
-  // the residual is read before the waits, so its load is not queued behind them
-  const float hin = (threadIdx.x < kCombRows && a.h_in) ? a.h_in[r] : 0.0f;
-  float v[kLayerMaxSlots];
-  poll_all(a, [&] {
-    if (!mine) return true;
-    bool ok = true;
+// ---- final item: the shared expert's down rows and the combine of the same rows ----------
+// The last items of the list.  Each takes kFinRows rows of the output: it
+// loads the shared expert's down rows (both column parts) first, stages the
+// shared activations' digit records and, with the same loads, the routed
+// slots' tagged part outputs of its rows and the exact route, contracts the
+// shared rows (part sums by the butterflies the down items use, so the same
+// bits), and writes
+//   hidden[r] = (h_in[r] + sum_k w[k] (E_perm[k][r] part 0 + part 1)) + S[r]
+// in the reference's slot order (infer.m:1689-1695, 1922).  Its weights are
+// the last bytes of the list, and the combine needs no further hand-off: the
+// routed outputs it polls were published while these weights streamed.
+//  Q4_K: 32 rows; lane (bq = lane / 16, rs = lane / 4 % 4, g = lane % 4) of
+//        wave w holds rows 8 w + 4 m + rs (m < 2), block quad bq of both
+//        parts (blocks bq and 4 + bq), group g: a wave's load is one resident
+//        layout step (4 rows x 4 blocks).
+//  Q6_K: 32 rows; lane (rr = lane / 16, H = lane % 16) of wave w holds rows
+//        8 w + rr + 4 j (j < 2), half block H (part H / 8).
+static_assert(kParts == 2, "final items: two column parts");
+constexpr int kFinRowsQ4 = 32, kFinRowsQ6 = 32;
+__host__ __device__ constexpr int fin_rows(bool q6) { return q6 ? kFinRowsQ6 : kFinRowsQ4; }
+__host__ __device__ constexpr int fin_items(bool q6) { return kHidden / fin_rows(q6); }
+constexpr int kFinMaxRouted = kLayerMaxSlots - 1;             // routed slots (FDM_MAX_K)
+constexpr int kFinWordsMax = 2 * kFinMaxRouted * kFinRowsQ4;  // routed part outputs of one item
+static_assert(kFinRowsQ4 >= kFinRowsQ6, "LDS of the final items sized for the Q4_K rows");
+
+template <bool Q6, bool PACKED>
+__device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSmem& sm) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int R = fin_rows(Q6);
+  const int r0 = item * R;
+  const bool has_shared = a.n_slots > a.K;
+  const uint8_t* dbase = (has_shared && a.shared) ? a.shared + 2 * (size_t)kGateBytes : nullptr;
+  // the residual first, so its load is not queued behind the waits
+  const float hin = (threadIdx.x < R && a.h_in) ? a.h_in[r0 + threadIdx.x] : 0.0f;
+  // weights of the shared rows
+  constexpr int kQ4M = kFinRowsQ4 / 16;  // Q4_K rows per lane
+  const int g = lane & 3, rs = (lane >> 2) & 3, bq = lane >> 4;
+  const int H = lane & 15, rr = lane >> 4;
+  Q4KGroupLoad ld0[kQ4M], ld1[kQ4M];
+  Q6KHalfLoad l6[2];
+  if (dbase) {
+    if (!Q6) {
 #pragma unroll
-    for (int s = 0; s < kLayerMaxSlots; ++s) {
-      if (s < a.n_slots) {
-        const uint64_t t = get_tagged(a.eo + ((size_t)s * kLayerMaxParts + p) * kHidden + r);
-        ok = ok && tag_is(t, a.epoch);
-        v[s] = tagged_f(t);
+      for (int m = 0; m < kQ4M; ++m) {
+        const int row = r0 + 4 * kQ4M * wave + 4 * m + rs;
+        if (PACKED) {
+          ld0[m] = q4k_load_group(dbase + (size_t)row * kQ4KRowFfn + (size_t)bq * kQ4KBlock, g);
+          ld1[m] = q4k_load_group(dbase + (size_t)row * kQ4KRowFfn + (size_t)(4 + bq) * kQ4KBlock, g);
+        } else {
+          ld0[m] = rel_load_group<true>(dbase, row, bq, g);
+          ld1[m] = rel_load_group<true>(dbase, row, 4 + bq, g);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int row = r0 + 8 * wave + rr + 4 * j;
+        l6[j] = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (H >> 1) * kQ6KBlock, H & 1);
       }
     }
+  }
+  // the shared activations' records (both parts) are waited for; the routed
+  // part outputs of the item's rows and the exact route are loaded by the
+  // same polls (the first returns with the weights) and waited for only
+  // after the shared rows are contracted
+  constexpr int kXW = (kFfn / 64) * kXgWords, kXPer = (kXW + 255) / 256;
+  constexpr int kEPer = (kFinWordsMax + 255) / 256;
+  const int nE = 2 * a.K * R;  // word e: slot e / (2 R), part e / R % 2, row e % R
+  const uint64_t* xsrc = act_xd_words(a, a.K, 0);
+  uint32_t xw[kXPer];
+  float ev[kEPer];
+  uint64_t tw = 0, tp = 0;
+  bool e_ok = true;
+  auto load_routed = [&] {
+    e_ok = true;
+#pragma unroll
+    for (int i = 0; i < kEPer; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      if (e < nE) {
+        const int s = e / (2 * R), p = (e / R) & 1, r = e % R;
+        const uint64_t t = get_tagged(a.eo + ((size_t)s * kLayerMaxParts + p) * kHidden + r0 + r);
+        e_ok = e_ok && tag_is(t, a.epoch);
+        ev[i] = tagged_f(t);
+      }
+    }
+    if (threadIdx.x < a.K) {
+      tw = get_tagged(a.route_w + threadIdx.x);
+      tp = get_tagged(a.route_perm + threadIdx.x);
+      e_ok = e_ok && tag_is(tw, a.epoch) && tag_is(tp, a.epoch);
+    }
+    return e_ok;
+  };
+  auto store_routed = [&] {
+#pragma unroll
+    for (int i = 0; i < kEPer; ++i) {
+      const int e = threadIdx.x + 256 * i;
+      if (e < nE) sm.fin.v[e] = ev[i];
+    }
+    if (threadIdx.x < a.K) {
+      sm.cw[threadIdx.x] = tagged_f(tw);
+      sm.cperm[threadIdx.x] = tagged_i(tp);
+    }
+  };
+  poll_all(a, [&] {
+    bool ok = true;
+    if (dbase) {
+#pragma unroll
+      for (int i = 0; i < kXPer; ++i) {
+        const int k = threadIdx.x + 256 * i;
+        if (k < kXW) {
+          const uint64_t t = get_tagged(xsrc + k);
+          ok = ok && tag_is(t, a.epoch);
+          xw[i] = (uint32_t)t;
+        }
+      }
+    }
+    load_routed();
     return ok;
   });
-  // the exact route is finished long before the last expert output; its
-  // weights and slot permutation go to LDS from the loads that checked them
-  uint64_t tw = 0, tp = 0;
-  poll_all(a, [&] {
-    if (threadIdx.x >= a.K) return true;
-    tw = get_tagged(a.route_w + threadIdx.x);
-    tp = get_tagged(a.route_perm + threadIdx.x);
-    return tag_is(tw, a.epoch) && tag_is(tp, a.epoch);
-  });
-  if (threadIdx.x < a.K) {
-    sm.cw[threadIdx.x] = tagged_f(tw);
-    sm.cperm[threadIdx.x] = tagged_i(tp);
-  }
-  if (mine) {
+  uint32_t* xdst = reinterpret_cast<uint32_t*>(sm.fin.xs);
 #pragma unroll
-    for (int s = 0; s < kLayerMaxSlots; ++s)
-      if (s < a.n_slots) sm.part[s][p][rr] = v[s];
+  for (int i = 0; i < kXPer; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    if (dbase && k < kXW) xdst[k] = xw[i];
+  }
+  store_routed();
+  const bool routed_ready = __syncthreads_and(e_ok);
+  // the shared rows: part sums p0, p1 by the butterflies of the down items
+  if (!Q6) {
+    float acc0[kQ4M] = {}, acc1[kQ4M] = {};
+    if (dbase) {
+      const Q4KScaleSel sel = q4k_scale_sel(g);
+      q4k_group_dot_rows<kQ4M>(ld0, sel, &sm.fin.xs[4 * bq + g], acc0);
+      q4k_group_dot_rows<kQ4M>(ld1, sel, &sm.fin.xs[16 + 4 * bq + g], acc1);
+    }
+#pragma unroll
+    for (int m = 0; m < kQ4M; ++m) {
+      // group index within the part = 4 bq + g: its bits 3, 2, 1, 0 are lane
+      // bits 5, 4, 1, 0 (the down items' xor 8, 4, 2, 1)
+      float p0 = acc0[m], p1 = acc1[m];
+      p0 += __shfl_xor(p0, 32);
+      p1 += __shfl_xor(p1, 32);
+      p0 += __shfl_xor(p0, 16);
+      p1 += __shfl_xor(p1, 16);
+      p0 += __shfl_xor(p0, 2);
+      p1 += __shfl_xor(p1, 2);
+      p0 += __shfl_xor(p0, 1);
+      p1 += __shfl_xor(p1, 1);
+      if ((lane & 0x33) == 0) sm.fin.esh[4 * kQ4M * wave + 4 * m + rs] = p0 + p1;
+    }
+  } else {
+    float acc[2] = {};
+    if (dbase) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        int gi = 2 * H;
+        __asm__ volatile("" : "+v"(gi));
+        acc[j] = q6k_half_dot_ld(l6[j], &sm.fin.xs[gi]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      // half block within the part = H % 8: the down items' xor 4, 2, 1
+      float v = acc[j];
+      v += __shfl_xor(v, 4);
+      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 1);
+      const float p1 = __shfl_xor(v, 8);  // lanes of part 0 receive part 1's sum
+      if ((lane & 15) == 0) sm.fin.esh[8 * wave + rr + 4 * j] = v + p1;
+    }
+  }
+  if (!routed_ready) {
+    poll_all(a, load_routed);
+    store_routed();
   }
   __syncthreads();
-  if (threadIdx.x >= kCombRows) return;
-  auto expert_out = [&](int s) {
-    float e = sm.part[s][0][rr];
-#pragma unroll
-    for (int q = 1; q < kParts; ++q) e += sm.part[s][q][rr];
-    return e;
-  };
+  if (threadIdx.x >= R) return;
+  const int r = threadIdx.x;
   float moe = 0.0f;
-  for (int k = 0; k < a.K; ++k) moe = fmaf(sm.cw[k], expert_out(sm.cperm[k]), moe);
-  const float sd = a.n_slots > a.K ? expert_out(a.K) : 0.0f;
-  a.out[r] = (hin + moe) + sd;
-  if (a.moe_out) a.moe_out[r] = moe;
+  for (int k = 0; k < a.K; ++k) {
+    const int s = sm.cperm[k];
+    const float e = sm.fin.v[(2 * s) * R + r] + sm.fin.v[(2 * s + 1) * R + r];
+    moe = fmaf(sm.cw[k], e, moe);
+  }
+  const float sd = has_shared ? sm.fin.esh[r] : 0.0f;
+  a.out[r0 + r] = (hin + moe) + sd;
+  if (a.moe_out) a.moe_out[r0 + r] = moe;
 }
 
 // First workgroup of each section of the work list:
 //   (with a norm weight: the fused rms_norm) | digits | router rows
 //   | route set | exact route
-//   | shared expert: gate/up of parts 0..P-1, then down of parts 0..P-1
+//   | shared expert: gate/up of parts 0..P-1, then its activation digits (P)
 //   | routed experts, part-major: step q holds gate/up of part q of every
-//     slot (q < P), then down of part q - lag of every slot (q >= lag)
-//   | combine tiles
+//     slot and then the activation digits of part q of every slot (q < P),
+//     then down of part q - lag of every slot (q >= lag)
+//   | final items (shared down + combine)
 struct LayerList {
-  int route, exact, router, xd, shared, routed, comb, total;
+  int route, exact, router, xd, shared, shadg, routed, fin, total;
   int gup, dnp;  // gate/up and down items per (slot, part)
 };
 
@@ -600,17 +801,19 @@ __host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, boo
   l.route = l.router + (expert ? 0 : kRows);
   l.exact = l.route + (expert ? 0 : 1);
   l.shared = l.exact + (expert ? 0 : 1);
-  l.routed = l.shared + hs * kParts * (l.gup + l.dnp);
-  l.comb = l.routed + K * kParts * (l.gup + l.dnp);
-  l.total = l.comb + kCombTiles;
+  l.shadg = l.shared + hs * kParts * l.gup;
+  l.routed = l.shadg + hs * kParts;
+  l.fin = l.routed + K * kParts * (l.gup + 1 + l.dnp);
+  l.total = l.fin + fin_items(q6);
   return l;
 }
 
-// Routed item `off` (0-based within the routed section): gate/up (dn = false,
-// idx = gate/up item) or down (dn = true, idx = down item) of (slot, part).
-__device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, bool& dn, int& slot,
+// Routed item `off` (0-based within the routed section): kind 0 gate/up
+// (idx = gate/up item), 1 activation digits, 2 down (idx = down item) of
+// (slot, part).
+__device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, int& kind, int& slot,
                                             int& part, int& idx) {
-  const int G = K * l.gup, D = K * l.dnp;
+  const int GU = K * l.gup, G = GU + K, D = K * l.dnp;
   int q, r;
   if (off < kLag * G) {
     q = off / G;
@@ -624,13 +827,18 @@ __device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, 
     q = kParts + o / D;
     r = G + o % D;  // a step past the last gate/up part holds down items only
   }
-  dn = r >= G && q >= kLag;
-  if (q >= kParts) dn = true;
-  if (!dn) {
+  if (r < GU) {
+    kind = 0;
     part = q;
     slot = r / l.gup;
     idx = r % l.gup;
+  } else if (r < G) {
+    kind = 1;
+    part = q;
+    slot = r - GU;
+    idx = 0;
   } else {
+    kind = 2;
     part = q - kLag;
     slot = (r - G) / l.dnp;
     idx = (r - G) % l.dnp;
@@ -655,22 +863,22 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
     route_item(a);
   } else if (!EXPERT && it == l.exact) {
     exact_item(a);
-  } else if (it < l.routed) {
+  } else if (it < l.shadg) {
     const int off = it - l.shared;
-    if (off < kParts * l.gup)
-      gateup_run<EXPERT>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, false, sm);
-    else
-      down_part<Q6, EXPERT>(a, a.K, (off - kParts * l.gup) / l.dnp, (off - kParts * l.gup) % l.dnp, false, sm);
-  } else if (!EXPERT && it < l.comb) {
-    bool dn;
-    int slot, part, idx;
-    routed_item(l, a.K, it - l.routed, dn, slot, part, idx);
-    if (!dn)
+    gateup_run<EXPERT>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, false, sm);
+  } else if (it < l.routed) {
+    adg_item(a, a.K, it - l.shadg, sm);
+  } else if (!EXPERT && it < l.fin) {
+    int kind, slot, part, idx;
+    routed_item(l, a.K, it - l.routed, kind, slot, part, idx);
+    if (kind == 0)
       gateup_run<false>(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, true, sm);
+    else if (kind == 1)
+      adg_item(a, slot, part, sm);
     else
-      down_part<Q6, false>(a, slot, part, idx, true, sm);
+      down_part<Q6>(a, slot, part, idx, sm);
   } else {
-    combine_tile(a, it - l.comb, sm);
+    final_item<Q6, EXPERT>(a, it - l.fin, sm);
   }
 }
 

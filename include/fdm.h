@@ -267,7 +267,9 @@ int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, floa
  *   d_hidden = d_h + sum_k w[k] E_k(h_post) + S(h_post),
  *   h_post = rms_norm(d_h, d_norm_w), bit-exact with infer.m:369-374.
  * d_h, d_norm_w: [7168] fp32, 16-byte aligned; d_hidden may alias d_h;
- * d_h_post (optional) receives h_post.  Routing, results and the rules for
+ * d_h_post (optional) receives h_post and must not overlap d_h (FDM_E_INVAL:
+ * the kernel writes it while other workgroups still read d_h).  Routing,
+ * results and the rules for
  * overlapping calls are fdm_moe_layer's on that h_post. */
 int fdm_moe_layer_norm(int L, const float *d_h, const float *d_norm_w, int K, float *d_hidden,
                        float *d_h_post, int *d_idx, float *d_w, void *stream);

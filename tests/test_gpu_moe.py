@@ -200,3 +200,19 @@ def test_moe_layer_norm_fused(fdm, oracle, layer, scale, tok):
     hio = hd.clone()
     fdm.moe_layer_norm(L, hio, nwd, K, hio)
     assert np.array_equal(to_host(hio).view(np.uint32), to_host(hid_ref).view(np.uint32))
+
+
+def test_moe_layer_norm_rejects_h_post_overlapping_h(fdm, layer):
+    """The norm item writes h_post while router rows and digit items still
+    read h, so an h_post that overlaps h is rejected before any launch."""
+    from flash_deepseek_amd._lib import FDM_E_INVAL
+    L, _ = layer
+    buf = empty_f32(2 * 7168)
+    nw = empty_f32(7168).fill_(1.0)
+    h = buf[:7168]
+    hid = empty_f32(7168)
+    for off in (0, 7167):  # the same buffer, and the last element of h under the first of h_post
+        with pytest.raises(fdm.FdmError) as err:
+            fdm.moe_layer_norm(L, h, nw, 8, hid, buf[off:off + 7168])
+        assert err.value.code == FDM_E_INVAL
+    fdm.sync()

@@ -5,7 +5,10 @@ shapes, so the outputs, the routing and the distinct-expert count must be
 bit-identical.  Two no-allocation calls run back to back, the second with
 fewer tokens (and on the digit-kernel path, T < FDM_BATCH_MFMA_MIN_T), so
 a leftover of the first call in the shared scratch would show; sizes past
-the scratch's limits are rejected."""
+the scratch's limits are rejected.  That the call allocates nothing is
+checked by capturing it into a HIP graph on a fresh stream in global
+capture mode, where any allocation (a workspace for that stream included)
+is refused and invalidates the capture."""
 import numpy as np
 import pytest
 
@@ -41,6 +44,48 @@ def step(fdm, fn, L, X, H, T):
     nd = torch.zeros(1, dtype=torch.int32, device="cuda")
     fn(L, X, H, T, K, out, idx, w, nd)
     return out, idx, w, nd
+
+
+@pytest.mark.parametrize("T", [8, 3], ids=["mfma_path", "dot4_path"])
+def test_noalloc_captures_in_a_graph(fdm, layer, T):
+    """The property the entry point exists for: it allocates nothing.  The
+    call is captured into a HIP graph on a fresh stream in global capture
+    mode (hipMalloc, and so a stream workspace, is refused there and the
+    capture fails).  Each replay, with eager work and synchronisations
+    between replays, equals the eager fdm_moe_forward_batched bit for bit."""
+    import torch
+    L = layer
+    X, H = tokens(T, 43 + T)
+    say(f"moe_forward_batched (eager reference) L={L} T={T}")
+    want = [to_host(t) for t in step(fdm, fdm.moe_forward_batched, L, X, H, T)]
+    fdm.sync()
+    out = empty_f32(T * 7168)
+    idx = torch.empty(T * K, dtype=torch.int32, device="cuda")
+    w = empty_f32(T * K)
+    nd = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    say(f"capturing moe_forward_batched_noalloc L={L} T={T} on a fresh stream")
+    with torch.cuda.graph(g, stream=s, capture_error_mode="global"):
+        fdm.moe_forward_batched_noalloc(L, X, H, T, K, out, idx, w, nd, stream=s.cuda_stream)
+    for r in range(3):
+        # eager work on the outputs between replays: a replay must rewrite all of them
+        out.fill_(float("nan"))
+        idx.fill_(-1)
+        w.fill_(float("nan"))
+        nd.fill_(-1)
+        torch.cuda.synchronize()
+        say(f"replay {r} L={L} T={T}")
+        g.replay()
+        torch.cuda.synchronize()
+        got = [to_host(t) for t in (out, idx, w, nd)]
+        assert np.array_equal(got[1], want[1]), f"replay {r}: routed ids differ"
+        assert bits_equal_nan_class(got[2], want[2]), f"replay {r}: routing weights differ"
+        assert int(got[3][0]) == int(want[3][0])
+        assert bits_equal_nan_class(got[0], want[0]), \
+            f"replay {r}: max |diff| {np.abs(got[0] - want[0]).max()}"
+    fdm.sync(s.cuda_stream)
 
 
 def test_noalloc_matches_batched(fdm, layer):
