@@ -60,14 +60,14 @@
 // a tagged word safe is that payload and tag are one 64-bit store, which
 // the memory system performs as a single access: a reader that sees the
 // tag sees the payload written with it.  The untagged digit record relies
-// on two properties of gfx950's memory pipeline instead: a wave's stores
-// are complete (acknowledged by the coherence point) once s_waitcnt has
-// counted them down, which the producers wait for before they bump the
-// arrival counter, and a wave's loads return in issue order, so the
-// readers' record loads, issued after the flag load saw the epoch, cannot
-// return data older than the flag.  The agent-scope (sc1) cache policy of
-// all these accesses bypasses the non-coherent per-XCD caches, so no stale
-// line of an earlier launch is read.
+// on the store counter instead: a wave's stores are complete (acknowledged
+// by the coherence point) once s_waitcnt has counted them down, which every
+// producer waits for before it bumps the arrival counter; the last arrival
+// then sets the flag, and a reader issues its record loads only after its
+// flag load has returned the epoch, so they cannot observe the record
+// before its stores completed.  The agent-scope (sc1) cache policy of all
+// these accesses bypasses the non-coherent per-XCD caches, so no stale line
+// of an earlier launch is read.
 #include "fdm_internal.h"
 #include "rms_device.h"
 #include "route_device.h"
