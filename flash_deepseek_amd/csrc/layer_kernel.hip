@@ -376,9 +376,8 @@ __device__ __forceinline__ void exact_item(const LayerArgs& a) {
 // 32-63 up, 16 lanes per row); SwiGLU in registers; the activations go out
 // tagged.  The route and the digits of h_post are waited for and staged
 // once per run, so their round trips are paid once for kGuPer tiles.
-template <bool PACKED>
-__device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int tile0, bool routed,
-                                           LayerSmem& sm) {
+template <bool PACKED, bool ROUTED>
+__device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int tile0, LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
   // The digit record (23 KB, every gate/up item reads all of it): all of a
@@ -404,40 +403,41 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
   // A routed slot waits for its expert (and the digits), requests the digit
   // record and then the weights, so the record lands first and each weight
   // group is used as soon as it arrives.  The shared expert's weights are
-  // requested before the digits are waited for.
-  if (routed) {
+  // requested before the digits are waited for.  The loads are issued on
+  // every path (an invalid expert id reads the layer's first expert and
+  // contributes 0), so the code is straight-line and the LDS stores of the
+  // record wait for the record's loads only, not for the weights behind it.
+  if (ROUTED) {
     wait_route_xd(a, slot, true, true, sm);
     load_xd();
   }
-  const uint8_t* blob = routed ? expert_blob(a, sm.eid) : a.shared;
+  const uint8_t* blob = ROUTED ? expert_blob(a, sm.eid) : a.shared;
+  const uint8_t* src = blob ? blob : a.experts;
   const Q4KScaleSel sel = q4k_scale_sel(g);
   for (int t = 0; t < kGuPer; ++t) {
     const int row = (tile0 + t) * kGuTileRows + 2 * wave + (q & 1);
     Q4KGroupLoad ld[7];
-    if (blob) {
-      // resident expert layout: each half-wave load reads one 512-byte run;
-      // packed layout (a caller's blob): 16-byte slices of the row's blocks
-      const uint8_t* mat = blob + (q >= 2 ? kGateBytes : 0);
+    // resident expert layout: each half-wave load reads one 512-byte run;
+    // packed layout (a caller's blob): 16-byte slices of the row's blocks
+    const uint8_t* mat = src + (q >= 2 ? kGateBytes : 0);
 #pragma unroll
-      for (int i = 0; i < 7; ++i)
-        ld[i] = PACKED ? q4k_load_group(mat + (size_t)row * kQ4KRowHidden + (size_t)(4 * i + (l16 >> 2)) * kQ4KBlock, g)
-                       : rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
-    }
+    for (int i = 0; i < 7; ++i)
+      ld[i] = PACKED ? q4k_load_group(mat + (size_t)row * kQ4KRowHidden + (size_t)(4 * i + (l16 >> 2)) * kQ4KBlock, g)
+                     : rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     if (t == 0) {
-      if (!routed) {
+      if (!ROUTED) {
         wait_route_xd(a, slot, false, true, sm);
         load_xd();
       }
       store_xd();
     }
     float acc = 0.0f;
-    if (blob) {
 #pragma unroll
-      for (int i = 0; i < 7; ++i) {
-        acc += q4k_group_dot_ld(ld[i], sel, &sm.xs[16 * i + l16]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    for (int i = 0; i < 7; ++i) {
+      acc += q4k_group_dot_ld(ld[i], sel, &sm.xs[16 * i + l16]);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    if (!blob) acc = 0.0f;
     acc = sum16(acc);
     const float up = __shfl(acc, (lane + 32) & 63);
     if (lane == 0 || lane == 16) {
@@ -865,14 +865,14 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
     exact_item(a);
   } else if (it < l.shadg) {
     const int off = it - l.shared;
-    gateup_run<EXPERT>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, false, sm);
+    gateup_run<EXPERT, false>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, sm);
   } else if (it < l.routed) {
     adg_item(a, a.K, it - l.shadg, sm);
   } else if (!EXPERT && it < l.fin) {
     int kind, slot, part, idx;
     routed_item(l, a.K, it - l.routed, kind, slot, part, idx);
     if (kind == 0)
-      gateup_run<false>(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, true, sm);
+      gateup_run<false, true>(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, sm);
     else if (kind == 1)
       adg_item(a, slot, part, sm);
     else
