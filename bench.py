@@ -139,6 +139,35 @@ def cpu_baseline(down, seconds, K=8):
     return ref, tuned
 
 
+def bench_read_ceiling(F, torch, args, stream, K, h_post, h_in):
+    """Per step: fdm_layer_read_ceiling over the step's rotated layer with K
+    distinct seeded expert ids; wall time per step (back-to-back launches, as
+    the headline) and the per-launch HIP-event average."""
+    rng = np.random.default_rng(4321)
+    n = args.warmup + args.steps
+    ids = np.stack([rng.choice(256, K, replace=False) for _ in range(n)]).astype(np.int32)
+    d_ids = torch.from_numpy(ids).cuda()
+    sink = torch.empty(HIDDEN, dtype=torch.int32, device="cuda")
+    run = lambda i: F.layer_read_ceiling(3 + i % args.layers, d_ids[i], K, h_post[i], h_in[i], sink,
+                                         stream=stream)
+    for i in range(args.warmup):
+        run(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.warmup, n):
+        run(i)
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / args.steps * 1e6
+    F.prof_enable(True)
+    F.prof_reset()
+    for i in range(args.warmup, n):
+        run(i)
+    torch.cuda.synchronize()
+    cnt, tot, mn, mx = F.prof_read("ceiling")
+    F.prof_enable(False)
+    return {"us_per_step": round(us, 2), "kernel_avg_us": round(tot / max(cnt, 1) * 1e3, 2)}
+
+
 def bench_matvec(F, torch, args, n_sets=64, calls=256):
     """Config 0: y = W x for a Q4_K W [2048 x 7168] (the dequant_matvec_q4k
     of one gate matrix) over n_sets distinct weight sets (> the 256 MB
@@ -539,6 +568,12 @@ def main():
     step_us = event_times(torch, lambda i: step(args.warmup + i), args.prof_steps)
     F.sync(stream)
 
+    # the streaming ceiling of the same bytes: one dependency-free launch per
+    # step that reads what the step's layer launch reads (router, 8 routed
+    # experts -- distinct seeded ids per step --, the shared expert, h_post,
+    # h_in) with the layer kernel's load policy, nothing else
+    ceiling = bench_read_ceiling(F, torch, args, stream, K, h_post, h_in)
+
     lb = layer_bytes(args.down, K)
     k_us = phases["layer"]["avg_us"]
     achieved = lb / (k_us * 1e-6) / 1e9 if k_us > 0 else 0.0
@@ -581,6 +616,15 @@ def main():
             "traffic_source": ("HBM bytes per launch from the rocprofv3 FETCH_SIZE + WRITE_SIZE passes "
                                "committed in profiles/ (traffic.json), not measured in this run"),
             "bytes_per_launch": lb,
+            "stream_ceiling": {
+                "kernel": "k_read_ceiling (fdm_layer_read_ceiling): the same bytes per launch, "
+                          "16-byte nontemporal loads, 64 KB per workgroup, no route / hand-off / math",
+                "us_per_step": ceiling["us_per_step"],
+                "kernel_avg_us": ceiling["kernel_avg_us"],
+                "gbps": round(lb / (ceiling["kernel_avg_us"] * 1e-6) / 1e9, 1),
+                "frac": round(lb / (ceiling["kernel_avg_us"] * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                "layer_kernel_over_ceiling": round(k_us / ceiling["kernel_avg_us"], 3),
+            },
         },
         "cpu_baseline": None,
     }

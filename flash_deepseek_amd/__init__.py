@@ -206,6 +206,15 @@ def moe_layer_norm(L, h, norm_w, K, hidden, h_post=None, idx=None, w=None, strea
          _stream(stream))
 
 
+def layer_read_ceiling(L, idx, K, h_post, h_in, sink, stream=None):
+    """Measurement only: read exactly the bytes one moe_layer launch on layer
+    L reads (router, the K routed experts idx (device int32), the shared
+    expert, h_post, h_in) with the layer kernel's load policy, and nothing
+    else; sink (7168 int32/uint32) receives words whose XOR is the XOR of every
+    32-bit word read."""
+    call("fdm_layer_read_ceiling", L, _p(idx), K, _p(h_post), _p(h_in), _p(sink), _stream(stream))
+
+
 def moe_forward_batched(L, X, H_in, T, K, hidden, idx=None, w=None, n_distinct=None,
                         stream=None):
     """T tokens through the MoE branch of layer L in one step, each selected
@@ -342,7 +351,7 @@ def dense_ffn(L, h_post, h_in, hidden, stream=None):
 PHASES = {"router": _lib.PROF_ROUTER, "gateup": _lib.PROF_GATEUP, "down": _lib.PROF_DOWN,
           "xdigits": _lib.PROF_XDIGITS, "matvec": _lib.PROF_MATVEC, "layer": _lib.PROF_LAYER,
           "batch": _lib.PROF_BATCH, "prefill": _lib.PROF_PREFILL, "dense": _lib.PROF_DENSE,
-          "attn": _lib.PROF_ATTN}
+          "attn": _lib.PROF_ATTN, "ceiling": _lib.PROF_CEILING}
 
 
 def prof_enable(on=True):

@@ -20,7 +20,7 @@ FDM_E_IO = -7
 FDM_E_FORMAT = -8
 
 (PROF_ROUTER, PROF_GATEUP, PROF_DOWN, PROF_XDIGITS, PROF_MATVEC, PROF_LAYER, PROF_BATCH,
- PROF_PREFILL, PROF_DENSE, PROF_ATTN) = range(10)
+ PROF_PREFILL, PROF_DENSE, PROF_ATTN, PROF_CEILING) = range(11)
 
 QK_K = 256
 Q4K_BLOCK_SIZE = 144
@@ -97,6 +97,7 @@ SIGNATURES = {
     "fdm_moe_forward_host": [_i, _vp, _vp, _vp, _i, _vp],
     "fdm_moe_layer": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp],
     "fdm_moe_layer_norm": [_i, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp],
+    "fdm_layer_read_ceiling": [_i, _vp, _i, _vp, _vp, _vp, _vp],
     "fdm_moe_forward_batched": [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp],
     "fdm_moe_forward_batched_noalloc": [_i, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp],
     "fdm_rms_norm": [_vp, _vp, _vp, _i, _i, _vp],

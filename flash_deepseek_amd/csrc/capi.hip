@@ -1375,6 +1375,50 @@ int fdm_moe_layer_norm(int L, const float* d_h, const float* d_norm_w, int K, fl
   return run_layer(L, d_h, d_norm_w, d_h_post, d_h, K, d_hidden, d_idx, d_w, stream);
 }
 
+// ---- the streaming ceiling of a batch-1 layer's bytes (measurement only) --------------------
+int fdm_layer_read_ceiling(int L, const int* d_idx, int K, const float* d_h_post, const float* d_h_in,
+                           uint32_t* d_sink, void* stream) {
+  Layer* y = nullptr;
+  if (int rc = get_layer(L, &y)) return rc;
+  if (int rc = check_K(K)) return rc;
+  if (!d_idx || !d_h_post || !d_sink) return fail(FDM_E_INVAL, "null pointer");
+  if (!aligned(d_h_post, 16) || (d_h_in && !aligned(d_h_in, 16)))
+    return fail(FDM_E_INVAL, "h_post / h_in must be 16-byte aligned");
+  ReadCeilArgs a{};
+  int n = 0, tiles = 0;
+  auto add = [&](const void* p, size_t b) {
+    a.seg[n] = static_cast<const uint8_t*>(p);
+    a.bytes[n] = b;
+    a.tile0[n] = tiles;
+    tiles += read_ceiling_tiles(b);
+    ++n;
+  };
+  add(y->Wg, (size_t)FDM_N_EXPERTS * FDM_HIDDEN * sizeof(float));
+  if (y->bias) add(y->bias, FDM_N_EXPERTS * sizeof(float));
+  a.first_routed = n;
+  for (int k = 0; k < K; ++k) add(nullptr, y->expert_size);
+  if (y->shared) add(y->shared, y->expert_size);
+  add(d_h_post, FDM_HIDDEN * sizeof(float));
+  if (d_h_in) add(d_h_in, FDM_HIDDEN * sizeof(float));
+  a.tile0[n] = tiles;
+  if (tiles > FDM_HIDDEN)
+    return fail(FDM_E_INVAL, "K=%d: %d tiles exceed the %d-word sink", K, tiles, FDM_HIDDEN);
+  a.n_seg = n;
+  a.K = K;
+  a.n_tiles = tiles;
+  a.experts = y->experts;
+  a.expert_size = y->expert_size;
+  a.n_experts = y->n_experts;
+  a.idx = d_idx;
+  a.sink = d_sink;
+  hipStream_t s = as_stream(stream);
+  {
+    ProfScope p(FDM_PROF_CEILING, s);
+    FDM_HIP(launch_read_ceiling(a, s));
+  }
+  return FDM_OK;
+}
+
 // ---- batched decode ---------------------------------------------------------------------
 }  // extern "C"
 

@@ -149,6 +149,26 @@ struct LayerArgs {
 constexpr unsigned kLayerSpinLimit = 1u << 17;  // polls of one wait (each >= ~1 us)
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
 
+// read_ceiling.hip: the batch-1 layer's bytes read with the layer kernel's
+// load policy and nothing else (the streaming ceiling of those bytes).
+// Segment s covers tiles tile0[s] .. tile0[s + 1] - 1 of 64 KB; segments
+// first_routed .. first_routed + K - 1 are the routed experts idx[k]
+// (device ids, resolved in the kernel).
+constexpr int kReadCeilMaxSeg = 4 + 1 + 16;
+struct ReadCeilArgs {
+  const uint8_t* seg[kReadCeilMaxSeg];
+  size_t bytes[kReadCeilMaxSeg];
+  int tile0[kReadCeilMaxSeg + 1];
+  int n_seg, first_routed, K, n_tiles;
+  const uint8_t* experts;
+  size_t expert_size;
+  int n_experts;   // an id outside 0 .. n_experts - 1 reads expert 0
+  const int* idx;
+  uint32_t* sink;  // [7168]
+};
+int read_ceiling_tiles(size_t bytes);
+hipError_t launch_read_ceiling(const ReadCeilArgs& a, hipStream_t s);
+
 // batched_kernels.hip
 // Batched decode of T tokens through one layer with token -> expert
 // dispatch (each selected expert's weights read once per step).  Routing

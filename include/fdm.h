@@ -274,6 +274,21 @@ int fdm_moe_layer(int L, const float *d_h_post, const float *d_h_in, int K, floa
 int fdm_moe_layer_norm(int L, const float *d_h, const float *d_norm_w, int K, float *d_hidden,
                        float *d_h_post, int *d_idx, float *d_w, void *stream);
 
+/* ---- the streaming ceiling of a batch-1 layer's bytes (measurement only; no
+ * counterpart in the reference).  One dependency-free launch that reads
+ * exactly the bytes one fdm_moe_layer launch on layer L reads -- the router
+ * weights and bias, the K routed experts d_idx[0..K) (device ints; an id
+ * outside the layer reads expert 0), the shared expert, d_h_post and d_h_in
+ * (may be NULL) -- with that kernel's load policy (16-byte nontemporal loads,
+ * 64 KB per workgroup, four workgroups per CU), and writes FDM_HIDDEN words
+ * to d_sink whose XOR is the XOR of every 32-bit word read.  No route, no
+ * hand-off, no math: its time against fdm_moe_layer's separates the device's
+ * streaming ceiling for these bytes from the kernel's own losses.
+ * FDM_E_INVAL when the bytes exceed FDM_HIDDEN tiles of 64 KB (K = 16 with a
+ * Q6_K down). */
+int fdm_layer_read_ceiling(int L, const int *d_idx, int K, const float *d_h_post, const float *d_h_in,
+                           uint32_t *d_sink, void *stream);
+
 /* ---- the polls one wait inside fdm_moe_layer's kernel makes before it gives
  * up (no counterpart in the reference, whose Metal waits are host-side,
  * infer.m:1681).  0 restores the default (2^17 polls of >= ~1 us each).  A
@@ -450,7 +465,8 @@ int fdm_dense_ffn(int L, const float *d_h_post, const float *d_h_in, float *d_hi
 #define FDM_PROF_PREFILL 7  /* fdm_moe_prefill: all layers              */
 #define FDM_PROF_DENSE 8    /* fdm_dense_ffn: both launches             */
 #define FDM_PROF_ATTN 9     /* fdm_attn_forward: the whole token        */
-#define FDM_PROF_PHASES 10
+#define FDM_PROF_CEILING 10 /* fdm_layer_read_ceiling                   */
+#define FDM_PROF_PHASES 11
 int fdm_prof_enable(int on);
 int fdm_prof_reset(void);
 int fdm_prof_read(int phase, int *count, double *total_ms, double *min_ms, double *max_ms);

@@ -216,3 +216,29 @@ def test_moe_layer_norm_rejects_h_post_overlapping_h(fdm, layer):
             fdm.moe_layer_norm(L, h, nw, 8, hid, buf[off:off + 7168])
         assert err.value.code == FDM_E_INVAL
     fdm.sync()
+
+
+def test_layer_read_ceiling_reads_the_layer_bytes(fdm, layer):
+    """fdm_layer_read_ceiling (the streaming-ceiling launch of the bench)
+    reads exactly the bytes one layer launch reads: the XOR of its sink equals
+    the XOR of every 32-bit word of the router weights and bias, the K routed
+    experts' packed blobs (the resident layout permutes whole 32-bit words, so
+    the XOR is the same), the shared expert, h_post and h_in."""
+    import torch
+    L, lay = layer
+    ids = np.array([3, 250, 17, 17, 99, 0, 128, 255], np.int32)  # a repeated id is read twice
+    h = np.random.default_rng(71).standard_normal(7168).astype(np.float32)
+    h_in = np.random.default_rng(72).standard_normal(7168).astype(np.float32)
+    sink = torch.zeros(7168, dtype=torch.int32, device="cuda")
+    say(f"layer_read_ceiling L={L} K={len(ids)}")
+    fdm.layer_read_ceiling(L, to_dev(ids), len(ids), to_dev(h), to_dev(h_in), sink)
+    got = int(np.bitwise_xor.reduce(to_host(sink).view(np.uint32)))
+
+    def xor32(a):
+        return int(np.bitwise_xor.reduce(np.ascontiguousarray(a).view(np.uint32).ravel()))
+
+    want = xor32(to_host(lay.Wg)) ^ xor32(to_host(lay.bias)) ^ xor32(lay.expert_bytes(-1))
+    want ^= xor32(h) ^ xor32(h_in)
+    for e in ids:
+        want ^= xor32(lay.expert_bytes(int(e)))
+    assert got == want, (hex(got), hex(want))
