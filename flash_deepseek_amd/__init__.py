@@ -210,8 +210,8 @@ def layer_read_ceiling(L, idx, K, h_post, h_in, sink, stream=None):
     """Measurement only: read exactly the bytes one moe_layer launch on layer
     L reads (router, the K routed experts idx (device int32), the shared
     expert, h_post, h_in) with the layer kernel's load policy, and nothing
-    else; sink (7168 int32/uint32) receives words whose XOR is the XOR of every
-    32-bit word read."""
+    else; sink (7168 int32/uint32) receives words whose sum (mod 2^32) is the
+    sum of every byte read."""
     call("fdm_layer_read_ceiling", L, _p(idx), K, _p(h_post), _p(h_in), _p(sink), _stream(stream))
 
 

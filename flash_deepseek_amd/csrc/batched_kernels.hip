@@ -246,7 +246,13 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
   const int n_items = n_items_of(b, D);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
-  const int row = tile * kBDnRows + wave * 4 + (lane >> 4);
+  // Q4_K: 16 lanes per row (lane / 16); Q6_K resident layout: lane (half h =
+  // bit 0, row r = bits 1-2, block b = bits 3-4 of column part pt = bit 5),
+  // so a wave's load reads 32 consecutive pieces of each part
+  const int h6 = lane & 1, r6 = (lane >> 1) & 3, b6 = (lane >> 3) & 3, p6 = lane >> 5;
+  const int H6 = 8 * p6 + 2 * b6 + h6;
+  const int row = tile * kBDnRows + wave * 4 + (Q6 ? r6 : lane >> 4);
+  const bool writer = Q6 ? (lane & 0x39) == 0 : l16 == 0;
   const int P = b.T * b.K;
   for (int d = blockIdx.y; d < n_items; d += gridDim.y) {
     int e;
@@ -254,12 +260,12 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
     const uint8_t* blob = r.shared ? b.shared : b.experts + (size_t)e * b.expert_size;
     const uint8_t* dbase = blob + 2 * (size_t)kGateBytes;
     Q4KGroupLoad ld[2];
-    Q6KHalfLoad l6;
+    Q6KHalfW l6;
     if (!Q6) {
 #pragma unroll
       for (int i = 0; i < 2; ++i) ld[i] = rel_load_group<true>(dbase, row, 4 * i + (l16 >> 2), l16 & 3);
     } else {
-      l6 = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (l16 >> 1) * kQ6KBlock, l16 & 1);
+      l6 = q6k_rel_load_half(dbase, row, 4 * p6 + b6, h6);
     }
     auto row_of = [&](int i) { return r.shared ? P + r.first + i : r.first + i; };
     Records<kFfn / 64> rec;
@@ -277,10 +283,19 @@ __global__ __launch_bounds__(256) void k_bdown(BatchArgs b) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) acc += q4k_group_dot_ld(ld[k], sel, &cur[16 * k + l16]);
       } else {
-        acc = q6k_half_dot_ld(l6, &cur[2 * l16]);
+        acc = q6k_half_dot_w(l6, &cur[2 * H6]);
       }
-      acc = sum16(acc);
-      if (l16 == 0) b.eo[(size_t)arow * kHidden + row] = acc;
+      if (!Q6) {
+        acc = sum16(acc);
+      } else {
+        // H6 bits 3, 2, 1, 0 are lane bits 5, 4, 3, 0: the xor butterfly over
+        // 8, 4, 2, 1, which gives lane H6 = 0 what sum16 gives its first lane
+        acc += __shfl_xor(acc, 32);
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 8);
+        acc += __shfl_xor(acc, 1);
+      }
+      if (writer) b.eo[(size_t)arow * kHidden + row] = acc;
       if (i + 1 < r.count) rec.store(xs[(i + 1) & 1]);
       __syncthreads();
     }

@@ -415,7 +415,7 @@ __device__ __forceinline__ void q4k_group_dot_rows(const Q4KGroupLoad (&ld)[R], 
 //  q0 and of q1, so a kernel that walks the blocks one at a time (the
 //  grouped GEMMs) reads every line at once instead of half of it now and
 //  the other half a block later, after the L2 may have dropped it.  A Q6_K
-//  down matrix keeps the packed layout.
+//  down matrix has a layout of its own (below).
 constexpr int kRelGuPieces = 32;
 constexpr int kRelDnPieces = 64;
 
@@ -444,6 +444,68 @@ __device__ __forceinline__ Q4KGroupLoad rel_load_group(const uint8_t* mat, int r
   return r;
 }
 
+// ---- the resident layout of a Q6_K down matrix ---------------------------------------------
+// A Q6_K down matrix [7168 x 2048] (8 blocks of 210 B per row) of a resident
+// layer is stored in steps of 16 rows x 4 blocks (64 blocks, 13,440 B = 105
+// whole 128-byte lines) at ((block / 4) * 448 + row / 16) * 13,440, so a
+// column part of 4 blocks is one contiguous run of steps.  Inside a step the
+// block's bytes are split by kind and every kind is aligned: with the block
+// index b = (row % 16 / 4) * 16 + (block % 4) * 4 + row % 4 and the piece
+// p = 2 b + half (a half is 128 weights: ql bytes 64 h .. 64 h + 63, qh
+// bytes 128 + 32 h .., scales 192 + 8 h .. of the packed block),
+//   ql chunk j (16 B, j < 4) of piece p at j * 2048 + 16 p
+//   qh chunk j (j < 2) at 8192 + j * 2048 + 16 p
+//   the half's 8 scales at 12288 + 8 p
+//   d of block b at 13312 + 2 b
+// so the 32 pieces of 4 rows x 4 blocks are consecutive: a wave's load of
+// them reads one contiguous 512-byte run per chunk, and no word needs the
+// byte realignment of the packed 210-byte blocks.  The values are untouched:
+// every byte of the packed blob has one place in the step.
+constexpr int kRel6Step = 13440;
+constexpr int kRel6Ql = 0, kRel6Qh = 8192, kRel6Sc = 12288, kRel6D = 13312;
+
+__host__ __device__ __forceinline__ size_t rel6_step_off(int row, int block) {
+  return ((size_t)(block >> 2) * (kHidden / 16) + (size_t)(row >> 4)) * kRel6Step;
+}
+__host__ __device__ __forceinline__ int rel6_block_index(int row, int block) {
+  return ((row & 15) >> 2) * 16 + (block & 3) * 4 + (row & 3);
+}
+
+// The words one lane needs for one 128-element half of a Q6_K block, aligned.
+struct Q6KHalfW {
+  uint32_t ql[16], qh[8], sc[2];
+  uint32_t d;  // the block's fp16 d in the low 16 bits
+};
+
+__device__ __forceinline__ Q6KHalfW q6k_rel_load_half(const uint8_t* mat, int row, int block, int half) {
+  const uint8_t* s = mat + rel6_step_off(row, block);
+  const int b = rel6_block_index(row, block), p = 2 * b + half;
+  Q6KHalfW r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(s + kRel6Ql + j * 2048 + 16 * p));
+    r.ql[4 * j] = v.x;
+    r.ql[4 * j + 1] = v.y;
+    r.ql[4 * j + 2] = v.z;
+    r.ql[4 * j + 3] = v.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(s + kRel6Qh + j * 2048 + 16 * p));
+    r.qh[4 * j] = v.x;
+    r.qh[4 * j + 1] = v.y;
+    r.qh[4 * j + 2] = v.z;
+    r.qh[4 * j + 3] = v.w;
+  }
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 sc = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(s + kRel6Sc + 8 * p));
+  r.sc[0] = sc.x;
+  r.sc[1] = sc.y;
+  const uint32_t dw = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(s + kRel6D + 4 * (b >> 1)));
+  r.d = (b & 1) ? dw >> 16 : dw;
+  return r;
+}
+
 // funnel: the 4 bytes starting `byte_shift` (0..3) bytes into the 8-byte
 // little-endian pair (lo, hi).
 __device__ __forceinline__ uint32_t funnel(uint32_t lo, uint32_t hi, uint32_t byte_shift) {
@@ -464,47 +526,41 @@ __device__ __forceinline__ float q6k_half_dot(const uint32_t* ql, const uint32_t
   const uint32_t* a1 = reinterpret_cast<const uint32_t*>(x1->a);
   const uint32_t* b1 = reinterpret_cast<const uint32_t*>(x1->b);
   const uint32_t* c1 = reinterpret_cast<const uint32_t*>(x1->c);
-  // acc[quarter][scale half]: quarter k covers elements 32k..32k+31 of the
-  // half (k = 0..3); scale half = l / 16.
-  int A[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-  int B[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-  int C[4][2] = {{0, 0}, {0, 0}, {0, 0}, {0, 0}};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int s = i >> 2;
-    const uint32_t wl = ql[i], wl2 = ql[8 + i], wh = qh[i];
-    // Each byte becomes 4*(q-32) as int8: the 6-bit q sits in bits 2..7 and
-    // flipping bit 7 subtracts 128.
-    const uint32_t v0 = (((wl & 0x0F0F0F0Fu) << 2) | ((wh & 0x03030303u) << 6)) ^ 0x80808080u;
-    const uint32_t v1 = (((wl2 & 0x0F0F0F0Fu) << 2) | ((wh & 0x0C0C0C0Cu) << 4)) ^ 0x80808080u;
-    const uint32_t v2 = (((wl >> 2) & 0x3C3C3C3Cu) | ((wh & 0x30303030u) << 2)) ^ 0x80808080u;
-    const uint32_t v3 = (((wl2 >> 2) & 0x3C3C3C3Cu) | (wh & 0xC0C0C0C0u)) ^ 0x80808080u;
-    A[0][s] = sdot4(v0, a0[i], A[0][s]);
-    B[0][s] = sdot4(v0, b0[i], B[0][s]);
-    C[0][s] = sdot4(v0, c0[i], C[0][s]);
-    A[1][s] = sdot4(v1, a0[8 + i], A[1][s]);
-    B[1][s] = sdot4(v1, b0[8 + i], B[1][s]);
-    C[1][s] = sdot4(v1, c0[8 + i], C[1][s]);
-    A[2][s] = sdot4(v2, a1[i], A[2][s]);
-    B[2][s] = sdot4(v2, b1[i], B[2][s]);
-    C[2][s] = sdot4(v2, c1[i], C[2][s]);
-    A[3][s] = sdot4(v3, a1[8 + i], A[3][s]);
-    B[3][s] = sdot4(v3, b1[8 + i], B[3][s]);
-    C[3][s] = sdot4(v3, c1[8 + i], C[3][s]);
-  }
+  // quarter k covers elements 32k..32k+31 of the half (k = 0..3), scale
+  // half s = l / 16: the integer sums of one quarter are complete (and
+  // folded) before the next quarter's begin, so only six are live.
   const float xs[4] = {x0->s[0], x0->s[1], x1->s[0], x1->s[1]};
   float acc = 0.0f;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
+    const uint32_t* ak = (k < 2 ? a0 : a1) + 8 * (k & 1);
+    const uint32_t* bk = (k < 2 ? b0 : b1) + 8 * (k & 1);
+    const uint32_t* ck = (k < 2 ? c0 : c1) + 8 * (k & 1);
+    int A[2] = {0, 0}, B[2] = {0, 0}, C[2] = {0, 0};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int s = i >> 2;
+      const uint32_t wl = ql[i], wl2 = ql[8 + i], wh = qh[i];
+      // Each byte becomes 4*(q-32) as int8: the 6-bit q sits in bits 2..7 and
+      // flipping bit 7 subtracts 128.
+      uint32_t v;
+      if (k == 0) v = (((wl & 0x0F0F0F0Fu) << 2) | ((wh & 0x03030303u) << 6)) ^ 0x80808080u;
+      else if (k == 1) v = (((wl2 & 0x0F0F0F0Fu) << 2) | ((wh & 0x0C0C0C0Cu) << 4)) ^ 0x80808080u;
+      else if (k == 2) v = (((wl >> 2) & 0x3C3C3C3Cu) | ((wh & 0x30303030u) << 2)) ^ 0x80808080u;
+      else v = (((wl2 >> 2) & 0x3C3C3C3Cu) | (wh & 0xC0C0C0C0u)) ^ 0x80808080u;
+      A[s] = sdot4(v, ak[i], A[s]);
+      B[s] = sdot4(v, bk[i], B[s]);
+      C[s] = sdot4(v, ck[i], C[s]);
+    }
     // scales sc[2k + s]: byte (2k + s) of the 8 scale bytes, as int8
     const uint32_t word = sc[k >> 1];
     const int sh = (k & 1) * 16;
     const int sa = (int)(int8_t)((word >> sh) & 0xFF);
     const int sb = (int)(int8_t)((word >> (sh + 8)) & 0xFF);
     // |sc * sum| < 2^31: 128 * 16 * 128 * 127 per scale half
-    const int ia = sa * A[k][0] + sb * A[k][1];
-    const int ib = sa * B[k][0] + sb * B[k][1];
-    const int ic = sa * C[k][0] + sb * C[k][1];
+    const int ia = sa * A[0] + sb * A[1];
+    const int ib = sa * B[0] + sb * B[1];
+    const int ic = sa * C[0] + sb * C[1];
     acc = fmaf(xs[k], digit_fold(ia, ib, ic), acc);
   }
   return acc * 0.25f;
@@ -537,6 +593,10 @@ __device__ __forceinline__ Q6KHalfLoad q6k_load_half(const uint8_t* blk, int h) 
   r.sc[1] = (uint32_t)s16[2] | ((uint32_t)s16[3] << 16);
   r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
   return r;
+}
+
+__device__ __forceinline__ float q6k_half_dot_w(const Q6KHalfW& r, const XGroup* __restrict__ xg) {
+  return half_to_float(r.d) * q6k_half_dot(r.ql, r.qh, r.sc, xg, xg + 1);
 }
 
 __device__ __forceinline__ float q6k_half_dot_ld(const Q6KHalfLoad& r,

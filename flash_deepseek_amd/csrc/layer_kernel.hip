@@ -553,15 +553,18 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
       if (gl == 0) put_tagged(eo + row0 + RPW * j, a.epoch, __float_as_uint(v));
     }
   } else {
-    constexpr int LR = kDnLanesQ6, RPW = 64 / LR;
-    const int gl = lane % LR;  // half block of the row's part
-    const int row0 = item * kDnRowsQ6 + wave * (kDnRowsQ6L * RPW) + lane / LR;
-    const int H = part * kDnLanesQ6 + gl;  // half block of the row
-    Q6KHalfLoad l6[kDnRowsQ6L];
+    // Q6_K resident layout: lane (half h = bit 0, row r of a 4-row group =
+    // bits 1-2, block b of the part = bits 3-4, 4-row group g4 = bit 5); the
+    // wave's rows are one 16-row step, so its load j of a half block per lane
+    // reads 64 consecutive pieces (rows 8 j .. 8 j + 7 of the step)
+    static_assert(kDnLanesQ6 == 8 && kDnRowsQ6L == 2 && kDnRowsQ6 == 64, "Q6_K down item: 16 rows per wave");
+    const int h = lane & 1, r = (lane >> 1) & 3, b = (lane >> 3) & 3, g4 = lane >> 5;
+    const int gl = 2 * b + h;  // half block of the row's part
+    const int row0 = item * kDnRowsQ6 + wave * 16 + 4 * g4 + r;  // + 8 j
+    Q6KHalfW l6[kDnRowsQ6L];
     if (blob) {
 #pragma unroll
-      for (int j = 0; j < kDnRowsQ6L; ++j)
-        l6[j] = q6k_load_half(dbase + (size_t)(row0 + RPW * j) * kQ6KRowFfn + (H >> 1) * kQ6KBlock, H & 1);
+      for (int j = 0; j < kDnRowsQ6L; ++j) l6[j] = q6k_rel_load_half(dbase, row0 + 8 * j, part * 4 + b, h);
     }
     stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
     float acc[kDnRowsQ6L] = {};
@@ -570,16 +573,19 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
       for (int j = 0; j < kDnRowsQ6L; ++j) {
         int gi = 2 * gl;
         __asm__ volatile("" : "+v"(gi));
-        acc[j] = q6k_half_dot_ld(l6[j], &sm.xs[gi]);
+        acc[j] = q6k_half_dot_w(l6[j], &sm.xs[gi]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
     for (int j = 0; j < kDnRowsQ6L; ++j) {
+      // the half blocks of a row's part, gl bits 2, 1, 0 = lane bits 4, 3, 0,
+      // summed in the order of the xor butterfly over 4, 2, 1
       float v = acc[j];
-#pragma unroll
-      for (int m = LR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m);
-      if (gl == 0) put_tagged(eo + row0 + RPW * j, a.epoch, __float_as_uint(v));
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 8);
+      v += __shfl_xor(v, 1);
+      if ((lane & 0x19) == 0) put_tagged(eo + row0 + 8 * j, a.epoch, __float_as_uint(v));
     }
   }
 }
@@ -599,10 +605,15 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
 //        wave w holds rows 8 w + 4 m + rs (m < 2), block quad bq of both
 //        parts (blocks bq and 4 + bq), group g: a wave's load is one resident
 //        layout step (4 rows x 4 blocks).
-//  Q6_K: 32 rows; lane (rr = lane / 16, H = lane % 16) of wave w holds rows
-//        8 w + rr + 4 j (j < 2), half block H (part H / 8).
+//  Q6_K: 16 rows; lane (half h = bit 0, row r = bits 1-2, block b = bits
+//        3-4, part = bit 5) of wave w holds row 4 w + r, half
+//        h of block 4 part + b: in the Q6_K resident layout a wave's load
+//        reads 32 consecutive pieces of each part.
 static_assert(kParts == 2, "final items: two column parts");
-constexpr int kFinRowsQ4 = 32, kFinRowsQ6 = 32;
+#ifndef FDM_FIN_ROWS_Q6
+#define FDM_FIN_ROWS_Q6 16  // two Q6_K half-block loads per lane would not fit 128 VGPRs
+#endif
+constexpr int kFinRowsQ4 = 32, kFinRowsQ6 = FDM_FIN_ROWS_Q6;
 __host__ __device__ constexpr int fin_rows(bool q6) { return q6 ? kFinRowsQ6 : kFinRowsQ4; }
 __host__ __device__ constexpr int fin_items(bool q6) { return kHidden / fin_rows(q6); }
 constexpr int kFinMaxRouted = kLayerMaxSlots - 1;             // routed slots (FDM_MAX_K)
@@ -622,9 +633,12 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
   // weights of the shared rows
   constexpr int kQ4M = kFinRowsQ4 / 16;  // Q4_K rows per lane
   const int g = lane & 3, rs = (lane >> 2) & 3, bq = lane >> 4;
-  const int H = lane & 15, rr = lane >> 4;
+  const int h6 = lane & 1, r6 = (lane >> 1) & 3, b6 = (lane >> 3) & 3, p6 = lane >> 5;
+  const int H = 8 * p6 + 2 * b6 + h6;  // half block of the row
   Q4KGroupLoad ld0[kQ4M], ld1[kQ4M];
-  Q6KHalfLoad l6[2];
+  constexpr int kQ6M = kFinRowsQ6 / 16;  // Q6_K rows per lane
+  Q6KHalfLoad l6p[kQ6M];  // packed blob
+  Q6KHalfW l6[kQ6M];      // resident layout
   if (dbase) {
     if (!Q6) {
 #pragma unroll
@@ -640,9 +654,12 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int row = r0 + 8 * wave + rr + 4 * j;
-        l6[j] = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (H >> 1) * kQ6KBlock, H & 1);
+      for (int j = 0; j < kQ6M; ++j) {
+        const int row = r0 + 4 * kQ6M * wave + 4 * j + r6;
+        if (PACKED)
+          l6p[j] = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (H >> 1) * kQ6KBlock, h6);
+        else
+          l6[j] = q6k_rel_load_half(dbase, row, 4 * p6 + b6, h6);
       }
     }
   }
@@ -736,25 +753,26 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
       if ((lane & 0x33) == 0) sm.fin.esh[4 * kQ4M * wave + 4 * m + rs] = p0 + p1;
     }
   } else {
-    float acc[2] = {};
+    float acc[kQ6M] = {};
     if (dbase) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < kQ6M; ++j) {
         int gi = 2 * H;
         __asm__ volatile("" : "+v"(gi));
-        acc[j] = q6k_half_dot_ld(l6[j], &sm.fin.xs[gi]);
+        acc[j] = PACKED ? q6k_half_dot_ld(l6p[j], &sm.fin.xs[gi]) : q6k_half_dot_w(l6[j], &sm.fin.xs[gi]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      // half block within the part = H % 8: the down items' xor 4, 2, 1
+    for (int j = 0; j < kQ6M; ++j) {
+      // half block within the part = 2 b + h: bits 2, 1, 0 are lane bits 4,
+      // 3, 0 (the down items' xor 4, 2, 1)
       float v = acc[j];
-      v += __shfl_xor(v, 4);
-      v += __shfl_xor(v, 2);
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 8);
       v += __shfl_xor(v, 1);
-      const float p1 = __shfl_xor(v, 8);  // lanes of part 0 receive part 1's sum
-      if ((lane & 15) == 0) sm.fin.esh[8 * wave + rr + 4 * j] = v + p1;
+      const float p1 = __shfl_xor(v, 32);  // lanes of part 0 receive part 1's sum
+      if ((lane & 0x39) == 0) sm.fin.esh[4 * kQ6M * wave + 4 * j + r6] = v + p1;
     }
   }
   if (!routed_ready) {
@@ -882,15 +900,14 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
   }
 }
 
-// Q4_K down: every item fits 128 VGPRs, so four workgroups per CU.  Q6_K
-// down rows need more registers (the realigned 6-bit words): three.
+// Every item fits 128 VGPRs, so four workgroups per CU.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_layer_q4k(
     LayerArgs a) {
   __shared__ LayerSmem sm;
   layer_item<false, false>(a, sm);
 }
 
-__global__ __launch_bounds__(256) void k_layer_q6k(LayerArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_layer_q6k(LayerArgs a) {
   __shared__ LayerSmem sm;
   layer_item<true, false>(a, sm);
 }
@@ -903,7 +920,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   layer_item<false, true>(a, sm);
 }
 
-__global__ __launch_bounds__(256) void k_expert_q6k(LayerArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_q6k(LayerArgs a) {
   __shared__ LayerSmem sm;
   layer_item<true, true>(a, sm);
 }

@@ -116,7 +116,14 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
   const uint8_t* blob = slot_blob(t, slot);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
-  const int row = tile * kDnRows + wave * 4 + (lane >> 4);
+  // Q4_K: 16 lanes per row (lane / 16); Q6_K: lane (half h = bit 0, row r =
+  // bits 1-2, block b = bits 3-4 of column part pt = bit 5), the mapping of
+  // the Q6_K resident layout (a wave's load reads 32 consecutive pieces of
+  // each part), also used on packed blobs
+  const int h6 = lane & 1, r6 = (lane >> 1) & 3, b6 = (lane >> 3) & 3, p6 = lane >> 5;
+  const int H6 = 8 * p6 + 2 * b6 + h6;
+  const int row = tile * kDnRows + wave * 4 + (Q6 ? r6 : lane >> 4);
+  const bool writer = Q6 ? (lane & 0x39) == 0 : l16 == 0;
   float acc = 0.0f;
   XStage<kFfn / 64> st;
   st.load(act_xd + (size_t)slot * (kFfn / 64), kFfn / 64);
@@ -139,17 +146,30 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
     }
   } else {
     // 16 halves of 128 elements per 2048-column row: one per lane
-    Q6KHalfLoad ld;
-    if (blob)
-      ld = q6k_load_half(blob + 2 * (size_t)kGateBytes + (size_t)row * kQ6KRowFfn +
-                             (l16 >> 1) * kQ6KBlock,
-                         l16 & 1);
+    const uint8_t* mat = blob ? blob + 2 * (size_t)kGateBytes : nullptr;
+    Q6KHalfW lw;
+    Q6KHalfLoad lp;
+    if (blob) {
+      if (t.rel)
+        lw = q6k_rel_load_half(mat, row, 4 * p6 + b6, h6);
+      else
+        lp = q6k_load_half(mat + (size_t)row * kQ6KRowFfn + (H6 >> 1) * kQ6KBlock, h6);
+    }
     st.store(xs, kFfn / 64);
     __syncthreads();
-    if (blob) acc = q6k_half_dot_ld(ld, &xs[2 * l16]);
+    if (blob) acc = t.rel ? q6k_half_dot_w(lw, &xs[2 * H6]) : q6k_half_dot_ld(lp, &xs[2 * H6]);
   }
-  acc = sum16(acc);
-  if (l16 == 0) {
+  if (!Q6) {
+    acc = sum16(acc);
+  } else {
+    // H6 bits 3, 2, 1, 0 are lane bits 5, 4, 3, 0: the xor butterfly over 8,
+    // 4, 2, 1, which gives lane H6 = 0 what sum16 gives its first lane
+    acc += __shfl_xor(acc, 32);
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 8);
+    acc += __shfl_xor(acc, 1);
+  }
+  if (writer) {
     store_agent(eo + (size_t)slot * kHidden + row, acc);
     wait_stores_done();
   }

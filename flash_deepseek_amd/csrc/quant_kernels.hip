@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__
 // One thread per Q4_K block of a blob's gate, up or Q4_K down matrix: the
 // block's header dwords and its 8 half-groups go to their REL pieces (see
 // rel_step / rel_piece).  Blob b of n: src + b * src_stride ->
-// dst + b * expert_size.  A Q6_K down matrix is copied by the caller.
+// dst + b * expert_size.  A Q6_K down matrix goes through k_rel_pack_q6.
 __global__ __launch_bounds__(256) void k_rel_pack(const uint8_t* __restrict__ src, size_t src_stride,
                                                   uint8_t* __restrict__ dst, size_t expert_size,
                                                   int n_blobs, int with_down) {
@@ -131,6 +131,30 @@ __global__ __launch_bounds__(256) void k_rel_pack(const uint8_t* __restrict__ sr
   }
 }
 
+// Q6_K down matrices into their resident layout (fdm_device.h): one thread
+// per 210-byte block, byte by byte (made once per layer, not a hot path).
+__global__ __launch_bounds__(256) void k_rel_pack_q6(const uint8_t* __restrict__ src, size_t src_stride,
+                                                     uint8_t* __restrict__ dst, size_t expert_size, int n_blobs) {
+  const size_t per = (size_t)kHidden * (kFfn / kQK);  // blocks per matrix
+  const size_t total = per * (size_t)n_blobs;
+  const size_t off = 2 * (size_t)kGateBytes;
+  for (size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x; k < total; k += (size_t)gridDim.x * blockDim.x) {
+    const size_t n = k / per, kb = k % per;
+    const int row = (int)(kb / (kFfn / kQK)), block = (int)(kb % (kFfn / kQK));
+    const uint8_t* b = src + n * src_stride + off + (size_t)row * kQ6KRowFfn + (size_t)block * kQ6KBlock;
+    uint8_t* st = dst + n * expert_size + off + rel6_step_off(row, block);
+    const int bi = rel6_block_index(row, block);
+    for (int h = 0; h < 2; ++h) {
+      const int p = 2 * bi + h;
+      for (int i = 0; i < 64; ++i) st[kRel6Ql + (i >> 4) * 2048 + 16 * p + (i & 15)] = b[64 * h + i];
+      for (int i = 0; i < 32; ++i) st[kRel6Qh + (i >> 4) * 2048 + 16 * p + (i & 15)] = b[128 + 32 * h + i];
+      for (int i = 0; i < 8; ++i) st[kRel6Sc + 8 * p + i] = b[192 + 8 * h + i];
+    }
+    st[kRel6D + 2 * bi] = b[208];
+    st[kRel6D + 2 * bi + 1] = b[209];
+  }
+}
+
 static unsigned grid_for_waves(size_t waves) {
   size_t wg = (waves + 3) / 4;
   const size_t cap = (size_t)(g_num_cus > 0 ? g_num_cus : 256) * 16;
@@ -168,10 +192,13 @@ hipError_t launch_rel_pack(const uint8_t* src, size_t src_stride, uint8_t* dst, 
                      expert_size, n_blobs, down_q6 ? 0 : 1);
   if (hipError_t e = hipGetLastError()) return e;
   if (!down_q6) return hipSuccess;
-  // a Q6_K down keeps the packed layout: one strided copy of every blob's down part
-  const size_t off = 2 * (size_t)kGateBytes;
-  return hipMemcpy2DAsync(dst + off, expert_size, src + off, src_stride, expert_size - off, (size_t)n_blobs,
-                          hipMemcpyDeviceToDevice, s);
+  // the Q6_K down matrices: their own resident layout
+  const size_t q6_blocks = (size_t)n_blobs * 57344;
+  size_t wg6 = (q6_blocks + 255) / 256;
+  if (wg6 > cap) wg6 = cap;
+  hipLaunchKernelGGL(k_rel_pack_q6, dim3((unsigned)(wg6 ? wg6 : 1)), dim3(256), 0, s, src, src_stride, dst,
+                     expert_size, n_blobs);
+  return hipGetLastError();
 }
 
 }  // namespace fdm

@@ -7,10 +7,11 @@
 // per CU), and writes 7168 words.  Its time is what the device's memory
 // system gives for the layer's bytes with no hand-off, no route and no math;
 // the layer kernel's time against it separates the device ceiling from the
-// kernel's own losses.  Each workgroup folds its bytes by XOR into one word
-// (sink[tile]); the other sink words are written as 0, so the XOR of the
-// sink is the XOR of every 32-bit word read (a permutation-invariant check
-// of what was read).
+// kernel's own losses.  Each workgroup sums its bytes (mod 2^32, one dot4
+// against ones per word) into one word (sink[tile]); the other sink words
+// are written as 0, so the sum of the sink is the sum of every byte read (a
+// check of what was read that no byte permutation, such as the resident
+// expert layout, changes).
 #include "fdm_internal.h"
 
 namespace fdm {
@@ -41,13 +42,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k
   }
   uint32_t x = 0;
 #pragma unroll
-  for (int j = 0; j < kVecPerThread; ++j) x ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+  for (int j = 0; j < kVecPerThread; ++j) {
+    x = __builtin_amdgcn_udot4(v[j].x, 0x01010101u, x, false);
+    x = __builtin_amdgcn_udot4(v[j].y, 0x01010101u, x, false);
+    x = __builtin_amdgcn_udot4(v[j].z, 0x01010101u, x, false);
+    x = __builtin_amdgcn_udot4(v[j].w, 0x01010101u, x, false);
+  }
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) x ^= (uint32_t)__shfl_xor((int)x, m);
+  for (int m = 32; m >= 1; m >>= 1) x += (uint32_t)__shfl_xor((int)x, m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
   __syncthreads();
   if (threadIdx.x == 0) {
-    a.sink[t] = (red[0] ^ red[1]) ^ (red[2] ^ red[3]);
+    a.sink[t] = (red[0] + red[1]) + (red[2] + red[3]);
     if (t + a.n_tiles < kHidden) a.sink[t + a.n_tiles] = 0u;
   }
 }

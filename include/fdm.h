@@ -281,7 +281,7 @@ int fdm_moe_layer_norm(int L, const float *d_h, const float *d_norm_w, int K, fl
  * outside the layer reads expert 0), the shared expert, d_h_post and d_h_in
  * (may be NULL) -- with that kernel's load policy (16-byte nontemporal loads,
  * 64 KB per workgroup, four workgroups per CU), and writes FDM_HIDDEN words
- * to d_sink whose XOR is the XOR of every 32-bit word read.  No route, no
+ * to d_sink whose sum (mod 2^32) is the sum of every byte read.  No route, no
  * hand-off, no math: its time against fdm_moe_layer's separates the device's
  * streaming ceiling for these bytes from the kernel's own losses.
  * FDM_E_INVAL when the bytes exceed FDM_HIDDEN tiles of 64 KB (K = 16 with a

@@ -220,10 +220,11 @@ def test_moe_layer_norm_rejects_h_post_overlapping_h(fdm, layer):
 
 def test_layer_read_ceiling_reads_the_layer_bytes(fdm, layer):
     """fdm_layer_read_ceiling (the streaming-ceiling launch of the bench)
-    reads exactly the bytes one layer launch reads: the XOR of its sink equals
-    the XOR of every 32-bit word of the router weights and bias, the K routed
-    experts' packed blobs (the resident layout permutes whole 32-bit words, so
-    the XOR is the same), the shared expert, h_post and h_in."""
+    reads exactly the bytes one layer launch reads: the sum of its sink
+    (mod 2^32) equals the sum of every byte of the router weights and bias,
+    the K routed experts' packed blobs (the resident layout is a permutation
+    of their bytes, so the sum is the same), the shared expert, h_post and
+    h_in."""
     import torch
     L, lay = layer
     ids = np.array([3, 250, 17, 17, 99, 0, 128, 255], np.int32)  # a repeated id is read twice
@@ -232,13 +233,13 @@ def test_layer_read_ceiling_reads_the_layer_bytes(fdm, layer):
     sink = torch.zeros(7168, dtype=torch.int32, device="cuda")
     say(f"layer_read_ceiling L={L} K={len(ids)}")
     fdm.layer_read_ceiling(L, to_dev(ids), len(ids), to_dev(h), to_dev(h_in), sink)
-    got = int(np.bitwise_xor.reduce(to_host(sink).view(np.uint32)))
+    got = int(to_host(sink).view(np.uint32).astype(np.uint64).sum()) % (1 << 32)
 
-    def xor32(a):
-        return int(np.bitwise_xor.reduce(np.ascontiguousarray(a).view(np.uint32).ravel()))
+    def bytesum(a):
+        return int(np.ascontiguousarray(a).view(np.uint8).astype(np.uint64).sum())
 
-    want = xor32(to_host(lay.Wg)) ^ xor32(to_host(lay.bias)) ^ xor32(lay.expert_bytes(-1))
-    want ^= xor32(h) ^ xor32(h_in)
+    want = bytesum(to_host(lay.Wg)) + bytesum(to_host(lay.bias)) + bytesum(lay.expert_bytes(-1))
+    want += bytesum(h) + bytesum(h_in)
     for e in ids:
-        want ^= xor32(lay.expert_bytes(int(e)))
-    assert got == want, (hex(got), hex(want))
+        want += bytesum(lay.expert_bytes(int(e)))
+    assert got == want % (1 << 32), (hex(got), hex(want % (1 << 32)))
