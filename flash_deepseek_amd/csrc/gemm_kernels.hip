@@ -6,18 +6,21 @@
 // with 6-bit sc, m and 4-bit q, so
 //   sum_k w_k x_k = d * sum_k sc_k q_k x_k - dmin * sum_sb m_sb X_sb
 // (X_sb: the sum of the sub-block's 32 activations).  The integer sc*q <= 945
-// is exact in fp16 and is built per element by one packed integer multiply-
-// add straight into fp16 bits: 0x6400 + sc*q is the half 1024 + sc*q.  The
-// MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulation) contracts it with the
-// activations, so the MFMA sums 1024 X + sum sc q x over a whole block and
-// the scales are applied once per block:
-//   y += d * C  -  sum_sb X_sb (1024 d + dmin m_sb)
+// is exact in fp16 and is built per element pair by one mask-or and one
+// packed fma: (0x6400 | q) is the half 1024 + q, and (1024 + q) sc - 1024 sc
+// is sc q exactly (one rounding of an exact half).  The MFMA
+// (v_mfma_f32_16x16x32_f16, fp32 accumulation) contracts it with the
+// activations over a whole block and the scales are applied once per block:
+//   y += d * C  -  sum_sb X_sb dmin m_sb
 // the second term by a 16x16x4 fp32 MFMA over the block's eight sub-blocks.
+// (Weights carried as 1024 + sc q, with 1024 X cancelled afterwards, would
+// inflate the accumulator several times over the sum it carries and cost
+// the batched path its fp32 grade on SwiGLU activations.)
 // Activations enter as P fp16 planes of x' = x * 2^s (a per-row power of
 // two: the largest |x'| lies in [2^13, 2^14)): P = 3 carries every fp32
 // value exactly (hi + mid + lo, 33 significant bits) -- batched decode, fp32
 // grade; P = 1 carries 11 bits -- prefill, whose bar is 1e-2.  X_sb is the
-// fp32 sum of the planes, so the 1024 X part of C cancels against it.
+// fp32 sum of the planes' values.
 //
 // Mapping.  A workgroup of 4 waves owns 64 gate and 64 up rows (wave w:
 // rows 16 w .. 16 w + 15 of both, so SwiGLU is applied in registers) or 128
@@ -87,26 +90,23 @@ __device__ __forceinline__ QLane qlane_load(const uint8_t* mat, int row, int blo
   return r;
 }
 
-// fp16 bits of 1024 + sc * q for the two q held in bits 0-3 of the halves
-// of q2 (the rest zero; q < 16, so sc * q < 1024 fits the 10-bit mantissa).
-__device__ __forceinline__ uint32_t magic2(uint32_t q2, u16x2 sc2) {
-  const u16x2 q = __builtin_bit_cast(u16x2, q2);
-  const u16x2 v = q * sc2 + (u16x2){0x6400, 0x6400};
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// The same halves for the two q held in bits 4-7 of the halves of w (the
-// rest of w arbitrary): 0x6400 | 16 q is the half 1024 + 16 q, and one fused
-// multiply-add per half, (1024 + 16 q) (sc / 16) + (1024 - 64 sc), gives
-// 1024 + sc q exactly (the exact result is a half: a single rounding keeps
-// it), with no shift to bring the nibble down.
-__device__ __forceinline__ uint32_t magic2_hi(uint32_t w, f16x2 sc16, f16x2 off) {
+// fp16 halves of sc * q for the two q held in bits 0-3 (MASK 0x000F000F)
+// of the halves of w, the rest of w arbitrary: 0x6400 | q is the half
+// 1024 + q, and one fused multiply-add per half, (1024 + q) sc - 1024 sc,
+// gives sc q exactly (q < 16, sc < 64: the exact result is a half, which the
+// single rounding keeps).  For the q in bits 4-7 (MASK 0x00F000F0),
+// 0x6400 | 16 q is the half 1024 + 16 q, and (1024 + 16 q) (sc / 16) - 64 sc
+// is sc q exactly, with no shift to bring the nibble down.  k holds the
+// multiplier in its low half and the addend in its high half; both halves of
+// the fma read them (op_sel).
+template <uint32_t MASK>
+__device__ __forceinline__ uint32_t magic2(uint32_t w, f16x2 k) {
   // one v_and_or_b32 (mask from an SGPR, 0x64006400 from a VGPR: a VOP3
   // takes no literal and one SGPR), which the compiler otherwise splits
   uint32_t m;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(m) : "v"(w), "s"(0x00F000F0u), "v"(0x64006400u));
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(m) : "v"(w), "s"(MASK), "v"(0x64006400u));
   const f16x2 v = __builtin_bit_cast(f16x2, m);
-  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, sc16, off));
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(v, (f16x2){k.x, k.x}, (f16x2){k.y, k.y}));
 }
 
 // The B operands of MFMA steps m (low nibbles) and m + 4 (high nibbles):
@@ -115,23 +115,22 @@ __device__ __forceinline__ uint32_t magic2_hi(uint32_t w, f16x2 sc16, f16x2 off)
 // which k_xplanes stores the activations): a dword of qs holds the low
 // nibbles of elements 0 and 2 at bits 0 and 16 and their high nibbles at
 // bits 4 and 20, elements 1 and 3 eight bits higher, so one shift per dword
-// and per fp16 pair one mask and one packed multiply-add suffice.
+// and per fp16 pair one mask-or and one packed fma suffice.
 struct BPair {
   f16x8 lo, hi;
 };
 
-__device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, f16x2 sc16_hi, f16x2 off_hi) {
-  constexpr uint32_t M = 0x000F000Fu;
+__device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, f16x2 k_lo, f16x2 k_hi) {
   const uint32_t v0 = w0 >> 8, v1 = w1 >> 8;
   u32x4 lo, hi;
-  lo.x = magic2(w0 & M, sc_lo);
-  lo.y = magic2(v0 & M, sc_lo);
-  lo.z = magic2(w1 & M, sc_lo);
-  lo.w = magic2(v1 & M, sc_lo);
-  hi.x = magic2_hi(w0, sc16_hi, off_hi);
-  hi.y = magic2_hi(v0, sc16_hi, off_hi);
-  hi.z = magic2_hi(w1, sc16_hi, off_hi);
-  hi.w = magic2_hi(v1, sc16_hi, off_hi);
+  lo.x = magic2<0x000F000Fu>(w0, k_lo);
+  lo.y = magic2<0x000F000Fu>(v0, k_lo);
+  lo.z = magic2<0x000F000Fu>(w1, k_lo);
+  lo.w = magic2<0x000F000Fu>(v1, k_lo);
+  hi.x = magic2<0x00F000F0u>(w0, k_hi);
+  hi.y = magic2<0x00F000F0u>(v0, k_hi);
+  hi.z = magic2<0x00F000F0u>(w1, k_hi);
+  hi.w = magic2<0x00F000F0u>(v1, k_hi);
   BPair b;
   b.lo = __builtin_bit_cast(f16x8, lo);
   b.hi = __builtin_bit_cast(f16x8, hi);
@@ -141,9 +140,9 @@ __device__ __forceinline__ BPair build_b(uint32_t w0, uint32_t w1, u16x2 sc_lo, 
 // Per-block constants of the lane's row and group.
 struct QScale {
   float d;
-  u16x2 sc_lo;         // sc of sub-block 2j, in both halves
-  f16x2 sc16_hi, off_hi;  // sc / 16 and 1024 - 64 sc of sub-block 2j+1 (halves)
-  float bc_lo, bc_hi;  // -(1024 d + dmin m) of sub-blocks 2j, 2j+1
+  f16x2 k_lo;          // {sc, -1024 sc} of sub-block 2j
+  f16x2 k_hi;          // {sc / 16, -64 sc} of sub-block 2j+1
+  float bc_lo, bc_hi;  // -dmin m of sub-blocks 2j, 2j+1
 };
 
 __device__ __forceinline__ QScale qscale(const u32x4 hdr, const Q4KScaleSel& sel) {
@@ -152,16 +151,15 @@ __device__ __forceinline__ QScale qscale(const u32x4 hdr, const Q4KScaleSel& sel
   QScale s;
   s.d = half_to_float(hdr.x);
   const float dmin = half_to_float(hdr.x >> 16);
-  s.sc_lo = (u16x2){(unsigned short)sc0, (unsigned short)sc0};
-  // the halves 1024 + sc1, then sc1 / 16 and 1024 - 64 sc1, all exact
-  const f16x2 h = __builtin_bit_cast(f16x2, (uint32_t)sc1 * 0x10001u + 0x64006400u);
-  s.sc16_hi = __builtin_elementwise_fma(h, (f16x2){(_Float16)0.0625f, (_Float16)0.0625f},
-                                        (f16x2){(_Float16)-64.0f, (_Float16)-64.0f});
-  s.off_hi = __builtin_elementwise_fma(s.sc16_hi, (f16x2){(_Float16)-1024.0f, (_Float16)-1024.0f},
-                                       (f16x2){(_Float16)1024.0f, (_Float16)1024.0f});
-  const float off = 1024.0f * s.d;  // exact: a power-of-two multiple of a half
-  s.bc_lo = -fmaf(dmin, (float)m0, off);
-  s.bc_hi = -fmaf(dmin, (float)m1, off);
+  // the halves 1024 + sc0 and 1024 + sc1, then {sc0, -1024 sc0} and
+  // {sc1 / 16, -64 sc1}, all exact
+  const f16x2 h = __builtin_bit_cast(f16x2, (uint32_t)sc0 + ((uint32_t)sc1 << 16) + 0x64006400u);
+  const f16x2 k = __builtin_elementwise_fma(h, (f16x2){(_Float16)1.0f, (_Float16)0.0625f},
+                                            (f16x2){(_Float16)-1024.0f, (_Float16)-64.0f});  // {sc0, sc1 / 16}
+  s.k_lo = (f16x2){k.x, k.x * (_Float16)-1024.0f};
+  s.k_hi = (f16x2){k.y, k.y * (_Float16)-1024.0f};
+  s.bc_lo = -(dmin * (float)m0);
+  s.bc_hi = -(dmin * (float)m1);
   return s;
 }
 
@@ -314,8 +312,8 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds0, ui
         // and used by both
         const u32x4& qa = m < 2 ? w[0].q0 : w[0].q1;
         const u32x4& qb = m < 2 ? w[1].q0 : w[1].q1;
-        const BPair B0 = build_b(qa[i0], qa[i0 + 1], sc[0].sc_lo, sc[0].sc16_hi, sc[0].off_hi);
-        const BPair B1 = build_b(qb[i0], qb[i0 + 1], sc[1].sc_lo, sc[1].sc16_hi, sc[1].off_hi);
+        const BPair B0 = build_b(qa[i0], qa[i0 + 1], sc[0].k_lo, sc[0].k_hi);
+        const BPair B1 = build_b(qb[i0], qb[i0 + 1], sc[1].k_lo, sc[1].k_hi);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -343,7 +341,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds0, ui
 #pragma unroll
       for (int t = 0; t < TL; ++t) {
         const u32x4& qa = m < 2 ? w[t].q0 : w[t].q1;
-        const BPair B = build_b(qa[i0], qa[i0 + 1], sc[t].sc_lo, sc[t].sc16_hi, sc[t].off_hi);
+        const BPair B = build_b(qa[i0], qa[i0 + 1], sc[t].k_lo, sc[t].k_hi);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -441,7 +439,7 @@ __device__ __forceinline__ void qgemm_body(const QGemmArgs& g, uint8_t* lds0, ui
 // An expert's weights are then read from HBM once per row group and served
 // from that XCD's L2 to its other chunks; every XCD does the same work.
 template <int P, int NB, bool DOWN>
-__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void k_qgemm(QGemmArgs g) {
+__global__ __launch_bounds__(kQWaves * 64) __attribute__((amdgpu_waves_per_eu((P == 3 && DOWN) ? 3 : 2))) void k_qgemm(QGemmArgs g) {
   constexpr int TL = qgemm_tiles(P, DOWN);
   constexpr int RG = (DOWN ? kHidden : kFfn) / qgemm_rows(TL, DOWN);
   constexpr int Q = RG / 8;

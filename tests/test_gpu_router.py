@@ -17,8 +17,10 @@ def route_dev(fdm, logits, bias, K, T):
     return to_host(idx).reshape(T, K), to_host(w).reshape(T, K)
 
 
-@pytest.mark.parametrize("T", [1, 5, 21, 64])
+@pytest.mark.parametrize("T", [1, 5, 21, 64, 256, 512])
 def test_router_logits_bit_exact(fdm, oracle, T):
+    """T = 256 and 512 run the blocked kernel of batched decode and prefill
+    (8 experts x 8 tokens per block); every logit of every token is checked."""
     say(f"router_logits T={T}")
     Wg = oracle.synth_normal(256 * 7168, 0.0, 0.01, 40).reshape(256, 7168)
     X = oracle.synth_normal(T * 7168, 0.0, 1.0, 41 + T).reshape(T, 7168)
