@@ -41,8 +41,8 @@ constexpr int kRmsThreads = 256;
 constexpr int kRmsMaxPer = kHidden / kRmsThreads;  // elements per thread at d = 7168 (28)
 constexpr int kRmsMaxRisky = 512;
 
-struct RmsSmem {
-  unsigned k[kHidden];        // per element: K_i of a run step, kRmsRisky for a risky step
+struct alignas(16) RmsSmem {
+  unsigned k[kHidden];        // per element: K_i of a run step, kRmsRisky for a risky step (16-byte aligned)
   float rx[kRmsMaxRisky];     // risky steps in order: x_r,
   unsigned rq[kRmsMaxRisky];  //   sum of K before r (mod 2^32),
   int re[kRmsMaxRisky];       //   exponent E of P_r (the run before r lies in [2^(E-1), 2^E))
@@ -79,6 +79,19 @@ __device__ __forceinline__ T wave_scan_incl(T v) {
   return v;
 }
 
+// The lanes before this one within the wave, from the inclusive scan: for
+// floats the previous lane's inclusive value (DPP wave_shr:1; lane 0
+// receives 0) -- inc - v would cancel where v dominates the earlier lanes
+// (an outlier), and the prefix would lose the relative accuracy step 2
+// relies on -- for integers inc - v (exact).
+template <typename T>
+__device__ __forceinline__ T lanes_before(T inc, T v) {
+  if constexpr (__is_same(T, float))
+    return dpp_zero<0x138, 0xF>(inc);
+  else
+    return inc - v;
+}
+
 // Exclusive prefix over the workgroup (256 threads, thread order) of a
 // value; the total in *tot.  Ends with every thread past its reads of the
 // wave sums (the array may be reused).
@@ -97,7 +110,7 @@ __device__ __forceinline__ T rms_block_excl(T v, T* wsum, T& tot) {
   }
   tot = all;
   __syncthreads();
-  return base + (inc - v);
+  return base + lanes_before(inc, v);
 }
 
 // Two exclusive prefixes at once (one pair of barriers).
@@ -145,14 +158,17 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
     if (mine(j)) tot = tot + xv[j] * xv[j];
   float total_f;
   const float base = rms_block_excl(tot, sm.wf, total_f);
-  // 2. classify each step; K of the run steps into LDS
+  // 2. classify each step; K of the run steps into LDS (the thread's slots
+  //    as 16-byte stores where they are whole vectors)
   const float lo_margin = 0.5f * (1.0f + 0x1p-10f);  // frexp mantissa of P_i at least this
   const float hi_margin = 1.0f - 0x1p-10f;           // (P_i + x^2) / 2^E at most this
   float p = base;
   unsigned ksum = 0;
   int nrisky = 0;
+  unsigned kk[4];
 #pragma unroll
   for (int j = 0; j < kRmsMaxPer; ++j) {
+    kk[j & 3] = 0u;
     if (mine(j)) {
       const float after = p + xv[j] * xv[j];
       int E;
@@ -162,11 +178,14 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
       const bool risky = !(p >= 0x1p-100f) || !(after < 0x1p126f) || !(m >= lo_margin) ||
                          !(ldexpf(after, -E) <= hi_margin) || fabs(q - K) == 0.5;
       const unsigned k = risky ? kRmsRisky : (unsigned)K;
-      sm.k[i0 + j] = k;
+      kk[j & 3] = k;
+      if (!FULL) sm.k[i0 + j] = k;
       ksum += risky ? 0u : k;
       nrisky += risky ? 1 : 0;
       p = after;
     }
+    if (FULL && (j & 3) == 3)
+      *reinterpret_cast<u32x4*>(&sm.k[i0 + j - 3]) = u32x4{kk[0], kk[1], kk[2], kk[3]};
   }
   unsigned ktot;
   int rtot;
@@ -192,10 +211,24 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
   p = base;
   unsigned kq = kbase;
   int r = rbase;
+  unsigned kv[kRmsMaxPer];  // every K read before the walk over them: one LDS round trip
+#pragma unroll
+  for (int j = 0; j < kRmsMaxPer; j += 4) {
+    if (FULL) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&sm.k[i0 + j]);
+      kv[j] = v.x;
+      kv[j + 1] = v.y;
+      kv[j + 2] = v.z;
+      kv[j + 3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) kv[j + i] = mine(j + i) ? sm.k[i0 + j + i] : 0u;
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kRmsMaxPer; ++j) {
     if (nrisky > 0 && mine(j)) {
-      const unsigned k = sm.k[i0 + j];
+      const unsigned k = kv[j];
       if (k == kRmsRisky) {
         int E;
         (void)frexpf(p, &E);

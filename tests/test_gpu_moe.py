@@ -202,6 +202,35 @@ def test_moe_layer_norm_fused(fdm, oracle, layer, scale, tok):
     assert np.array_equal(to_host(hio).view(np.uint32), to_host(hid_ref).view(np.uint32))
 
 
+NORM_KINDS = [("normal", 6), ("scaled", 12), ("outliers", 6), ("dominant", 24), ("small_ints", 4),
+              ("powers_of_two", 4), ("leading_zeros", 4), ("tiny_first", 4), ("tiny", 2)]
+
+
+@pytest.mark.parametrize("kind,T", NORM_KINDS, ids=[k for k, _ in NORM_KINDS])
+def test_moe_layer_norm_hidden_states(fdm, oracle, layer, kind, T):
+    """The fused rms_norm on the hidden-state kinds of the rms_norm tests:
+    h_post bit-exact with the oracle's rms_norm for every token, including
+    sums with many ties or below 2^-100 (the two-pass and plain-chain paths)
+    and a dominating element."""
+    import zlib
+    import torch
+    from tests.test_gpu_rms import tokens
+    L, _ = layer
+    K = 8
+    rng = np.random.default_rng(zlib.crc32(("layer-" + kind).encode()))
+    x = tokens(kind, T, 7168, rng)
+    nw = rng.normal(1.0, 0.1, 7168).astype(np.float32)
+    nwd = to_dev(nw)
+    hid, hp = empty_f32(7168), empty_f32(7168)
+    idx = torch.empty(K, dtype=torch.int32, device="cuda")
+    w = empty_f32(K)
+    for t in range(T):
+        say(f"moe_layer_norm L={L} kind={kind} token={t}")
+        fdm.moe_layer_norm(L, to_dev(x[t]), nwd, K, hid, hp, idx, w)
+        want = oracle.rms_norm(x[t], nw)
+        assert np.array_equal(to_host(hp).view(np.uint32), want.view(np.uint32)), (kind, t)
+
+
 def test_moe_layer_norm_rejects_h_post_overlapping_h(fdm, layer):
     """The norm item writes h_post while router rows and digit items still
     read h, so an h_post that overlaps h is rejected before any launch."""

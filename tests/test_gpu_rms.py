@@ -6,7 +6,9 @@ inside a binade, and only the steps near binade edges and the ties walked
 in order.  The inputs are chosen to exercise every branch of that scheme:
 many Gaussian tokens at scales from 2^-40 to 2^40 (binade crossings at
 every position), small integers and powers of two (exact ties under
-round-half-even), a few large outliers, leading zeros, a tiny first element,
+round-half-even), a few large outliers, one element that outweighs every
+element before it by 2^20..2^22 in square (a float prefix formed as
+inclusive sum minus the own value cancels there), leading zeros, a tiny first element,
 sums that stay below 2^-100 (the plain-chain fallback), non-finite values,
 and widths other than 7168."""
 import zlib
@@ -34,6 +36,15 @@ def tokens(kind, T, d, rng):
             v = np.ldexp(1.0, rng.integers(-10, 10, d))
         elif kind == "outliers":
             v = np.where(rng.integers(0, 16, d) == 0, rng.standard_normal(d) * 1e3, rng.standard_normal(d) * 1e-3)
+        elif kind == "dominant":
+            # at the end of an early 28-element chunk; an emulation of the
+            # device's scan order shows inclusive-minus-own prefixes give a
+            # wrong sum for about 1 token in 13 of these
+            v = (rng.standard_normal(d) * 0.05).astype(np.float32)
+            c = int(rng.integers(1, 64))
+            pos = 28 * c + 27 - int(rng.integers(0, 4))
+            pre = float(np.sum(v[: 28 * c].astype(np.float64) ** 2))
+            v[pos] = np.float32(np.sqrt(pre * 2.0 ** rng.uniform(20, 22)))
         elif kind == "leading_zeros":
             v = rng.standard_normal(d)
             v[: int(rng.integers(1, min(d, 500)))] = 0.0
@@ -57,7 +68,7 @@ def run(fdm, x, w, inplace=False):
 
 
 KINDS = [("normal", 64), ("scaled", 512), ("integers", 64), ("small_ints", 32), ("powers_of_two", 32),
-         ("outliers", 64), ("leading_zeros", 32), ("tiny_first", 16), ("tiny", 8)]
+         ("outliers", 64), ("dominant", 128), ("leading_zeros", 32), ("tiny_first", 16), ("tiny", 8)]
 
 
 @pytest.mark.parametrize("kind,T", KINDS, ids=[k for k, _ in KINDS])
