@@ -33,6 +33,7 @@ GATE_BYTES = 57344 * 144                     # one Q4_K 2048 x 7168 matrix
 DOWN_BYTES = {"q4k": 57344 * 144, "q6k": 57344 * 210}
 ROUTER_BYTES = 256 * 7168 * 4 + 256 * 4      # W_g + bias
 HIDDEN, FFN = 7168, 2048
+FDM_STREAM_LAYER = 60  # the streamed layer of the stream leg (the resident ones are 3 ..)
 COPY_BYTES = 256 << 20   # calibration copy of the counter passes
 
 
@@ -414,6 +415,77 @@ def bench_dense(F, torch, args, stream, steps=60, warmup=6):
             "frac": round(layer_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def bench_stream(F, torch, args, stream, K, tokens=24):
+    """Streamed layer (fdm_moe_layer_streamed): the 256 routed experts stay in
+    a layer file in the packed layout, held in the host page cache (written
+    here, so every read is a page-cache hit), and are read into an HBM cache
+    of n_cache slots on demand.  Per call: route on the device, the ids to the
+    host, the shared expert and the cache hits launched at once, each miss's
+    kernels queued behind its own chunk copies as its last chunk is read
+    (16 reader threads), combine.  Host wall clock per synchronized call.
+    n_cache 8: a new seeded token per call (nearly every expert a miss);
+    n_cache 256: the warm-up tokens again (every expert a hit)."""
+    import shutil
+    import tempfile
+    from flash_deepseek_amd.synthetic import make_layer, make_tokens
+    lay = make_layer(901, down_q6=(args.down == "q6k"))
+    es = lay.expert_size
+    need = 256 * es
+    folder = None
+    for cand in ("/dev/shm", tempfile.gettempdir()):
+        try:
+            if shutil.disk_usage(cand).free > need + (1 << 30):
+                folder = cand
+                break
+        except OSError:
+            pass
+    if folder is None:
+        return {"skipped": f"no folder with {need / 1e9:.1f} GB free for the layer file"}
+    fd, path = tempfile.mkstemp(prefix="fdm_layer_", suffix=".bin", dir=folder)
+    out = {"layer_file_bytes": need, "expert_bytes": es, "K": K, "reader_threads": 16, "folder": folder}
+    try:
+        with os.fdopen(fd, "wb") as f:
+            for e0 in range(0, 256, 16):
+                f.write(lay.experts[e0 * es:(e0 + 16) * es].cpu().numpy().tobytes())
+        lay.experts = None
+        torch.cuda.empty_cache()
+        L = FDM_STREAM_LAYER
+        hid = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+        warm = 4
+        for n_cache in (8, 256):
+            F.stream_layer(L, path, es, lay.Wg, lay.bias, lay.shared, n_cache=n_cache, n_threads=16)
+            try:
+                hp = make_tokens(warm + tokens, 9100 + n_cache)
+                hi = make_tokens(warm + tokens, 9200 + n_cache)
+                for i in range(warm):
+                    F.moe_layer_streamed(L, hp[i], hi[i], K, hid, stream=stream)
+                torch.cuda.synchronize()
+                pick = (lambda i: i % warm) if n_cache == 256 else (lambda i: warm + i)
+                h0, m0, b0 = F.stream_stats(L)
+                ms = []
+                for i in range(tokens):
+                    t0 = time.perf_counter()
+                    F.moe_layer_streamed(L, hp[pick(i)], hi[pick(i)], K, hid, stream=stream)
+                    torch.cuda.synchronize()
+                    ms.append((time.perf_counter() - t0) * 1e3)
+                F.sync(stream)
+                h1, m1, b1 = F.stream_stats(L)
+                r = {"tokens": tokens, "misses_per_token": round((m1 - m0) / tokens, 2),
+                     "hits_per_token": round((h1 - h0) / tokens, 2),
+                     "expert_mb_read_per_token": round((b1 - b0) / tokens / 1e6, 1)}
+                a = sorted(ms)
+                r["ms_per_token"] = {"median": round(a[len(a) // 2], 3), "p10": round(a[len(a) // 10], 3),
+                                     "p90": round(a[(9 * len(a)) // 10], 3)}
+                tot_s = sum(ms) / 1e3
+                r["expert_read_gbps"] = round((b1 - b0) / tot_s / 1e9, 2) if tot_s > 0 else 0.0
+                out[f"n_cache_{n_cache}"] = r
+            finally:
+                F.release_layer(L)
+    finally:
+        os.unlink(path)
+    return out
+
+
 def bench_attn(F, torch, args, stream, steps=50):
     """MLA attention of decode tokens (one layer, R1 shapes, F16 weights) at
     a cache of args.attn positions: the cache is filled first, then `steps`
@@ -473,6 +545,9 @@ def main():
                     help="also time MLA attention of decode tokens at this KV cache length (0 to skip)")
     ap.add_argument("--dense", type=int, default=3,
                     help="also time the dense FFN over this many F16 dense layers (0 to skip)")
+    ap.add_argument("--stream", type=int, default=1,
+                    help="also time a streamed layer from a page-cached layer file, K = 8, with 8 "
+                         "and 256 cache slots (0 to skip)")
     ap.add_argument("--configs", type=int, default=1,
                     help="also time the single matvec, the single expert (Q4_K and Q6_K down) "
                          "and the Q6_K-down layer (0 to skip)")
@@ -642,6 +717,8 @@ def main():
         result["dense"] = bench_dense(F, torch, args, stream)
     if args.attn:
         result["attn"] = bench_attn(F, torch, args, stream)
+    if args.stream:
+        result["stream"] = bench_stream(F, torch, args, stream, K)
     if not args.no_cpu_baseline:
         ref, tuned = cpu_baseline(args.down, args.cpu_seconds, K)
         result["cpu_baseline"] = ref

@@ -1868,9 +1868,9 @@ int fdm_moe_layer_streamed(int L, const float* d_h_post, const float* d_h_in, in
   FDM_HIP(hipStreamSynchronize(s));
   std::lock_guard<std::mutex> lock(y.mu);
   FDM_HIP(hipEventSynchronize(y.done));  // the previous call's kernels have read the cache
-  // the selected experts into the cache (parallel pread, infer.m:1577-1602)
   std::string err;
-  if (int rc = y.es.fetch(w.ids_h, K, w.slots_h, &err)) return fail(rc, "layer %d: %s", L, err.c_str());
+  bool miss[FDM_MAX_K];
+  if (int rc = y.es.plan(w.ids_h, K, w.slots_h, miss, &err)) return fail(rc, "layer %d: %s", L, err.c_str());
   FDM_HIP(hipMemcpyAsync(w.stage_idx, w.slots_h, K * sizeof(int), hipMemcpyHostToDevice, s));
   SlotTable t;
   t.experts = y.es.cache();
@@ -1883,8 +1883,28 @@ int fdm_moe_layer_streamed(int L, const float* d_h_post, const float* d_h_in, in
   t.n_slots = K + (y.shared ? 1 : 0);
   t.rel = false;
   FDM_HIP(launch_xdigits(d_h_post, FDM_HIDDEN / 64, w.xd, s));
-  FDM_HIP(launch_gateup(t, w.xd, w.act, w.act_xd, w.gu_count, s));
-  FDM_HIP(launch_down_combine(t, y.q6, w.act_xd, d_h_in, d_hidden, nullptr, w.eo, w.dn_count, s));
+  // the shared expert and the cache hits at once, in one launch pair ...
+  SlotTable now = t;
+  for (int k = 0; k < K; ++k)
+    if (miss[k]) now.skip |= 1u << k;
+  if (now.skip != (1u << t.n_slots) - 1) {
+    FDM_HIP(launch_gateup(now, w.xd, w.act, w.act_xd, w.gu_count, s));
+    FDM_HIP(launch_down_combine(now, y.q6, w.act_xd, d_h_in, d_hidden, nullptr, w.eo, w.dn_count, s));
+  }
+  // ... and each miss as soon as its copies land, while the others are read
+  // (whichever launch completes a row tile's last slot combines it, in slot
+  // order: the same bits as one launch)
+  auto ready = [&](int k) -> int {
+    if (launch_gateup(t, w.xd, w.act, w.act_xd, w.gu_count, s, k, 1) != hipSuccess ||
+        launch_down_combine(t, y.q6, w.act_xd, d_h_in, d_hidden, nullptr, w.eo, w.dn_count, s, k, 1) != hipSuccess)
+      return FDM_E_HIP;
+    return FDM_OK;
+  };
+  const int read_rc = y.es.read(s, ready, &err);
+  if (read_rc != FDM_OK) {
+    (void)hipEventRecord(y.done, s);
+    return fail(read_rc, "layer %d: %s", L, err.c_str());
+  }
   FDM_HIP(hipEventRecord(y.done, s));
   if (d_idx) FDM_HIP(hipMemcpyAsync(d_idx, w.idx, K * sizeof(int), hipMemcpyDeviceToDevice, s));
   if (d_w) FDM_HIP(hipMemcpyAsync(d_w, w.w, K * sizeof(float), hipMemcpyDeviceToDevice, s));

@@ -7,6 +7,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <functional>
 #include <string>
 #include <unordered_map>
 #include <utility>
@@ -81,19 +82,26 @@ struct SlotTable {
   int K;                   // routed slots
   int n_slots;             // K or K + 1 (shared)
   bool rel;                // blobs in the resident expert layout (else packed)
+  int slot0 = 0;           // the first slot a launch runs (set by the launch functions)
+  uint32_t skip = 0;       // bit k: slot k is not run by this launch (another launch runs it)
 };
-// gate/up matvecs + SwiGLU for every slot; writes act[slot][2048] and the
-// digits of act (act_xd[slot][32]).  counters: (FDM_MAX_K + 1) x 64 ints,
-// zero on entry and left zero.
+// gate/up matvecs + SwiGLU for slots slot0 .. slot0 + n_run - 1 (n_run < 0:
+// every slot), except those t.skip names; writes act[slot][2048] and the digits of act
+// (act_xd[slot][32]).  counters: (FDM_MAX_K + 1) x 64 ints, zero on entry
+// and left zero.
 hipError_t launch_gateup(const SlotTable& t, const XGroup* xd, float* act, XGroup* act_xd,
-                         int* counters, hipStream_t s);
-// down matvecs for every slot (into eo[slot][7168]) and the combine:
+                         int* counters, hipStream_t s, int slot0 = 0, int n_run = -1);
+// down matvecs for slots slot0 .. slot0 + n_run - 1 (n_run < 0: every slot),
+// except those t.skip names, into eo[slot][7168]; the launches of one call
+// may split the slots
+// between them, and whichever launch completes a row tile's n_slots-th
+// slot combines it:
 //   out[i] = (h_in[i] + sum_{k<K} w[k] * E_k[i]) + S[i]
 // moe_out (optional) receives sum_k w[k] * E_k[i].  counters: 448 ints,
-// zero on entry and left zero.
+// zero on entry and left zero once every slot of the call has run.
 hipError_t launch_down_combine(const SlotTable& t, bool down_q6, const XGroup* act_xd,
                                const float* h_in, float* out, float* moe_out, float* eo,
-                               int* counters, hipStream_t s);
+                               int* counters, hipStream_t s, int slot0 = 0, int n_run = -1);
 
 // layer_kernel.hip
 // The batch-1 MoE layer of one token in one launch: digits, router, route,
@@ -290,8 +298,21 @@ class ExpertStream {
   // FDM_OK or an FDM_E_* code with *err set
   int open(const char* path, size_t expert_size, int n_experts, int n_cache, int n_threads, int device,
            std::string* err);
-  // makes experts ids[0..K) resident; slots[k] = the cache slot of ids[k]
-  int fetch(const int* ids, int K, int* slots, std::string* err);
+  // The cache bookkeeping of one token: slots[k] = the cache slot of
+  // ids[k]; miss[k] = its blob is to be read by read().  FDM_OK or
+  // FDM_E_INVAL with *err set.
+  int plan(const int* ids, int K, int* slots, bool* miss, std::string* err);
+  // Reads the planned misses with the pool's threads (4 MB chunks, each
+  // copied host-to-device on its thread's stream behind an event) and, on
+  // the calling thread, as the last chunk copy of a miss is queued: makes
+  // `compute` wait for that miss's copies, then calls ready(k) for each
+  // slot k holding it, so its kernels run as soon as it lands while other
+  // misses are still read.  Returns once every read and every ready() call
+  // is done (the copies may still be in flight).  On a read or copy error
+  // the misses not read in full leave the cache, ready() is still called
+  // for their slots (so the caller's launches complete its call), and the
+  // error is returned.
+  int read(hipStream_t compute, const std::function<int(int)>& ready, std::string* err);
   uint8_t* cache() const { return cache_; }
   int n_cache() const { return n_cache_; }
   uint64_t hits() const { return hits_; }
@@ -306,6 +327,12 @@ class ExpertStream {
   std::vector<int> slot_of_, expert_in_;
   std::vector<uint64_t> last_use_;
   uint64_t tick_ = 0, hits_ = 0, misses_ = 0, bytes_ = 0;
+  struct Miss {
+    int expert, slot;
+    std::vector<int> ks;  // the token's slots holding it
+  };
+  std::vector<Miss> plan_;           // the planned misses of the current token
+  std::vector<hipEvent_t> chunk_ev_;  // one per chunk of up to FDM_MAX_K misses
 };
 // frees the pinned read buffers shared by all streamed layers
 void release_stream_pool();

@@ -14,8 +14,9 @@
 //   to finish turns the sub-block's activations into the digits the down
 //   matvec reads (a per-sub-block arrival counter).
 // k_down    one workgroup per (slot, 16-row tile): the slot's down rows.
-//   The last of the slots of a row tile to finish combines them in slot
-//   order, then adds the shared expert and the residual
+//   The last of the slots of a row tile to finish (in this launch or an
+//   earlier one of the same call: streamed layers launch slot by slot)
+//   combines them in slot order, then adds the shared expert and the residual
 //   (moe_out += w_k * E_k, infer.m:1690-1695; hidden = h_in + moe_out + sd,
 //   infer.m:1922).
 #include "fdm_internal.h"
@@ -40,7 +41,8 @@ __global__ __launch_bounds__(256) void k_gateup(SlotTable t, const XGroup* __res
                                                 int* __restrict__ counters) {
   __shared__ XGroup xs[kHidden / 64];
   __shared__ int last;
-  const int slot = blockIdx.x / kGuTiles, tile = blockIdx.x % kGuTiles;
+  const int slot = t.slot0 + blockIdx.x / kGuTiles, tile = blockIdx.x % kGuTiles;
+  if ((t.skip >> slot) & 1u) return;  // another launch of the call runs this slot
   const uint8_t* blob = slot_blob(t, slot);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
@@ -112,7 +114,8 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
                                               int* __restrict__ counters) {
   __shared__ XGroup xs[kFfn / 64];
   __shared__ int last;
-  const int slot = blockIdx.y, tile = blockIdx.x;
+  const int slot = t.slot0 + (int)blockIdx.y, tile = blockIdx.x;
+  if ((t.skip >> slot) & 1u) return;  // another launch of the call runs this slot
   const uint8_t* blob = slot_blob(t, slot);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15;
@@ -191,21 +194,28 @@ __global__ __launch_bounds__(256) void k_down(SlotTable t, const XGroup* __restr
 }
 
 hipError_t launch_gateup(const SlotTable& t, const XGroup* xd, float* act, XGroup* act_xd,
-                         int* counters, hipStream_t s) {
-  hipLaunchKernelGGL(k_gateup, dim3(kGuTiles * t.n_slots), dim3(256), 0, s, t, xd, act, act_xd,
-                     counters);
+                         int* counters, hipStream_t s, int slot0, int n_run) {
+  SlotTable r = t;
+  r.slot0 = slot0;
+  const int n = n_run < 0 ? t.n_slots - slot0 : n_run;
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gateup, dim3(kGuTiles * n), dim3(256), 0, s, r, xd, act, act_xd, counters);
   return hipGetLastError();
 }
 
 hipError_t launch_down_combine(const SlotTable& t, bool down_q6, const XGroup* act_xd,
                                const float* h_in, float* out, float* moe_out, float* eo,
-                               int* counters, hipStream_t s) {
-  const dim3 grid(kDnTiles, t.n_slots), block(256);
+                               int* counters, hipStream_t s, int slot0, int n_run) {
+  SlotTable r = t;
+  r.slot0 = slot0;
+  const int n = n_run < 0 ? t.n_slots - slot0 : n_run;
+  if (n <= 0) return hipSuccess;
+  const dim3 grid(kDnTiles, n), block(256);
   if (down_q6)
-    hipLaunchKernelGGL(k_down<true>, grid, block, 0, s, t, act_xd, h_in, out, moe_out, eo,
+    hipLaunchKernelGGL(k_down<true>, grid, block, 0, s, r, act_xd, h_in, out, moe_out, eo,
                        counters);
   else
-    hipLaunchKernelGGL(k_down<false>, grid, block, 0, s, t, act_xd, h_in, out, moe_out, eo,
+    hipLaunchKernelGGL(k_down<false>, grid, block, 0, s, r, act_xd, h_in, out, moe_out, eo,
                        counters);
   return hipGetLastError();
 }
