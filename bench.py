@@ -422,7 +422,7 @@ def bench_stream(F, torch, args, stream, K, tokens=24):
     of n_cache slots on demand.  Per call: route on the device, the ids to the
     host, the shared expert and the cache hits launched at once, each miss's
     kernels queued behind its own chunk copies as its last chunk is read
-    (16 reader threads), combine.  Host wall clock per synchronized call.
+    (32 reader threads), combine.  Host wall clock per synchronized call.
     n_cache 8: a new seeded token per call (nearly every expert a miss);
     n_cache 256: the warm-up tokens again (every expert a hit)."""
     import shutil
@@ -442,7 +442,7 @@ def bench_stream(F, torch, args, stream, K, tokens=24):
     if folder is None:
         return {"skipped": f"no folder with {need / 1e9:.1f} GB free for the layer file"}
     fd, path = tempfile.mkstemp(prefix="fdm_layer_", suffix=".bin", dir=folder)
-    out = {"layer_file_bytes": need, "expert_bytes": es, "K": K, "reader_threads": 16, "folder": folder}
+    out = {"layer_file_bytes": need, "expert_bytes": es, "K": K, "reader_threads": 32, "folder": folder}
     try:
         with os.fdopen(fd, "wb") as f:
             for e0 in range(0, 256, 16):
@@ -453,7 +453,7 @@ def bench_stream(F, torch, args, stream, K, tokens=24):
         hid = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
         warm = 4
         for n_cache in (8, 256):
-            F.stream_layer(L, path, es, lay.Wg, lay.bias, lay.shared, n_cache=n_cache, n_threads=16)
+            F.stream_layer(L, path, es, lay.Wg, lay.bias, lay.shared, n_cache=n_cache, n_threads=32)
             try:
                 hp = make_tokens(warm + tokens, 9100 + n_cache)
                 hi = make_tokens(warm + tokens, 9200 + n_cache)

@@ -16,10 +16,14 @@
 //   router row e (256)
 //   route: the expert set (1);  the exact route() (1)
 //   shared expert: gate/up items of both column parts, then the digit
-//     records of its activations (one item per part)
-//   routed experts, part-major: gate/up items of part q of every slot and
-//     the digit records of part q of every slot, then the down items of
-//     part q - lag of every slot, q = 0, 1, ...
+//     records of its activations (one item per part; in the expert-only
+//     list, where the final items are the next step, they make the records
+//     themselves)
+//   routed experts, part-major: gate/up items of part q of every slot, then
+//     the down items of part q - lag of every slot, q = 0, 1, ...; a down
+//     item makes its part's activation records itself from the tagged
+//     activations (no digit item between: one coherent round trip less on
+//     the tail)
 //   final items: the shared expert's down rows and the combine of the
 //     same rows (224)
 //
@@ -104,6 +108,9 @@ constexpr int kGuPerPart = kPartCols / kGuTileRows / kGuPer;  // gate/up items p
 static_assert(kGuPerPart * kGuTileRows * kGuPer == kPartCols, "gate/up items tile a part");
 // Q4_K down item: one lane per 64-element group of a row's part, kDnRowsQ4L
 // rows per lane.  Q6_K down item: one lane per 128-element half block.
+#ifndef FDM_ACT_DIRECT
+#define FDM_ACT_DIRECT 1
+#endif
 #ifndef FDM_LAYER_DNROWS
 #define FDM_LAYER_DNROWS 7
 #endif
@@ -166,7 +173,9 @@ __device__ __forceinline__ const uint8_t* expert_blob(const LayerArgs& a, int e)
 }
 
 // Thread 0 waits for the digits of h_post and, for a routed slot, for the
-// slot's expert; the expert id lands in sm.eid.
+// slot's expert; the expert id lands in sm.eid.  (One tagged flag per digit
+// item, polled by 28 threads, measured slower: every waiting gate/up item
+// then loads 28 words per round.)
 __device__ __forceinline__ void wait_route_xd(const LayerArgs& a, int slot, bool routed,
                                               bool need_xd, LayerSmem& sm) {
   poll_all(a, [&] {
@@ -461,6 +470,29 @@ __device__ __forceinline__ uint64_t* act_xd_words(const LayerArgs& a, int slot, 
   return a.act_xd + ((size_t)slot * (kFfn / 64) + group) * kXgWords;
 }
 
+// A poll of a whole digit record (hundreds of tagged words per round):
+// full() loads and checks every word.  When the first round finds the
+// record incomplete, thread 0 polls only one or two sentinel words of it
+// until they carry the epoch, then full() runs again (words land in any
+// order, so it still checks every tag): an item that waits long -- down and
+// final items are resident from the start of short lists -- would otherwise
+// reload every word each round, kilobytes of coherent loads per item
+// competing with the weight stream.  A record already complete costs one
+// round, as a plain poll.
+template <typename F>
+__device__ __forceinline__ void poll_record(const LayerArgs& a, const uint64_t* s0, const uint64_t* s1, F&& full) {
+  for (;;) {
+    if (__syncthreads_and(full())) return;
+    const bool ok = poll_all(a, [&] {
+      if (threadIdx.x != 0) return true;
+      bool got = tag_is(get_tagged(s0), a.epoch);
+      if (s1) got = got && tag_is(get_tagged(s1), a.epoch);
+      return got;
+    });
+    if (!ok) return;  // gave up: the error flag is set
+  }
+}
+
 __device__ __forceinline__ void adg_item(const LayerArgs& a, int slot, int part, LayerSmem& sm) {
   const int wave = threadIdx.x >> 6;
   const uint64_t* act = a.act + (size_t)slot * kFfn + part * kPartCols;
@@ -493,7 +525,7 @@ __device__ __forceinline__ void stage_act_digits(const LayerArgs& a, int slot, i
   constexpr int kW = NG * kXgWords, kPer = (kW + 255) / 256;
   const uint64_t* src = act_xd_words(a, slot, group0);
   uint32_t w[kPer];
-  poll_all(a, [&] {
+  poll_record(a, src + kW - 1, nullptr, [&] {
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -512,6 +544,30 @@ __device__ __forceinline__ void stage_act_digits(const LayerArgs& a, int slot, i
     const int k = threadIdx.x + 256 * i;
     if (k < kW) dst[k] = w[i];
   }
+  __syncthreads();
+}
+
+// The records of part `part` of a slot's activations made here, from the
+// part's 1024 tagged activations (four per thread), into sm.xs[0 .. 16):
+// no hand-off through a digit item (a coherent round trip each way).
+__device__ __forceinline__ void stage_act_direct(const LayerArgs& a, int slot, int part, LayerSmem& sm) {
+  const int wave = threadIdx.x >> 6;
+  const uint64_t* act = a.act + (size_t)slot * kFfn + part * kPartCols;
+  constexpr int kPer = kPartCols / 256;
+  float v[kPer];
+  poll_record(a, act + kPartCols - 1, nullptr, [&] {
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const uint64_t t = get_tagged(act + threadIdx.x + 256 * i);
+      ok = ok && tag_is(t, a.epoch);
+      v[i] = tagged_f(t);
+    }
+    return ok;
+  });
+  // element 256 i + 64 w + lane lives in wave w's lanes: record 4 i + w
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) digits_to_lds(v[i], sm.xs[4 * i + wave]);
   __syncthreads();
 }
 
@@ -540,7 +596,10 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
 #pragma unroll
       for (int j = 0; j < kDnRowsQ4L; ++j) ld[j] = rel_load_group<true>(dbase, row0 + RPW * j, blk, gl & 3);
     }
-    stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
+    if (FDM_ACT_DIRECT)
+      stage_act_direct(a, slot, part, sm);
+    else
+      stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
     float acc[kDnRowsQ4L] = {};
     // the lane's rows share one digit record: each quarter of it is read
     // from LDS once for all of them
@@ -566,7 +625,10 @@ __device__ __forceinline__ void down_part(const LayerArgs& a, int slot, int part
 #pragma unroll
       for (int j = 0; j < kDnRowsQ6L; ++j) l6[j] = q6k_rel_load_half(dbase, row0 + 8 * j, part * 4 + b, h);
     }
-    stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
+    if (FDM_ACT_DIRECT)
+      stage_act_direct(a, slot, part, sm);
+    else
+      stage_act_digits<kPartGroups>(a, slot, part * kPartGroups, sm);
     float acc[kDnRowsQ6L] = {};
     if (blob) {
 #pragma unroll
@@ -613,7 +675,10 @@ static_assert(kParts == 2, "final items: two column parts");
 #ifndef FDM_FIN_ROWS_Q6
 #define FDM_FIN_ROWS_Q6 16  // two Q6_K half-block loads per lane would not fit 128 VGPRs
 #endif
-constexpr int kFinRowsQ4 = 32, kFinRowsQ6 = FDM_FIN_ROWS_Q6;
+#ifndef FDM_FIN_ROWS_Q4
+#define FDM_FIN_ROWS_Q4 32
+#endif
+constexpr int kFinRowsQ4 = FDM_FIN_ROWS_Q4, kFinRowsQ6 = FDM_FIN_ROWS_Q6;
 __host__ __device__ constexpr int fin_rows(bool q6) { return q6 ? kFinRowsQ6 : kFinRowsQ4; }
 __host__ __device__ constexpr int fin_items(bool q6) { return kHidden / fin_rows(q6); }
 constexpr int kFinMaxRouted = kLayerMaxSlots - 1;             // routed slots (FDM_MAX_K)
@@ -672,6 +737,12 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
   const int nE = 2 * a.K * R;  // word e: slot e / (2 R), part e / R % 2, row e % R
   const uint64_t* xsrc = act_xd_words(a, a.K, 0);
   uint32_t xw[kXPer];
+  // one expert (the expert-only list): its activations' records are made
+  // here from the 2048 tagged activations, no digit items
+  constexpr bool kDirect = PACKED && FDM_ACT_DIRECT;
+  constexpr int kAPer = kFfn / 256;
+  const uint64_t* sact = a.act + (size_t)a.K * kFfn;
+  float av[kDirect ? kAPer : 1];
   float ev[kEPer];
   uint64_t tw = 0, tp = 0;
   bool e_ok = true;
@@ -705,27 +776,46 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
       sm.cperm[threadIdx.x] = tagged_i(tp);
     }
   };
-  poll_all(a, [&] {
+  // the last word of each part's records (activations) as sentinels
+  // (without a shared expert the first round always succeeds)
+  poll_record(a, kDirect ? sact + kPartCols - 1 : xsrc + kXW / 2 - 1, kDirect ? sact + kFfn - 1 : xsrc + kXW - 1, [&] {
     bool ok = true;
     if (dbase) {
+      if constexpr (kDirect) {
 #pragma unroll
-      for (int i = 0; i < kXPer; ++i) {
-        const int k = threadIdx.x + 256 * i;
-        if (k < kXW) {
-          const uint64_t t = get_tagged(xsrc + k);
+        for (int i = 0; i < kAPer; ++i) {
+          const uint64_t t = get_tagged(sact + threadIdx.x + 256 * i);
           ok = ok && tag_is(t, a.epoch);
-          xw[i] = (uint32_t)t;
+          av[i] = tagged_f(t);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kXPer; ++i) {
+          const int k = threadIdx.x + 256 * i;
+          if (k < kXW) {
+            const uint64_t t = get_tagged(xsrc + k);
+            ok = ok && tag_is(t, a.epoch);
+            xw[i] = (uint32_t)t;
+          }
         }
       }
     }
     load_routed();
     return ok;
   });
-  uint32_t* xdst = reinterpret_cast<uint32_t*>(sm.fin.xs);
+  if constexpr (kDirect) {
+    // element 256 i + 64 w + lane lives in wave w's lanes: record 4 i + w
+    if (dbase) {
 #pragma unroll
-  for (int i = 0; i < kXPer; ++i) {
-    const int k = threadIdx.x + 256 * i;
-    if (dbase && k < kXW) xdst[k] = xw[i];
+      for (int i = 0; i < kAPer; ++i) digits_to_lds(av[i], sm.fin.xs[4 * i + wave]);
+    }
+  } else {
+    uint32_t* xdst = reinterpret_cast<uint32_t*>(sm.fin.xs);
+#pragma unroll
+    for (int i = 0; i < kXPer; ++i) {
+      const int k = threadIdx.x + 256 * i;
+      if (dbase && k < kXW) xdst[k] = xw[i];
+    }
   }
   store_routed();
   const bool routed_ready = __syncthreads_and(e_ok);
@@ -801,6 +891,7 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
 //     slot and then the activation digits of part q of every slot (q < P),
 //     then down of part q - lag of every slot (q >= lag)
 //   | final items (shared down + combine)
+constexpr int kAdgRouted = FDM_ACT_DIRECT ? 0 : 1;  // activation digit items per routed (slot, part)
 struct LayerList {
   int route, exact, router, xd, shared, shadg, routed, fin, total;
   int gup, dnp;  // gate/up and down items per (slot, part)
@@ -820,8 +911,11 @@ __host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, boo
   l.exact = l.route + (expert ? 0 : 1);
   l.shared = l.exact + (expert ? 0 : 1);
   l.shadg = l.shared + hs * kParts * l.gup;
-  l.routed = l.shadg + hs * kParts;
-  l.fin = l.routed + K * kParts * (l.gup + 1 + l.dnp);
+  // activation digit items: the shared expert's (at the head, off the
+  // critical path) unless the list has only it; routed slots' down items
+  // make their records themselves
+  l.routed = l.shadg + ((expert && FDM_ACT_DIRECT) ? 0 : hs * kParts);
+  l.fin = l.routed + K * kParts * (l.gup + kAdgRouted + l.dnp);
   l.total = l.fin + fin_items(q6);
   return l;
 }
@@ -831,7 +925,7 @@ __host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, boo
 // (slot, part).
 __device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, int& kind, int& slot,
                                             int& part, int& idx) {
-  const int GU = K * l.gup, G = GU + K, D = K * l.dnp;
+  const int GU = K * l.gup, G = GU + K * kAdgRouted, D = K * l.dnp;
   int q, r;
   if (off < kLag * G) {
     q = off / G;

@@ -283,7 +283,9 @@ hipError_t launch_matvec1(const MatvecArgs& a, bool q6, hipStream_t s) {
 }
 
 // ---- one launch by column parts (Q4_K, in_dim = 1024 P) -------------------------------
-// Items of 256 threads, part-major: (part p, 16-row block).  An item turns its
+// Items of 256 threads, part-major: (part p, 16-row block).  (Row-block-major
+// order, where a row block's P items read its whole rows together, measured
+// no faster.)  An item turns its
 // part's 1024 activations into digit records itself (4 KB of x: no hand-off
 // before the math), contracts its 16 rows x 4 blocks (16 lanes per row, one
 // 64-element group each) and publishes each row's partial sum as a tagged
@@ -300,10 +302,12 @@ __global__ __launch_bounds__(256) void k_matvec2_q4k(Matvec2Args a) {
   const int row = 16 * rb + 4 * wave + (lane >> 4);
   const int l16 = lane & 15, g = l16 & 3;
   const uint8_t* bp = a.W + ((size_t)min(row, a.rows - 1) * (4 * P) + 4 * p + (l16 >> 2)) * kQ4KBlock;
-  const Q4KGroupLoad ld = q4k_load_group(bp, g);
+  // x before the weights: loads return in order, so the digits are made
+  // while the weights are still in flight
   float xv[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) xv[i] = a.x[1024 * p + 64 * (4 * wave + i) + lane];
+  const Q4KGroupLoad ld = q4k_load_group(bp, g);
 #pragma unroll
   for (int i = 0; i < 4; ++i) digits_to_lds(xv[i], xs[4 * wave + i]);
   __syncthreads();
@@ -316,20 +320,28 @@ __global__ __launch_bounds__(256) void k_matvec2_q4k(Matvec2Args a) {
   __syncthreads();
   const int r = 16 * rb + (int)threadIdx.x;
   if (threadIdx.x >= 16 || r >= a.rows) return;
+  // the earlier parts' partials of row r: every load in flight at once,
+  // again for those not yet published
+  uint64_t v[P > 1 ? P - 1 : 1];
+#pragma unroll
+  for (int q = 0; q < P - 1; ++q) v[q] = get_tagged(a.part + (size_t)q * a.rows + r);
+  for (unsigned n = 0;; ++n) {
+    bool all = true;
+#pragma unroll
+    for (int q = 0; q < P - 1; ++q) all = all && tag_is(v[q], a.epoch);
+    if (all) break;
+    if (n >= a.spin_limit || ((n & 63) == 63 && load_u32_agent(a.err) == a.epoch)) {
+      store_u32_agent(a.err, a.epoch);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+    for (int q = 0; q < P - 1; ++q)
+      if (!tag_is(v[q], a.epoch)) v[q] = get_tagged(a.part + (size_t)q * a.rows + r);
+  }
   float sum = 0.0f;
 #pragma unroll
-  for (int q = 0; q < P - 1; ++q) {
-    uint64_t v = get_tagged(a.part + (size_t)q * a.rows + r);
-    for (unsigned n = 0; !tag_is(v, a.epoch); ++n) {
-      if (n >= a.spin_limit || ((n & 63) == 63 && load_u32_agent(a.err) == a.epoch)) {
-        store_u32_agent(a.err, a.epoch);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-      v = get_tagged(a.part + (size_t)q * a.rows + r);
-    }
-    sum = q == 0 ? tagged_f(v) : sum + tagged_f(v);
-  }
+  for (int q = 0; q < P - 1; ++q) sum = q == 0 ? tagged_f(v[q]) : sum + tagged_f(v[q]);
   a.y[r] = P == 1 ? own[threadIdx.x] : sum + own[threadIdx.x];
 }
 
