@@ -109,11 +109,11 @@ int bind_scratch(int device) {
 // Per-token scratch of the attention (grown to the largest max_seq).
 struct AttnScratch {
   float *normed = nullptr, *q_a = nullptr, *q_a_n = nullptr, *q = nullptr, *kv_a = nullptr, *c_kv_n = nullptr;
-  float *q_abs = nullptr, *scores = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr;
+  float *q_abs = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr, *stat = nullptr;
   int seq = 0;
   void release() {
     // kv_a lives in q_a's allocation (the two projections run as one matvec)
-    for (float* p : {normed, q_a, q_a_n, q, c_kv_n, q_abs, scores, wc, attn, part})
+    for (float* p : {normed, q_a, q_a_n, q, c_kv_n, q_abs, wc, attn, part, stat})
       if (p) (void)hipFree(p);
     *this = AttnScratch();
   }
@@ -1956,10 +1956,9 @@ static int ensure_attn(Workspace& w, int seq, hipStream_t s) {
   FDM_HIP(hipStreamSynchronize(s));
   ws.release();
   const size_t H = FDM_HIDDEN, QA = 1536, QB = 128 * 192, KVA = 576, O = 128 * 128;
-  const size_t n[] = {H, QA + KVA, QA, QB, 512, 128 * 512, (size_t)128 * seq, 128 * 512, O,
-                      (size_t)((seq + 63) / 64) * 128 * 512};
-  float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.c_kv_n, &ws.q_abs, &ws.scores, &ws.wc, &ws.attn,
-                 &ws.part};
+  const size_t n[] = {H, QA + KVA, QA, QB, 512, 128 * 512, 128 * 512, O, (size_t)((seq + 63) / 64) * 128 * 512,
+                      (size_t)((seq + 63) / 64) * 128 * 2};
+  float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.c_kv_n, &ws.q_abs, &ws.wc, &ws.attn, &ws.part, &ws.stat};
   for (int i = 0; i < 10; ++i)
     if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
       ws.release();
@@ -2139,10 +2138,10 @@ int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
   m.k_b = a.k_b;
   m.v_b = a.v_b;
   m.q_abs = ws.q_abs;
-  m.scores = ws.scores;
   m.wc = ws.wc;
   m.attn = ws.attn;
   m.part = ws.part;
+  m.stat = ws.stat;
   m.scale = (mscale * mscale) / sqrtf(192.0f);
   FDM_HIP(launch_mla_attend(m, s));
   FDM_HIP(launch_mv_f16(a.o_proj, ws.attn, d_hidden, d_hidden, FDM_HIDDEN, 128 * 128, s));

@@ -277,17 +277,16 @@ struct MlaArgs {
   int pos, len;          // RoPE position; cache rows before this token
   float *cache_c, *cache_k;  // [max_seq][512], [max_seq][64]
   const uint16_t *k_b, *v_b;  // F16 [128][512][128], [128][128][512]
-  float *q_abs, *scores, *wc, *attn;  // [128][512], [128][S], [128][512], [128][128]
+  float *q_abs, *wc, *attn;  // [128][512], [128][512], [128][128]
   float* part;                        // [ceil(S / 64)][128][512] partial latent sums
+  float* stat;                        // [ceil(S / 64)][128][2]: each chunk's max score and exp sum
   float scale;
 };
 // y[r] = (res ? res[r] : 0) + W[r] . x; cols % 512 == 0, cols <= 16384
 hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, float* y, int rows, int cols,
                          hipStream_t s);
-// y[h][r] = W[h][r] . x[h * x_stride ..]; cols 128 or 512
-hipError_t launch_mv_f16_heads(const uint16_t* W, const float* x, int x_stride, float* y, int heads, int rows_h,
-                               int cols, hipStream_t s);
-// RoPE + cache append, Q_abs, scores, softmax, weighted latent sum, v_b
+// RoPE + cache append, Q_abs, then scores + softmax + weighted latent sum by
+// chunks, the chunks merged and v_b
 hipError_t launch_mla_attend(const MlaArgs& a, hipStream_t s);
 
 // expert_stream.hip: routed experts read from a packed layer file into an
