@@ -486,10 +486,15 @@ def bench_stream(F, torch, args, stream, K, tokens=24):
     return out
 
 
-def bench_attn(F, torch, args, stream, steps=50):
+def bench_attn(F, torch, args, stream, steps=50, K=8):
     """MLA attention of decode tokens (one layer, R1 shapes, F16 weights) at
     a cache of args.attn positions: the cache is filled first, then `steps`
-    tokens are timed (positions args.attn .. args.attn + steps - 1)."""
+    tokens are timed (positions args.attn .. args.attn + steps - 1).  Then
+    the reference's whole MoE decode layer (layer_forward, infer.m:1837-1924)
+    as one chain per token, for `steps` more tokens: attention with its
+    residual (fdm_attn_forward), then rms_norm + router + route + experts +
+    combine + residual in one launch (fdm_moe_layer_norm, over the rotated
+    resident MoE layers), in place on the token's hidden state."""
     g = torch.Generator(device="cuda").manual_seed(766)
 
     def f16(rows, cols, *lead):
@@ -503,9 +508,9 @@ def bench_attn(F, torch, args, stream, steps=50):
          "q_b": f16(128 * 192, 1536), "kv_a": f16(576, HIDDEN), "kv_a_norm": norm(512),
          "k_b": f16(512, 128, 128), "v_b": f16(128, 512, 128), "o_proj": f16(HIDDEN, 128 * 128)}
     S = args.attn
-    F.attn_upload(0, w, max_seq=S + steps)
+    F.attn_upload(0, w, max_seq=S + 2 * steps)
     wbytes = sum(a.nbytes for a in w.values())
-    X = torch.randn((S + steps, HIDDEN), generator=g, device="cuda")
+    X = torch.randn((S + 2 * steps, HIDDEN), generator=g, device="cuda")
     for pos in range(S):
         F.attn_forward(0, X[pos], pos, stream=stream)
     torch.cuda.synchronize()
@@ -518,12 +523,28 @@ def bench_attn(F, torch, args, stream, steps=50):
     dt = (time.perf_counter() - t0) / steps
     n, tot, mn, mx = F.prof_read("attn")
     F.prof_enable(False)
-    F.attn_release(0)
     kern = tot / n * 1e-3 if n else dt
     step_bytes = wbytes + (S + steps // 2) * 576 * 4 * 3
-    return {"cache_len": S, "us_per_token": round(dt * 1e6, 2), "kernels_us": round(kern * 1e6, 2),
-            "weight_bytes": wbytes, "gbps": round(step_bytes / kern / 1e9, 1),
-            "frac": round(step_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)}
+    out = {"cache_len": S, "us_per_token": round(dt * 1e6, 2), "kernels_us": round(kern * 1e6, 2),
+           "weight_bytes": wbytes, "gbps": round(step_bytes / kern / 1e9, 1),
+           "frac": round(step_bytes / kern / 1e9 / HBM_PEAK_GBPS, 4)}
+    # the whole decode layer, chained per token on one stream
+    nw = (1.0 + 0.1 * torch.randn(HIDDEN, generator=g, device="cuda")).contiguous()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i, pos in enumerate(range(S + steps, S + 2 * steps)):
+        F.attn_forward(0, X[pos], pos, stream=stream)
+        F.moe_layer_norm(3 + i % args.layers, X[pos], nw, K, X[pos], stream=stream)
+    torch.cuda.synchronize()
+    F.sync(stream)
+    dl = (time.perf_counter() - t0) / steps
+    F.attn_release(0)
+    out["decode_layer"] = {
+        "workload": "layer_forward of a MoE layer at batch 1: MLA attention at this cache length + residual, "
+                    "then rms_norm + router + route + 8 routed and 1 shared expert + combine + residual "
+                    f"({args.layers} resident MoE layers rotated), in place, chained on one stream",
+        "tokens": steps, "us_per_token": round(dl * 1e6, 2)}
+    return out
 
 
 def main():
@@ -716,7 +737,7 @@ def main():
     if args.dense:
         result["dense"] = bench_dense(F, torch, args, stream)
     if args.attn:
-        result["attn"] = bench_attn(F, torch, args, stream)
+        result["attn"] = bench_attn(F, torch, args, stream, K=K)
     if args.stream:
         result["stream"] = bench_stream(F, torch, args, stream, K)
     if not args.no_cpu_baseline:
