@@ -341,10 +341,9 @@ __device__ __forceinline__ void route_item(const LayerArgs& a) {
   float sc[4];
   wait_scores(a, sc);
   if (threadIdx.x >= 64) return;
-  // each slot goes out as soon as it is certain: the first after two
-  // extractions, so slot 0's weights stream while the set is completed
+  // every slot goes out as soon as it is certain (all at once for K <= 8)
   route_set_publish(sc, bj, a.K, [&](int slot, int id) {
-    if (lane == 0) put_tagged(a.prov + slot, a.epoch, (uint32_t)id);
+    if (slot >= 0) put_tagged(a.prov + slot, a.epoch, (uint32_t)id);
   });
 }
 

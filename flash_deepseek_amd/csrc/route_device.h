@@ -283,27 +283,103 @@ __device__ __forceinline__ bool topk_set(const int vk[4], int K, int& id_out) {
 }
 
 // ---- the expert set, largest first, published slot by slot -------------------------------
-// Maximum of an int over the whole wave (uniform result).
+// Maximum of an int over the whole wave (uniform result): DPP row shifts
+// leave each row's maximum in its lane 15, row_bcast:15 folds rows 0 and 2
+// into rows 1 and 3, row_bcast:31 folds row 1 into rows 2 and 3, so lane
+// 63 holds the maximum; one readlane.
 __device__ __forceinline__ int wave_max_i32(int v) {
   v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x111, 0xF, 0xF, false));
   v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x112, 0xF, 0xF, false));
   v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x114, 0xF, 0xF, false));
   v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x118, 0xF, 0xF, false));
-  const int a = __builtin_amdgcn_readlane(v, 15), b = __builtin_amdgcn_readlane(v, 31);
-  const int c = __builtin_amdgcn_readlane(v, 47), d = __builtin_amdgcn_readlane(v, 63);
-  return max(max(a, b), max(c, d));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x142, 0xA, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(INT_MIN, v, 0x143, 0xC, 0xF, false));
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
-// The set route() selects, found by repeated extraction of the largest
-// masked key (lowest expert id first among equal keys), K + 1 times.  The
-// reference's scan keeps the K largest keys; which of several EQUAL keys it
-// keeps depends on its slot order, so the extracted set is the reference's
-// set unless the K-th and (K+1)-th keys are equal (or fewer than K keys
-// exceed -1e30).  Slot s (s-th largest key) is certain as soon as a strictly
-// smaller key follows it, and is handed to publish(s, id) at that point:
-// the first slots go out after two extractions, long before the set is
-// complete.  In the ambiguous case the exact scan runs and the slots not
-// yet published receive the rest of the reference's (multi)set.
+// ---- the eight largest packed keys of the wave, by a merge network -------------------
+// Packed keys are unique, so "largest" is a strict order.  cx keeps the
+// larger of two in a, the smaller in b.
+__device__ __forceinline__ void cx(int& a, int& b) {
+  const int hi = max(a, b);
+  b = min(a, b);
+  a = hi;
+}
+
+// Sorts a bitonic sequence of eight, largest first.
+__device__ __forceinline__ void bitonic8(int (&t)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) cx(t[i], t[i + 4]);
+#pragma unroll
+  for (int i = 0; i < 8; i += 4) {
+    cx(t[i], t[i + 2]);
+    cx(t[i + 1], t[i + 3]);
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) cx(t[i], t[i + 1]);
+}
+
+// The partner's list by one DPP pattern (lanes it does not reach get
+// INT_MIN), merged into the lane's own: the eight largest of both lists
+// (each sorted, largest first) are max(t[i], p[7 - i]), a bitonic sequence.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void merge8(int (&t)[8]) {
+  int p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_update_dpp(INT_MIN, t[i], CTRL, ROWS, 0xF, false);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t[i] = max(t[i], p[7 - i]);
+  bitonic8(t);
+}
+
+// The eight largest of the wave's 256 keys (lane l holds k[0..3]), largest
+// first, in t[0..7] of lanes 48-63 (INT_MIN where fewer than eight keys
+// exist).  Each lane sorts its four; lanes l and l^1 merge their fours into
+// one sorted eight (quad_perm [1,0,3,2]); then lists merge with l^2
+// (quad_perm [2,3,0,1]), the other quad of the half row (row_half_mirror),
+// the other half row (row_mirror), row 0 into 1 and row 2 into 3
+// (row_bcast:15) and row 1 into 3 (row_bcast:31).  About 200 VALU
+// operations and no scalar round trip: every slot is known at once.
+__device__ __forceinline__ void top8_wave(const int (&k)[4], int (&t)[8]) {
+  int a[4] = {k[0], k[1], k[2], k[3]};
+  cx(a[0], a[1]);
+  cx(a[2], a[3]);
+  cx(a[0], a[2]);
+  cx(a[1], a[3]);
+  cx(a[1], a[2]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    t[i] = a[i];
+    // the partner's four, reversed: a bitonic sequence of eight
+    t[7 - i] = __builtin_amdgcn_update_dpp(INT_MIN, a[i], 0xB1, 0xF, 0xF, false);
+  }
+  bitonic8(t);
+  merge8<0x4E, 0xF>(t);   // quad_perm [2,3,0,1]
+  merge8<0x141, 0xF>(t);  // row_half_mirror
+  merge8<0x140, 0xF>(t);  // row_mirror
+  merge8<0x142, 0xA>(t);  // row_bcast:15 into rows 1 and 3
+  merge8<0x143, 0xC>(t);  // row_bcast:31 into rows 2 and 3
+}
+
+// The set route() selects.  Keys are PACKED: the order-preserving key's
+// upper 24 bits, then 255 - expert id, so the keys are unique and each
+// names its expert (the lowest id first among equal truncated keys).
+// Truncation is monotone, so the K largest packed keys are the reference's
+// set of the K largest full keys whenever the K-th and (K+1)-th TRUNCATED
+// keys differ: everything selected is then strictly above everything left,
+// and route()'s scan always keeps the keys strictly above its K-th.  Which
+// of several equal keys the scan keeps depends on its slot order, so when
+// those two truncated keys are equal (full keys tied, or within 256 units
+// of the last place), or fewer than K keys exceed -1e30, the exact scan
+// decides.  publish(slot, id) is called by every lane of the wave; a lane
+// with slot < 0 has nothing to publish.
+//  K <= 8: the eight largest by a merge network (top8_wave), every slot
+//    published at once by lanes 48 .. 48 + K - 1.
+//  K > 8: repeated extraction of the largest key, K + 1 times (one wave
+//    maximum each); slot s (the s-th extraction) is certain, and published,
+//    as soon as a strictly smaller truncated key follows it.
+// In the ambiguous case the slots not yet published receive the rest of
+// the reference's (multi)set from the exact scan.
 template <typename Publish>
 __device__ __forceinline__ void route_set_publish(const float score[4], const float bj[4], int K,
                                                   Publish&& publish) {
@@ -312,48 +388,77 @@ __device__ __forceinline__ void route_set_publish(const float score[4], const fl
   int vk[4];
   route_keys(score, bj, vk);
   const int floor = sort_key(-1e30f);
-  int key[4] = {vk[0], vk[1], vk[2], vk[3]};
-  int m = max(max(key[0], key[1]), max(key[2], key[3]));
-  int prev_key = INT_MAX;
-  int ext = 0;    // lane k: the k-th extracted expert
-  int n_pub = 0;  // slots 0 .. n_pub-1 published
-  bool ambiguous = false;
-  for (int k = 0; k <= K; ++k) {
-    const int wm = wave_max_i32(m);
-    if (wm <= floor) {
-      ambiguous = k < K;  // fewer than K candidates
-      break;
-    }
-    if (k == K) {
-      ambiguous = wm == prev_key;  // the K-th key is tied with the (K+1)-th
-      break;
-    }
-    // lowest expert id (64 j + lane) holding wm
-    int jj = 3, ll = 0;
+  int pk[4];
+  bool near_floor = false;  // a candidate whose truncated key is the floor's
 #pragma unroll
-    for (int j = 3; j >= 0; --j) {
-      const unsigned long long b = __ballot(key[j] == wm);
-      if (b) {
-        jj = j;
-        ll = __ffsll(b) - 1;
+  for (int j = 0; j < 4; ++j) {
+    const bool cand = vk[j] > floor;
+    near_floor = near_floor || (cand && (vk[j] >> 8) == (floor >> 8));
+    pk[j] = (cand && (vk[j] >> 8) != (floor >> 8)) ? ((vk[j] & ~255) | (255 - (64 * j + lane))) : INT_MIN;
+  }
+  bool ambiguous = __ballot(near_floor) != 0;
+  int ext = 0;    // extraction: lane k holds the k-th extracted expert
+  int n_pub = 0;  // slots 0 .. n_pub-1 published
+  if (K <= 8) {
+    if (!ambiguous) {
+      int t[8];
+      top8_wave(pk, t);
+      int tk = t[0], tn = t[0];  // the K-th and (K+1)-th largest (lanes 48-63)
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        tk = i == K - 1 ? t[i] : tk;
+        tn = i == K ? t[i] : tn;
+      }
+      const int kth = __builtin_amdgcn_readlane(tk, 63);
+      int next;
+      if (K < 8) {
+        next = __builtin_amdgcn_readlane(tn, 63);
+      } else {
+        // the ninth: the largest key below the eighth
+        int m = INT_MIN;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = max(m, pk[j] < kth ? pk[j] : INT_MIN);
+        next = wave_max_i32(m);
+      }
+      ambiguous = kth == INT_MIN || (next != INT_MIN && (next >> 8) == (kth >> 8));
+      if (!ambiguous) {
+        const int s = lane - 48;
+        int v = t[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) v = s == i ? t[i] : v;
+        publish((s >= 0 && s < K) ? s : -1, 255 - (v & 255));
+        return;
       }
     }
-    if (k > 0 && prev_key > wm) {
-      // every slot so far holds a key >= prev_key > wm: all certain
-      for (int s = n_pub; s < k; ++s) publish(s, __builtin_amdgcn_readlane(ext, s));
-      n_pub = k;
-    }
-    prev_key = wm;
-    if (lane == k) ext = 64 * jj + ll;
-    if (lane == ll) {
+  } else {
+    int m = max(max(pk[0], pk[1]), max(pk[2], pk[3]));
+    int prev_t = INT_MAX;
+    for (int k = 0; k <= K && !ambiguous; ++k) {
+      const int wm = wave_max_i32(m);
+      if (wm == INT_MIN) {
+        ambiguous = k < K;  // fewer than K candidates
+        break;
+      }
+      const int wt = wm >> 8;
+      if (k == K) {
+        ambiguous = wt == prev_t;  // the K-th truncated key is tied with the (K+1)-th
+        break;
+      }
+      if (k > 0 && prev_t > wt) {
+        // every slot so far holds a truncated key >= prev_t > wt: all certain
+        for (int s = n_pub; s < k; ++s) publish(lane == 0 ? s : -1, __builtin_amdgcn_readlane(ext, s));
+        n_pub = k;
+      }
+      prev_t = wt;
+      if (lane == k) ext = 255 - (wm & 255);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) key[j] = j == jj ? INT_MIN : key[j];
-      m = max(max(key[0], key[1]), max(key[2], key[3]));
+      for (int j = 0; j < 4; ++j) pk[j] = pk[j] == wm ? INT_MIN : pk[j];
+      m = max(max(pk[0], pk[1]), max(pk[2], pk[3]));
     }
-  }
-  if (!ambiguous) {
-    for (int s = n_pub; s < K; ++s) publish(s, __builtin_amdgcn_readlane(ext, s));
-    return;
+    if (!ambiguous) {
+      for (int s = n_pub; s < K; ++s) publish(lane == 0 ? s : -1, __builtin_amdgcn_readlane(ext, s));
+      return;
+    }
   }
   // Ambiguous: the exact scan gives the reference's slots (lane k: slot k's
   // id; slots never filled hold expert 0, possibly several times).  The
@@ -372,7 +477,7 @@ __device__ __forceinline__ void route_set_publish(const float score[4], const fl
   unsigned long long rest = __ballot(!matched);
   for (int s = n_pub; s < K && rest; ++s) {
     const int l = __ffsll(rest) - 1;
-    publish(s, __builtin_amdgcn_readlane(eid, l));
+    publish(lane == 0 ? s : -1, __builtin_amdgcn_readlane(eid, l));
     rest &= rest - 1;
   }
 }

@@ -84,16 +84,20 @@ def lay_h(oracle, tok):
     return oracle.synth_normal(7168, 0.0, 1.0, 500 + tok)
 
 
-@pytest.mark.parametrize("K", [5, 7])
-def test_moe_layer_tied_set(fdm, oracle, layer, K):
+@pytest.mark.parametrize("K,nudge", [(5, 0.0), (7, 0.0), (5, 2.0 ** -22), (7, 2.0 ** -22), (8, 2.0 ** -22)])
+def test_moe_layer_tied_set(fdm, oracle, layer, K, nudge):
     """Every router row and bias duplicated in adjacent experts (same group):
     each choice occurs twice, so with K odd the K-th largest is tied with an
-    expert left out and the set itself depends on route()'s scan order."""
+    expert left out and the set itself depends on route()'s scan order.
+    With a nudge the odd expert's bias is larger by 2^-22: the choices of a
+    pair differ in their last few bits only, so the K-th and (K+1)-th keys
+    agree in their upper 24 bits (the set kernel's packed keys tie) while
+    the reference's order is strict."""
     L, lay = layer
     Wg = lay.Wg.clone()
     Wg[1::2] = Wg[0::2]
     bias = lay.bias.clone()
-    bias[1::2] = bias[0::2]
+    bias[1::2] = bias[0::2] + nudge
     L2 = L + 20
     fdm.attach_layer(L2, lay.experts, lay.expert_size, Wg, bias, lay.shared)
     try:
