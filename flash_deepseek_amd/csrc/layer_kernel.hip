@@ -137,12 +137,14 @@ struct LayerSmem {
       float esh[32];                                 // the shared expert's output of each row
     } fin;                                           // final items
     RmsSmem rms;              // the fused rms_norm (router rows and digit items)
+    float ssc[256];           // the route item: scores handed from a polling wave to wave 0
   };
   float red[4];
   float inv;                  // the fused rms_norm's 1 / rms
   float cw[kLayerMaxSlots];   // combine: route() weights in slot order
   int cperm[kLayerMaxSlots];  // combine: the expert-set slot of each
   int eid;                  // expert of the item's slot
+  int sflag;                // the route item: 0 waiting, 1 scores in ssc, 2 gave up
 };
 
 // Whole-workgroup wait: every thread runs try_once() (its share of the
@@ -329,10 +331,61 @@ __device__ __forceinline__ void wait_scores(const LayerArgs& a, float sc[4]) {
   });
 }
 
+// The 256 tagged scores into wave 0's registers (lane l: expert 64 j + l in
+// sc[j]), polled by waves 1-3, staggered by ~0.5 us each: the first to see
+// every tag of this call writes the scores to LDS and raises an LDS flag
+// that wave 0 spins on.  A value is then seen within ~1/3 of a round trip
+// plus one round trip of landing (one poller: 1/2 to 1), and no poll load is
+// left outstanding in wave 0's registers when it starts the set.  Every
+// thread calls it (one barrier).
+__device__ __forceinline__ void wait_scores_staggered(const LayerArgs& a, float sc[4], LayerSmem& sm) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  volatile int* flag = &sm.sflag;
+  if (threadIdx.x == 0) *flag = 0;
+  __syncthreads();
+  if (wave == 0) {
+    while (*flag == 0) __builtin_amdgcn_s_sleep(1);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sc[j] = sm.ssc[64 * j + lane];
+    return;
+  }
+  if (wave == 2) __builtin_amdgcn_s_sleep(19);
+  if (wave == 3) __builtin_amdgcn_s_sleep(38);
+  unsigned* err = a.flags + kStride * kFlagErr;
+  for (unsigned n = 0;; ++n) {
+    float v[4];
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint64_t t = get_tagged(a.scores + 64 * j + lane);
+      ok = ok && tag_is(t, a.epoch);
+      v[j] = tagged_f(t);
+    }
+    const bool all = __ballot(!ok) == 0;
+    if (*flag != 0) return;  // another poller was first
+    if (all) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sm.ssc[64 * j + lane] = v[j];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (lane == 0) *flag = 1;
+      return;
+    }
+    if (n >= a.spin_limit || ((n & 63) == 63 && load_u32_agent(err) == a.epoch)) {
+      if (lane == 0) {
+        store_u32_agent(err, a.epoch);
+        *flag = 2;
+      }
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
 // ---- route: the expert set ------------------------------------------------------------
 // On the critical path of every routed weight load: the bias is fetched
 // before the wait, and the wave issues ahead of the SIMD's expert waves.
-__device__ __forceinline__ void route_item(const LayerArgs& a) {
+__device__ __forceinline__ void route_item(const LayerArgs& a, LayerSmem& sm) {
   const int lane = threadIdx.x & 63;
   __builtin_amdgcn_s_setprio(3);
   float bj[4];
@@ -354,7 +407,7 @@ __device__ __forceinline__ void route_item(const LayerArgs& a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) sc[j] = (float)(64 * j + lane) * (1.0f / 256.0f);
     } else {
-      wait_scores(a, sc);
+      wait_scores_staggered(a, sc, sm);
     }
     if (threadIdx.x < 64)
       route_set_publish(sc, bj, a.K, [&](int slot, int id) {
@@ -993,7 +1046,7 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
   } else if (!EXPERT && it < l.route) {
     router_row(a, it - l.router, sm);
   } else if (!EXPERT && it == l.route) {
-    route_item(a);
+    route_item(a, sm);
   } else if (!EXPERT && it == l.exact) {
     exact_item(a);
   } else if (it < l.shadg) {
