@@ -17,10 +17,17 @@
 //     less than 2^-18 more.
 //  2. Step i is a "run" step when P_i and P_i + x_i^2 both lie inside one
 //     binade with a relative margin of 2^-10 to its ends (so the true ss_i
-//     and ss_(i+1) lie in it too), P_i >= 2^-100 (normal grid) and the
-//     exact x_i^2 / u (in double) is not a tie; it then adds
-//     K_i = rint(x_i^2 / u) < 2^23.  Every other step is "risky" (the first
-//     step always is: P_0 = 0).
+//     and ss_(i+1) lie in it too), P_i >= 2^-100 (normal grid) and
+//     x_i^2 / u is safely away from a tie; it then adds
+//     K_i = rint(x_i^2 / u) < 2^24.  Every other step is "risky" (the first
+//     step always is: P_0 = 0).  x_i^2 / u is formed exactly in floats:
+//     x^2 = h + l with h = x*x, l = fma(x, x, -h) (exact for |x| >= 2^-40,
+//     smaller x are risky), both scaled by 2^(24-E); K = rint(h'), and the
+//     step is risky unless |(h' - K) + l'| < 1/2 - 2^-23 -- (h' - K) is
+//     exact and the rounded sum is within 2^-26 of the true fraction, so a
+//     step that passes has |fraction| < 1/2 and K is the exact rint.  A risky step keeps the
+//     binade exponent E of P_i in its LDS slot (bit 31 set), so the list of
+//     risky steps needs no second pass over the prefix.
 //  3. Consecutive run steps share one binade, so a run adds exactly
 //     u * (sum of its K) -- one float addition, exact because the result
 //     stays on the grid inside the binade.  The K are summed mod 2^32 (a
@@ -42,7 +49,7 @@ constexpr int kRmsMaxPer = kHidden / kRmsThreads;  // elements per thread at d =
 constexpr int kRmsMaxRisky = 512;
 
 struct alignas(16) RmsSmem {
-  unsigned k[kHidden];        // per element: K_i of a run step, kRmsRisky for a risky step (16-byte aligned)
+  unsigned k[kHidden];        // per element: K_i of a run step, kRmsRisky | (E + 256) for a risky step (16-byte aligned)
   float rx[kRmsMaxRisky];     // risky steps in order: x_r,
   unsigned rq[kRmsMaxRisky];  //   sum of K before r (mod 2^32),
   int re[kRmsMaxRisky];       //   exponent E of P_r (the run before r lies in [2^(E-1), 2^E))
@@ -52,7 +59,7 @@ struct alignas(16) RmsSmem {
   int wr[4];
   float ss;
 };
-constexpr unsigned kRmsRisky = 0xFFFFFFFFu;
+constexpr unsigned kRmsRisky = 0x80000000u;  // flag of a risky step's slot; bits 0-15: its E + 256
 
 // DPP move of a 32-bit value (lanes without a source receive 0).
 template <int CTRL, int ROW_MASK, typename T>
@@ -158,8 +165,9 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
     if (mine(j)) tot = tot + xv[j] * xv[j];
   float total_f;
   const float base = rms_block_excl(tot, sm.wf, total_f);
-  // 2. classify each step; K of the run steps into LDS (the thread's slots
-  //    as 16-byte stores where they are whole vectors)
+  // 2. classify each step; K of the run steps (or the flagged E of a risky
+  //    step) into LDS (the thread's slots as 16-byte stores where they are
+  //    whole vectors)
   const float lo_margin = 0.5f * (1.0f + 0x1p-10f);  // frexp mantissa of P_i at least this
   const float hi_margin = 1.0f - 0x1p-10f;           // (P_i + x^2) / 2^E at most this
   float p = base;
@@ -170,14 +178,22 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
   for (int j = 0; j < kRmsMaxPer; ++j) {
     kk[j & 3] = 0u;
     if (mine(j)) {
-      const float after = p + xv[j] * xv[j];
+      const float x = xv[j];
+      const float after = p + x * x;
       int E;
       const float m = frexpf(p, &E);  // p = m 2^E, m in [0.5, 1)
-      const double q = ldexp((double)xv[j] * (double)xv[j], 24 - E);  // exact x^2 / u, u = 2^(E - 24)
-      const double K = rint(q);
-      const bool risky = !(p >= 0x1p-100f) || !(after < 0x1p126f) || !(m >= lo_margin) ||
-                         !(ldexpf(after, -E) <= hi_margin) || fabs(q - K) == 0.5;
-      const unsigned k = risky ? kRmsRisky : (unsigned)K;
+      // x^2 / u = h' + l' exactly (u = 2^(E - 24))
+      const float h = x * x;
+      const float l = fmaf(x, x, -h);
+      const float hq = ldexpf(h, 24 - E), lq = ldexpf(l, 24 - E);
+      const float K = rintf(hq);
+      const float frac = (hq - K) + lq;
+      // every test evaluated (no short circuit): one mask per element, no
+      // branches in the unrolled loop
+      const bool risky = !(p >= 0x1p-100f) | !(after < 0x1p126f) | !(m >= lo_margin) |
+                         !(ldexpf(after, -E) <= hi_margin) | !(fabsf(x) >= 0x1p-40f) |
+                         !(fabsf(frac) < 0x1.fffffcp-2f);
+      const unsigned k = risky ? (kRmsRisky | (unsigned)(E + 256)) : (unsigned)K;
       kk[j & 3] = k;
       if (!FULL) sm.k[i0 + j] = k;
       ksum += risky ? 0u : k;
@@ -208,7 +224,6 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
     return sm.ss;
   }
   // 3. the risky steps in order: x, the K sum before them, the binade of P
-  p = base;
   unsigned kq = kbase;
   int r = rbase;
   unsigned kv[kRmsMaxPer];  // every K read before the walk over them: one LDS round trip
@@ -225,21 +240,20 @@ __device__ __forceinline__ float rms_sumsq_impl(const float (&xv)[kRmsMaxPer], i
       for (int i = 0; i < 4; ++i) kv[j + i] = mine(j + i) ? sm.k[i0 + j + i] : 0u;
     }
   }
+  if (nrisky > 0) {
 #pragma unroll
-  for (int j = 0; j < kRmsMaxPer; ++j) {
-    if (nrisky > 0 && mine(j)) {
-      const unsigned k = kv[j];
-      if (k == kRmsRisky) {
-        int E;
-        (void)frexpf(p, &E);
-        sm.rx[r] = xv[j];
-        sm.rq[r] = kq;
-        sm.re[r] = E;
-        ++r;
-      } else {
-        kq += k;
+    for (int j = 0; j < kRmsMaxPer; ++j) {
+      if (mine(j)) {
+        const unsigned k = kv[j];
+        const bool isr = (k & kRmsRisky) != 0u;
+        if (isr) {
+          sm.rx[r] = xv[j];
+          sm.rq[r] = kq;
+          sm.re[r] = (int)(k & 0xFFFFu) - 256;
+        }
+        kq += isr ? 0u : k;
+        r += isr ? 1 : 0;
       }
-      p = p + xv[j] * xv[j];
     }
   }
   __syncthreads();
