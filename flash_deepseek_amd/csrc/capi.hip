@@ -947,6 +947,11 @@ int run_matvec(bool q6, const void* d_W, const float* d_x, float* d_y, uint32_t 
   const uint8_t* W = static_cast<const uint8_t*>(d_W);
   // the layer kernel's tagged expert-output words hold the partial sums
   const size_t part_words = (size_t)kLayerMaxSlots * kLayerMaxParts * FDM_HIDDEN;
+  if (!q6 && matvec3_supported((int)in_dim)) {
+    ProfScope p(FDM_PROF_MATVEC, s);
+    FDM_HIP(launch_matvec3_q4k(W, d_x, d_y, (int)out_dim, (int)in_dim, s));
+    return FDM_OK;
+  }
   if (!q6 && matvec2_supported((int)in_dim, (int)out_dim, part_words)) {
     Matvec2Args a;
     a.W = W;

@@ -63,6 +63,8 @@ struct Matvec2Args {
 bool matvec2_supported(int in_dim, int rows, size_t part_words);
 hipError_t launch_matvec2_q4k(const Matvec2Args& a, int in_dim, hipStream_t s);
 bool matvec1_supported(bool q6, int in_dim);
+bool matvec3_supported(int in_dim);
+hipError_t launch_matvec3_q4k(const uint8_t* W, const float* x, float* y, int rows, int in_dim, hipStream_t s);
 hipError_t launch_matvec1(const MatvecArgs& a, bool q6, hipStream_t s);
 
 // router_kernels.hip

@@ -345,6 +345,131 @@ __global__ __launch_bounds__(256) void k_matvec2_q4k(Matvec2Args a) {
   a.y[r] = P == 1 ? own[threadIdx.x] : sum + own[threadIdx.x];
 }
 
+// ---- one launch in fp32 (Q4_K, in_dim = 1024, 2048 or 7168) -----------------------------
+// (Measured on MI355X, 2048 x 7168: 5.3 us against 6.7 us for the
+// column-part digit kernel below; a row over two waves, 6.1 us.)
+// No activation digits and no hand-off between workgroups: at batch 1 a
+// single matvec is latency-bound (8 MB streams in ~1.4 us), and the digit
+// records (each workgroup making the digits of its columns, then a second
+// round trip to add the column parts) cost more than the math they save.
+// Here every workgroup stages the whole x in LDS once (with each 32-element
+// sub-block's fp32 sum for the Q4_K min term; 16 bytes of padding per
+// 64-element group, so the lanes of a wave, one group each, read distinct
+// banks), and each row is contracted by
+// LPR lanes in fp32: lane i of a row takes the row's 64-element groups
+// i, i + LPR, ..; a group's 32 qs bytes are two sub-blocks (low nibbles:
+// elements 0-31, high: 32-63), each dotted with x as sum_k q_k x_k in fp32
+// (the nibbles widened two at a time by the fp8 conversion), then
+//   d (sc0 S0 + sc1 S1) - dmin (m0 X0 + m1 X1)
+// as dequant_matvec_q4k (shaders.metal:43-99) in fp32; the row's lane
+// partials are added by DPP into its first lane.  All loads of a workgroup
+// (its rows' weights and x) are issued before any math.
+template <int LPR, int GPL, int NG>
+__global__ __launch_bounds__(256) void k_matvec3_q4k(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                     float* __restrict__ y, int rows) {
+  constexpr int ng = NG;
+  extern __shared__ float xsh[];  // x, 68 floats per 64-element group (bank padding), then the sub-block sums [2 ng]
+  float* xss = xsh + 68 * ng;
+  static_assert(LPR == 16 || LPR == 32 || LPR == 64, "lanes per row");
+  constexpr int RPW = 64 / LPR;  // rows per wave
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int li = lane % LPR;
+  const int row = blockIdx.x * (4 * RPW) + wave * RPW + lane / LPR;
+  const int rr = min(row, rows - 1);
+  const int g = li & 3;
+  // x first (its LDS copy waits for these loads only), then the weights of
+  // the lane's groups (clamped: groups past the row load a valid group and
+  // contribute 0); each group's math waits for its own loads
+  constexpr int kNv = 16 * NG / 256;  // float4s of x per thread
+  static_assert(kNv * 256 == 16 * NG, "x in whole 256-thread steps");
+  f32x4 xv[kNv];
+#pragma unroll
+  for (int i = 0; i < kNv; ++i) xv[i] = reinterpret_cast<const f32x4*>(x)[threadIdx.x + 256 * i];
+  Q4KGroupLoad ld[GPL];
+#pragma unroll
+  for (int k = 0; k < GPL; ++k) {
+    const int G = min(li + k * LPR, ng - 1);
+    ld[k] = q4k_load_group(W + ((size_t)rr * (ng >> 2) + (G >> 2)) * kQ4KBlock, g);
+  }
+  // x into LDS; each sub-block's sum by the eight threads that hold it
+#pragma unroll
+  for (int i = 0; i < kNv; ++i) {
+    const int v = threadIdx.x + 256 * i;
+    *reinterpret_cast<f32x4*>(xsh + 68 * (v >> 4) + 4 * (v & 15)) = xv[i];
+    float sb = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+    sb = sb + dpp_row_shl<1>(sb);
+    sb = sb + dpp_row_shl<2>(sb);
+    sb = sb + dpp_row_shl<4>(sb);
+    if ((v & 7) == 0) xss[v >> 3] = sb;
+  }
+  __syncthreads();
+  // nibble q as an fp8 (e4m3) byte is q * 2^-c exactly (q < 16: exponent
+  // field 0 or 1), c the format's; the products are summed on that scale and
+  // the scale is folded into d
+  const float qscale = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < GPL; ++k) {
+    const int G = li + k * LPR;
+    const u32x4 hdr = q4k_quad_hdr(ld[k]);
+    const float* x0 = xsh + 68 * min(G, ng - 1);
+    const uint32_t w[8] = {ld[k].q0.x, ld[k].q0.y, ld[k].q0.z, ld[k].q0.w,
+                           ld[k].q1.x, ld[k].q1.y, ld[k].q1.z, ld[k].q1.w};
+    float S0 = 0.0f, S1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(x0 + 4 * i);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(x0 + 32 + 4 * i);
+      const int lo = (int)(w[i] & 0x0F0F0F0Fu), hi = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
+      const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+      const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+      S0 = fmaf(l01[0], a.x, S0);
+      S0 = fmaf(l01[1], a.y, S0);
+      S0 = fmaf(l23[0], a.z, S0);
+      S0 = fmaf(l23[1], a.w, S0);
+      S1 = fmaf(h01[0], b.x, S1);
+      S1 = fmaf(h01[1], b.y, S1);
+      S1 = fmaf(h23[0], b.z, S1);
+      S1 = fmaf(h23[1], b.w, S1);
+    }
+    int sc0, m0, sc1, m1;
+    q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, q4k_scale_sel(g), sc0, m0, sc1, m1);
+    const float d = half_to_float(hdr.x) * qscale, dmin = half_to_float(hdr.x >> 16);
+    const int sb = 2 * min(G, ng - 1);
+    const float qx = fmaf((float)sc0, S0, (float)sc1 * S1);
+    const float mx = fmaf((float)m0, xss[sb], (float)m1 * xss[sb + 1]);
+    const float part = fmaf(d, qx, -dmin * mx);
+    acc += G < ng ? part : 0.0f;
+  }
+  // the row's LPR lanes into its first lane
+  if constexpr (LPR == 64) {
+    acc = wave_sum_lane0(acc);
+  } else {
+    // LPR = 32: rows 1 and 3 of 16 lanes into rows 0 and 2 (permlane16_swap)
+    if constexpr (LPR == 32)
+      acc = acc + __uint_as_float(__builtin_amdgcn_permlane16_swap(__float_as_uint(acc), __float_as_uint(acc), false, false)[1]);
+    acc = sum16(acc);
+  }
+  if (li == 0 && row < rows) y[row] = acc;
+}
+
+bool matvec3_supported(int in_dim) { return in_dim == 1024 || in_dim == 2048 || in_dim == 7168; }
+
+hipError_t launch_matvec3_q4k(const uint8_t* W, const float* x, float* y, int rows, int in_dim, hipStream_t s) {
+  const int ng = in_dim / 64;
+  const size_t lds = (size_t)ng * 68 * 4 + (size_t)ng * 2 * 4;
+  if (in_dim == 7168) {
+    hipLaunchKernelGGL((k_matvec3_q4k<64, 2, 112>), dim3((rows + 3) / 4), dim3(256), lds, s, W, x, y, rows);
+  } else if (in_dim == 2048) {
+    hipLaunchKernelGGL((k_matvec3_q4k<32, 1, 32>), dim3((rows + 7) / 8), dim3(256), lds, s, W, x, y, rows);
+  } else if (in_dim == 1024) {
+    hipLaunchKernelGGL((k_matvec3_q4k<16, 1, 16>), dim3((rows + 15) / 16), dim3(256), lds, s, W, x, y, rows);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 bool matvec2_supported(int in_dim, int rows, size_t part_words) {
   const int P = in_dim / 1024;
   return in_dim % 1024 == 0 && P >= 1 && P <= 7 && (size_t)(P - 1) * (size_t)rows <= part_words;
