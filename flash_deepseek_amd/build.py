@@ -24,6 +24,7 @@ SOURCES = [
     "router_kernels.hip",
     "moe_kernels.hip",
     "layer_kernel.hip",
+    "expert_kernels.hip",
     "read_ceiling.hip",
     "batched_kernels.hip",
     "prefill_kernels.hip",

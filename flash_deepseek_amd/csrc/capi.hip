@@ -1024,9 +1024,10 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
     return fail(FDM_E_INVAL, "blob must be 4-byte and x 16-byte aligned");
   if (d_act && !aligned(d_act, 4)) return fail(FDM_E_INVAL, "act must be 4-byte aligned");
   hipStream_t s = as_stream(stream);
-  // one launch of the layer kernel's work list without router or route:
-  // the expert runs as the shared slot of a zero-routed-expert layer, read
-  // from the caller's packed blob
+  // one launch on the caller's packed blob: with a Q4_K down matrix the
+  // fp32 expert kernel (expert_kernels.hip); with Q6_K the layer kernel's
+  // work list without router or route (the expert as the shared slot of a
+  // zero-routed-expert layer)
   Workspace* ws = nullptr;
   if (int rc = stream_workspace(s, &ws)) return rc;
   LayerArgs a;
@@ -1050,7 +1051,8 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   a.act_out = d_act;
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    FDM_HIP(launch_layer(a, s));
+    // Q4_K down: the fp32 expert kernel; Q6_K down: the layer kernel's list
+    FDM_HIP(q6 ? launch_layer(a, s) : launch_expert_f32(a, s));
   }
   return FDM_OK;
 }

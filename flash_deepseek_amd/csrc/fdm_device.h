@@ -342,6 +342,46 @@ __device__ __forceinline__ float q4k_group_dot_ld(const Q4KGroupLoad& r, const Q
   return q4k_group_dot(q4k_quad_hdr(r), r.q0, r.q1, sel, x);
 }
 
+// ---- fp32 dot of one Q4_K group with x held in LDS -------------------------------------
+// x in LDS as 68 floats per 64-element group (16 bytes of padding, so the
+// lanes of a wave, one group each, read distinct banks), the fp32 sum of
+// each 32-element sub-block beside it.  Returns
+//   d (sc0 S0 + sc1 S1) - dmin (m0 X0 + m1 X1),  S = sum_k q_k x_k in fp32,
+// dequant_matvec_q4k's arithmetic (shaders.metal:43-99) in fp32.  A nibble
+// q read as an fp8 (e4m3) byte is q * 2^-c exactly (q < 16: exponent field 0
+// or 1), so the fp8 conversion widens two nibbles per instruction; the
+// products are summed on that scale and qscale = 2^c is folded into d.
+constexpr int kXPad = 68;
+__device__ __forceinline__ float q4k_fp8_qscale() { return 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0]; }
+__device__ __forceinline__ float q4k_group_dot_f32(const Q4KGroupLoad& ld, const u32x4 hdr, int g,
+                                                   const float* __restrict__ x0, float xsum0, float xsum1,
+                                                   float qscale) {
+  const uint32_t w[8] = {ld.q0.x, ld.q0.y, ld.q0.z, ld.q0.w, ld.q1.x, ld.q1.y, ld.q1.z, ld.q1.w};
+  float S0 = 0.0f, S1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(x0 + 4 * i);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(x0 + 32 + 4 * i);
+    const int lo = (int)(w[i] & 0x0F0F0F0Fu), hi = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
+    const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+    const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
+    S0 = fmaf(l01[0], a.x, S0);
+    S0 = fmaf(l01[1], a.y, S0);
+    S0 = fmaf(l23[0], a.z, S0);
+    S0 = fmaf(l23[1], a.w, S0);
+    S1 = fmaf(h01[0], b.x, S1);
+    S1 = fmaf(h01[1], b.y, S1);
+    S1 = fmaf(h23[0], b.z, S1);
+    S1 = fmaf(h23[1], b.w, S1);
+  }
+  int sc0, m0, sc1, m1;
+  q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, q4k_scale_sel(g), sc0, m0, sc1, m1);
+  const float d = half_to_float(hdr.x) * qscale, dmin = half_to_float(hdr.x >> 16);
+  const float qx = fmaf((float)sc0, S0, (float)sc1 * S1);
+  const float mx = fmaf((float)m0, xsum0, (float)m1 * xsum1);
+  return fmaf(d, qx, -dmin * mx);
+}
+
 // R rows' groups (the same group position g in every row) against ONE
 // digit record in LDS: each quarter of the record (12 registers of digits)
 // is read once and applied to all R rows, so a lane's LDS traffic is one

@@ -158,6 +158,9 @@ struct LayerArgs {
 };
 constexpr unsigned kLayerSpinLimit = 1u << 17;  // polls of one wait (each >= ~1 us)
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);
+// expert_kernels.hip: one expert with a Q4_K down matrix in one fp32 launch
+// (a.shared: the caller's packed blob; a.act, a.epoch, a.flags, a.spin_limit).
+hipError_t launch_expert_f32(const LayerArgs& a, hipStream_t s);
 
 // read_ceiling.hip: the batch-1 layer's bytes read with the layer kernel's
 // load policy and nothing else (the streaming ceiling of those bytes).

@@ -369,7 +369,7 @@ __global__ __launch_bounds__(256) void k_matvec3_q4k(const uint8_t* __restrict__
                                                      float* __restrict__ y, int rows) {
   constexpr int ng = NG;
   extern __shared__ float xsh[];  // x, 68 floats per 64-element group (bank padding), then the sub-block sums [2 ng]
-  float* xss = xsh + 68 * ng;
+  float* xss = xsh + kXPad * ng;
   static_assert(LPR == 16 || LPR == 32 || LPR == 64, "lanes per row");
   constexpr int RPW = 64 / LPR;  // rows per wave
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) void k_matvec3_q4k(const uint8_t* __restrict__
 #pragma unroll
   for (int i = 0; i < kNv; ++i) {
     const int v = threadIdx.x + 256 * i;
-    *reinterpret_cast<f32x4*>(xsh + 68 * (v >> 4) + 4 * (v & 15)) = xv[i];
+    *reinterpret_cast<f32x4*>(xsh + kXPad * (v >> 4) + 4 * (v & 15)) = xv[i];
     float sb = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
     sb = sb + dpp_row_shl<1>(sb);
     sb = sb + dpp_row_shl<2>(sb);
@@ -403,42 +403,13 @@ __global__ __launch_bounds__(256) void k_matvec3_q4k(const uint8_t* __restrict__
     if ((v & 7) == 0) xss[v >> 3] = sb;
   }
   __syncthreads();
-  // nibble q as an fp8 (e4m3) byte is q * 2^-c exactly (q < 16: exponent
-  // field 0 or 1), c the format's; the products are summed on that scale and
-  // the scale is folded into d
-  const float qscale = 1.0f / __builtin_amdgcn_cvt_pk_f32_fp8(1, false)[0];
+  const float qscale = q4k_fp8_qscale();
   float acc = 0.0f;
 #pragma unroll
   for (int k = 0; k < GPL; ++k) {
-    const int G = li + k * LPR;
-    const u32x4 hdr = q4k_quad_hdr(ld[k]);
-    const float* x0 = xsh + 68 * min(G, ng - 1);
-    const uint32_t w[8] = {ld[k].q0.x, ld[k].q0.y, ld[k].q0.z, ld[k].q0.w,
-                           ld[k].q1.x, ld[k].q1.y, ld[k].q1.z, ld[k].q1.w};
-    float S0 = 0.0f, S1 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(x0 + 4 * i);
-      const f32x4 b = *reinterpret_cast<const f32x4*>(x0 + 32 + 4 * i);
-      const int lo = (int)(w[i] & 0x0F0F0F0Fu), hi = (int)((w[i] >> 4) & 0x0F0F0F0Fu);
-      const auto l01 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), l23 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
-      const auto h01 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), h23 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
-      S0 = fmaf(l01[0], a.x, S0);
-      S0 = fmaf(l01[1], a.y, S0);
-      S0 = fmaf(l23[0], a.z, S0);
-      S0 = fmaf(l23[1], a.w, S0);
-      S1 = fmaf(h01[0], b.x, S1);
-      S1 = fmaf(h01[1], b.y, S1);
-      S1 = fmaf(h23[0], b.z, S1);
-      S1 = fmaf(h23[1], b.w, S1);
-    }
-    int sc0, m0, sc1, m1;
-    q4k_scale_min_pair(hdr.y, hdr.z, hdr.w, q4k_scale_sel(g), sc0, m0, sc1, m1);
-    const float d = half_to_float(hdr.x) * qscale, dmin = half_to_float(hdr.x >> 16);
-    const int sb = 2 * min(G, ng - 1);
-    const float qx = fmaf((float)sc0, S0, (float)sc1 * S1);
-    const float mx = fmaf((float)m0, xss[sb], (float)m1 * xss[sb + 1]);
-    const float part = fmaf(d, qx, -dmin * mx);
+    const int G = li + k * LPR, Gc = min(G, ng - 1);
+    const float part = q4k_group_dot_f32(ld[k], q4k_quad_hdr(ld[k]), g, xsh + kXPad * Gc, xss[2 * Gc],
+                                         xss[2 * Gc + 1], qscale);
     acc += G < ng ? part : 0.0f;
   }
   // the row's LPR lanes into its first lane
@@ -457,7 +428,7 @@ bool matvec3_supported(int in_dim) { return in_dim == 1024 || in_dim == 2048 || 
 
 hipError_t launch_matvec3_q4k(const uint8_t* W, const float* x, float* y, int rows, int in_dim, hipStream_t s) {
   const int ng = in_dim / 64;
-  const size_t lds = (size_t)ng * 68 * 4 + (size_t)ng * 2 * 4;
+  const size_t lds = (size_t)ng * kXPad * 4 + (size_t)ng * 2 * 4;
   if (in_dim == 7168) {
     hipLaunchKernelGGL((k_matvec3_q4k<64, 2, 112>), dim3((rows + 3) / 4), dim3(256), lds, s, W, x, y, rows);
   } else if (in_dim == 2048) {
