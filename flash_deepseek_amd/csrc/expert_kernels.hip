@@ -31,7 +31,6 @@ constexpr int kExGuItems = kFfn / kExGuRows;    // 512
 constexpr int kExFinRows = 32;                  // down rows per final item
 constexpr int kExFinItems = kHidden / kExFinRows;  // 224
 constexpr int kExXGroups = kHidden / 64;        // 112
-constexpr int kExAGroups = kFfn / 64;           // 32
 
 struct ExpertSmem {
   float x[kExXGroups * kXPad];  // x (gate/up items) or the activations (final items), padded
