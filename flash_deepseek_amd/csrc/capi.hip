@@ -108,12 +108,12 @@ int bind_scratch(int device) {
 
 // Per-token scratch of the attention (grown to the largest max_seq).
 struct AttnScratch {
-  float *normed = nullptr, *q_a = nullptr, *q_a_n = nullptr, *q = nullptr, *kv_a = nullptr, *c_kv_n = nullptr;
+  float *normed = nullptr, *q_a = nullptr, *q = nullptr, *kv_a = nullptr;
   float *q_abs = nullptr, *wc = nullptr, *attn = nullptr, *part = nullptr, *stat = nullptr;
   int seq = 0;
   void release() {
     // kv_a lives in q_a's allocation (the two projections run as one matvec)
-    for (float* p : {normed, q_a, q_a_n, q, c_kv_n, q_abs, wc, attn, part, stat})
+    for (float* p : {normed, q_a, q, q_abs, wc, attn, part, stat})
       if (p) (void)hipFree(p);
     *this = AttnScratch();
   }
@@ -1963,10 +1963,11 @@ static int ensure_attn(Workspace& w, int seq, hipStream_t s) {
   FDM_HIP(hipStreamSynchronize(s));
   ws.release();
   const size_t H = FDM_HIDDEN, QA = 1536, QB = 128 * 192, KVA = 576, O = 128 * 128;
-  const size_t n[] = {H, QA + KVA, QA, QB, 512, 128 * 512, 128 * 512, O, (size_t)((seq + 63) / 64) * 128 * 512,
-                      (size_t)((seq + 63) / 64) * 128 * 2};
-  float** p[] = {&ws.normed, &ws.q_a, &ws.q_a_n, &ws.q, &ws.c_kv_n, &ws.q_abs, &ws.wc, &ws.attn, &ws.part, &ws.stat};
-  for (int i = 0; i < 10; ++i)
+  const size_t chunks = (size_t)((seq + kMlaChunkPos - 1) / kMlaChunkPos);
+  // normed[0]: the attention norm's 1 / rms (the rest of H is spare)
+  const size_t n[] = {H, QA + KVA, QB, 128 * 512, 128 * 512, O, chunks * 128 * 512, chunks * 128 * 2};
+  float** p[] = {&ws.normed, &ws.q_a, &ws.q, &ws.q_abs, &ws.wc, &ws.attn, &ws.part, &ws.stat};
+  for (int i = 0; i < 8; ++i)
     if (hipMalloc(p[i], n[i] * 4) != hipSuccess) {
       ws.release();
       return fail(FDM_E_NOMEM, "cannot allocate the attention scratch");
@@ -2125,18 +2126,20 @@ int fdm_attn_forward(int L, float* d_hidden, int pos, void* stream) {
   if (int rc = ensure_attn(*w, a.max_seq, s)) return rc;
   AttnScratch& ws = w->attn;
   ProfScope prof(FDM_PROF_ATTN, s);
-  FDM_HIP(launch_rms_norm(d_hidden, a.attn_norm, ws.normed, 1, FDM_HIDDEN, s));
   // q_a and kv_a (infer.m:781-789) read the same input: one matvec over the
-  // stacked [1536 + 576] rows, then both rms_norms in one launch
-  FDM_HIP(launch_mv_f16(a.q_a, ws.normed, nullptr, ws.q_a, 1536 + 576, FDM_HIDDEN, s));
-  FDM_HIP(launch_rms_norm_pair(ws.q_a, a.q_a_norm, ws.q_a_n, 1536, ws.kv_a, a.kv_a_norm, ws.c_kv_n, 512, s));
-  FDM_HIP(launch_mv_f16(a.q_b, ws.q_a_n, nullptr, ws.q, 128 * 192, 1536, s));
+  // stacked [1536 + 576] rows against hidden * attn_norm, the attention
+  // norm's 1 / rms computed beside it (ws.normed[0]) and applied by the
+  // launches after: q_b with the q_a norm inside it, the latent's norm and
+  // k_rope in the prep launch
+  FDM_HIP(launch_mv_f16_xw(a.q_a, d_hidden, a.attn_norm, ws.q_a, 1536 + 576, ws.normed, s));
+  FDM_HIP(launch_mv_f16_rn(a.q_b, ws.q_a, ws.normed, a.q_a_norm, ws.q, 128 * 192, 1536, s));
   // softmax scale with the YaRN mscale (infer.m:802-815), in float as there
   const float mscale = 0.1f * logf(40.0f) + 1.0f;
   MlaArgs m;
   m.q = ws.q;
   m.kv_a = ws.kv_a;
-  m.c_kv_n = ws.c_kv_n;
+  m.kv_scale = ws.normed;
+  m.kv_a_norm = a.kv_a_norm;
   m.freq = a.freq;
   m.pos = pos;
   m.len = a.len;

@@ -220,13 +220,10 @@ hipError_t launch_combine(const BatchArgs& b, hipStream_t s);
 // prefill_kernels.hip
 // rms_norm per token (infer.m:369-374), bit-exact: o = x * inv * w.  d <= 7168.
 hipError_t launch_rms_norm(const float* x, const float* w, float* o, int T, int d, hipStream_t s);
-// Two rows of widths d0, d1 (<= 7168) in one launch, each as launch_rms_norm.
 // rms_norm of T tokens of 7168 (o, as launch_rms_norm) and the one-plane
 // activation planes of o for the grouped GEMMs (launch_xplanes, planes = 1).
 hipError_t launch_rms_norm_planes(const float* x, const float* w, float* o, int T, _Float16* xp, float* xs,
                                   float* xe, hipStream_t s);
-hipError_t launch_rms_norm_pair(const float* x0, const float* w0, float* o0, int d0, const float* x1,
-                                const float* w1, float* o1, int d1, hipStream_t s);
 
 // gemm_kernels.hip: grouped expert GEMMs (batched decode, prefill) on MFMA.
 // Rows: pair position p (routed), T*K + t (shared expert of token t).
@@ -274,22 +271,30 @@ hipError_t launch_transpose_heads(const uint16_t* src, size_t head_stride, uint1
                                   int cols, hipStream_t s);
 
 // attn_kernels.hip: MLA attention of one decode token
+constexpr int kMlaChunkPos = 64;  // cache positions per attention chunk (16 or 32 or 64)
 struct MlaArgs {
   float* q;              // [128][192] (q_b output; the rope part rotated in place)
-  const float* kv_a;     // [576]: latent (512) + k_rope (64), before RoPE
-  const float* c_kv_n;   // [512]: rms_norm of the latent
+  const float* kv_a;     // [576]: latent (512) + k_rope (64), before RoPE, times *kv_scale
+  const float* kv_scale;  // the attention norm's 1 / rms that kv_a still owes
+  const float* kv_a_norm;  // [512]: the latent's norm weights
   const float* freq;     // [32]: yarn_freq(i)
   int pos, len;          // RoPE position; cache rows before this token
   float *cache_c, *cache_k;  // [max_seq][512], [max_seq][64]
   const uint16_t *k_b, *v_b;  // F16 [128][512][128], [128][128][512]
   float *q_abs, *wc, *attn;  // [128][512], [128][512], [128][128]
-  float* part;                        // [ceil(S / 64)][128][512] partial latent sums
-  float* stat;                        // [ceil(S / 64)][128][2]: each chunk's max score and exp sum
+  float* part;                        // [ceil(S / kMlaChunkPos)][128][512] partial latent sums
+  float* stat;                        // [ceil(S / kMlaChunkPos)][128][2]: each chunk's max score and exp sum
   float scale;
 };
 // y[r] = (res ? res[r] : 0) + W[r] . x; cols % 512 == 0, cols <= 16384
 hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, float* y, int rows, int cols,
                          hipStream_t s);
+// y[r] = W[r] . (x * nw) (x of 7168), *inv = the exact 1 / rms of x
+hipError_t launch_mv_f16_xw(const uint16_t* W, const float* x, const float* nw, float* y, int rows, float* inv,
+                            hipStream_t s);
+// y[r] = W[r] . rms_norm(x * (*xmul), nw) (the norm bit-exact); cols 1536
+hipError_t launch_mv_f16_rn(const uint16_t* W, const float* x, const float* xmul, const float* nw, float* y, int rows,
+                            int cols, hipStream_t s);
 // RoPE + cache append, Q_abs, then scores + softmax + weighted latent sum by
 // chunks, the chunks merged and v_b
 hipError_t launch_mla_attend(const MlaArgs& a, hipStream_t s);

@@ -305,4 +305,92 @@ __device__ __forceinline__ float rms_inv(float ss, int d) {
   return 1.0f / sqrtf(ss / (float)d + 1e-6f);
 }
 
+// ---- rms_norm: o = x * (1 / sqrt(sum x^2 / d + 1e-6)) * w -------------------------------
+// (x = xr * mul elementwise: mul = 1 leaves xr as it is; the attention
+// passes the scale its raw projections still owe)
+// One workgroup per token.  The sum of squares is the reference's
+// sequential fma chain, evaluated bit for bit by rms_sumsq_exact (runs of
+// integer steps inside a binade, the steps at binade edges and ties walked
+// in order); sqrt and division are IEEE; o = (x * inv) * w as infer.m:372.
+// At d = 7168 (16-byte aligned rows) every load is a 16-byte vector load
+// issued before the sum, so the row's latency is paid once.
+__device__ __forceinline__ void rms_norm_row(const float* __restrict__ xr, const float* __restrict__ w,
+                                             float* orow, int d, RmsSmem& sm, float mul = 1.0f) {
+  const int n = (d + kRmsThreads - 1) / kRmsThreads;
+  const int i0 = threadIdx.x * n;
+  const bool vec = d == kHidden && (reinterpret_cast<uintptr_t>(xr) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(orow) & 15) == 0 &&
+                   (!w || (reinterpret_cast<uintptr_t>(w) & 15) == 0);
+  float xv[kRmsMaxPer];
+  if (vec) {
+    constexpr int kV = kHidden / 4 / kRmsThreads;  // 7 vectors per thread
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(xr);
+    f32x4 xc[kV], wc[kV];
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      const f32x4 v = x4[i0 / 4 + k] * mul;  // the thread's 28 consecutive elements
+      xv[4 * k] = v.x;
+      xv[4 * k + 1] = v.y;
+      xv[4 * k + 2] = v.z;
+      xv[4 * k + 3] = v.w;
+      xc[k] = x4[threadIdx.x + kRmsThreads * k] * mul;  // coalesced, for the output
+      wc[k] = w ? reinterpret_cast<const f32x4*>(w)[threadIdx.x + kRmsThreads * k] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+    }
+    const float inv = rms_inv(rms_sumsq_exact(xv, d, sm), d);
+#pragma unroll
+    for (int k = 0; k < kV; ++k) {
+      f32x4 v;
+      v.x = xc[k].x * inv;
+      v.y = xc[k].y * inv;
+      v.z = xc[k].z * inv;
+      v.w = xc[k].w * inv;
+      if (w) {
+        v.x = v.x * wc[k].x;
+        v.y = v.y * wc[k].y;
+        v.z = v.z * wc[k].z;
+        v.w = v.w * wc[k].w;
+      }
+      reinterpret_cast<f32x4*>(orow)[threadIdx.x + kRmsThreads * k] = v;
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < kRmsMaxPer; ++j) {
+    const float v = xr[min(i0 + j, d - 1)] * mul;  // every slot loads; past the row it is a zero step
+    xv[j] = (j < n && i0 + j < d) ? v : 0.0f;
+  }
+  const float inv = rms_inv(rms_sumsq_exact(xv, d, sm), d);
+  for (int i = threadIdx.x; i < d; i += kRmsThreads) {
+    const float v = (xr[i] * mul) * inv;
+    orow[i] = w ? v * w[i] : v;
+  }
+}
+
+// The exact 1 / rms of x[0..d) = xr * mul (d <= 7168) in every thread of
+// the workgroup, as rms_norm_row computes it; read in the thread layout of
+// rms_sumsq_exact (16-byte loads at d = 7168 when xr is 16-byte aligned).
+__device__ __forceinline__ float rms_norm_inv(const float* __restrict__ xr, int d, RmsSmem& sm, float mul = 1.0f) {
+  const int n = (d + kRmsThreads - 1) / kRmsThreads;
+  const int i0 = threadIdx.x * n;
+  float xv[kRmsMaxPer];
+  if (d == kHidden && (reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
+    const f32x4* x4 = reinterpret_cast<const f32x4*>(xr);
+#pragma unroll
+    for (int k = 0; k < kRmsMaxPer / 4; ++k) {
+      const f32x4 v = x4[i0 / 4 + k] * mul;
+      xv[4 * k] = v.x;
+      xv[4 * k + 1] = v.y;
+      xv[4 * k + 2] = v.z;
+      xv[4 * k + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRmsMaxPer; ++j) {
+      const float v = xr[min(i0 + j, d - 1)] * mul;  // every slot loads; past the row it is a zero step
+      xv[j] = (j < n && i0 + j < d) ? v : 0.0f;
+    }
+  }
+  return rms_inv(rms_sumsq_exact(xv, d, sm), d);
+}
+
 }  // namespace fdm

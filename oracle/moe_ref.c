@@ -272,6 +272,42 @@ static void mv_f16_rows_d(const uint16_t *W, const double *x, double *y, int row
     }
 }
 
+/* The cache row of one token at position pos (infer.m:786-800, 817-827):
+ * c_kv = rms_norm(kv_a[:512] . rms_norm(hidden, attn_norm), kv_a_norm) and
+ * the YaRN-rotated k_rope = kv_a[512:576], the matvec in double and rounded
+ * to float as orc_mla_forward stores them (it calls this). */
+static void mla_cache_row(const float *attn_norm, const uint16_t *kv_a, const float *kv_a_norm,
+                          const float *hidden, int pos, float *c_row, float *k_row) {
+    const int H = ORC_HIDDEN, KVL = 512, ROPE = 64;
+    float *normed = (float *)malloc(sizeof(float) * H);
+    double *xd = (double *)malloc(sizeof(double) * H);
+    double kva[576];
+    float kvf[512];
+    float freq[32];
+    orc_yarn_freq(freq);
+    orc_rms_norm(hidden, attn_norm, normed, H);
+    for (int i = 0; i < H; ++i) xd[i] = normed[i];
+    mv_f16_rows_d(kv_a, xd, kva, 576, H);
+    for (int i = 0; i < KVL; ++i) kvf[i] = (float)kva[i];
+    orc_rms_norm(kvf, kv_a_norm, c_row, KVL);
+    for (int i = 0; i < ROPE / 2; ++i) {
+        const float ang = (float)pos * freq[i];
+        const double c = cos((double)ang), sn = sin((double)ang);
+        const double a = kva[KVL + 2 * i], b = kva[KVL + 2 * i + 1];
+        k_row[2 * i] = (float)(a * c - b * sn);
+        k_row[2 * i + 1] = (float)(a * sn + b * c);
+    }
+    free(normed); free(xd);
+}
+
+/* Only the cache append of mla_forward: row len of the cache for a token at
+ * position pos, without its attention output (tests fill long caches with
+ * it and check the forward of the tokens after). */
+void orc_mla_append(const float *attn_norm, const uint16_t *kv_a, const float *kv_a_norm, const float *hidden,
+                    float *cache_c, float *cache_k, int len, int pos) {
+    mla_cache_row(attn_norm, kv_a, kv_a_norm, hidden, pos, cache_c + (size_t)len * 512, cache_k + (size_t)len * 64);
+}
+
 /* mla_forward (infer.m:766-903) of one token at position pos; the cache holds
  * len rows before it and receives row len.  Dot products, softmax and the
  * latent sums in double (the truth); the three rms_norms are the reference's
@@ -288,9 +324,6 @@ void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q
     double *qa = (double *)malloc(sizeof(double) * QA);
     float *qaf = (float *)malloc(sizeof(float) * QA);
     double *q = (double *)malloc(sizeof(double) * NH * QK);
-    double *kva = (double *)malloc(sizeof(double) * 576);
-    float *kvf = (float *)malloc(sizeof(float) * KVL);
-    float *ckv = (float *)malloc(sizeof(float) * KVL);
     double *qabs = (double *)malloc(sizeof(double) * NH * KVL);
     double *p = (double *)malloc(sizeof(double) * S);
     double *wc = (double *)malloc(sizeof(double) * KVL);
@@ -306,11 +339,9 @@ void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q
     orc_rms_norm(qaf, q_a_norm, qaf, QA);
     for (int i = 0; i < QA; ++i) qa[i] = qaf[i];
     mv_f16_rows_d(q_b, qa, q, NH * QK, QA);
-    mv_f16_rows_d(kv_a, xd, kva, 576, H);
-    for (int i = 0; i < KVL; ++i) kvf[i] = (float)kva[i];
-    orc_rms_norm(kvf, kv_a_norm, ckv, KVL);
-    /* interleaved-pair YaRN rotation (infer.m:626-655) */
-    double krot[64];
+    /* the cache row: c_kv and the rotated k_rope */
+    mla_cache_row(attn_norm, kv_a, kv_a_norm, hidden, pos, cache_c + (size_t)len * KVL, cache_k + (size_t)len * ROPE);
+    /* interleaved-pair YaRN rotation of q_rope (infer.m:626-655) */
     for (int i = 0; i < ROPE / 2; ++i) {
         const float ang = (float)pos * freq[i];
         const double c = cos((double)ang), sn = sin((double)ang);
@@ -320,12 +351,7 @@ void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q
             qr[2 * i] = a * c - b * sn;
             qr[2 * i + 1] = a * sn + b * c;
         }
-        const double a = kva[KVL + 2 * i], b = kva[KVL + 2 * i + 1];
-        krot[2 * i] = a * c - b * sn;
-        krot[2 * i + 1] = a * sn + b * c;
     }
-    for (int i = 0; i < KVL; ++i) cache_c[(size_t)len * KVL + i] = ckv[i];
-    for (int i = 0; i < ROPE; ++i) cache_k[(size_t)len * ROPE + i] = (float)krot[i];
     const double scale = orc_mla_scale();
     for (int h = 0; h < NH; ++h) {
         /* Q_abs[h] = k_b[h] (KV_LORA x NOPE) . q_nope[h] (infer.m:722-731) */
@@ -354,7 +380,7 @@ void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q
     }
     mv_f16_rows_d(o_proj, attn, o, H, NH * VH);
     for (int i = 0; i < H; ++i) hidden[i] = (float)((double)hidden[i] + o[i]);
-    free(normed); free(xd); free(qa); free(qaf); free(q); free(kva); free(kvf); free(ckv);
+    free(normed); free(xd); free(qa); free(qaf); free(q);
     free(qabs); free(p); free(wc); free(attn); free(o);
 }
 

@@ -76,6 +76,8 @@ void orc_dense_ffn(const uint16_t *gate, const uint16_t *up, const uint16_t *dow
 /* MLA attention of one decode token (infer.m:586-655, 766-903), see moe_ref.c. */
 void orc_yarn_freq(float *freq);
 float orc_mla_scale(void);
+void orc_mla_append(const float *attn_norm, const uint16_t *kv_a, const float *kv_a_norm, const float *hidden,
+                    float *cache_c, float *cache_k, int len, int pos);
 void orc_mla_forward(const float *attn_norm, const uint16_t *q_a, const float *q_a_norm, const uint16_t *q_b,
                      const uint16_t *kv_a, const float *kv_a_norm, const uint16_t *k_b, const uint16_t *v_b,
                      const uint16_t *o_proj, float *hidden, float *cache_c, float *cache_k, int len, int pos);

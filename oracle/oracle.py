@@ -58,6 +58,7 @@ def _load():
         "orc_yarn_freq": (None, [_f32p]),
         "orc_mla_scale": (ctypes.c_float, []),
         "orc_mla_forward": (None, [_vp] * 9 + [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
+        "orc_mla_append": (None, [_vp] * 3 + [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_router_logits": (None, [_f32p, _f32p, _f32p, ctypes.c_int, ctypes.c_int]),
         "orc_route_ex": (None, [_f32p, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                 ctypes.c_int, ctypes.c_float, _i32p, _f32p]),
@@ -230,6 +231,15 @@ def mla_forward(w, hidden, cache, pos):
     L.orc_mla_forward(*args, h, cache.c, cache.k, cache.len, pos)
     cache.len += 1
     return h
+
+
+def mla_append(w, hidden, cache, pos):
+    """Only the cache append of mla_forward (the token's c_kv and rotated
+    k_rope as row cache.len), for filling long caches cheaply."""
+    h = np.ascontiguousarray(hidden, dtype=np.float32)
+    args = [_ptr(np.ascontiguousarray(w[n])) for n in ("attn_norm", "kv_a", "kv_a_norm")]
+    L.orc_mla_append(*args, h, cache.c, cache.k, cache.len, pos)
+    cache.len += 1
 
 
 # ---- router -------------------------------------------------------------------

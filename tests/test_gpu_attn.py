@@ -49,6 +49,39 @@ def test_attn_tokens_match_oracle(fdm, oracle, attn_layer):
     assert np.array_equal(to_host(d).view(np.uint32), first[1].view(np.uint32))
 
 
+def test_attn_long_cache_matches_oracle(fdm, oracle):
+    """A cache of up to 2100 positions: the scores, softmax and latent sums
+    run over many chunks, merged by the combine (every merge path: a few
+    chunks, one batch of chunk loads, and the batched walk of long caches).
+    The oracle fills its cache with the append alone and runs the whole
+    forward at the checked lengths."""
+    w = mla_weights(829)
+    say("attn_upload L=5 max_seq=2112")
+    fdm.attn_upload(5, w, max_seq=2112)
+    try:
+        cache = oracle.MlaCache(2112)
+        rng = np.random.default_rng(11)
+        checks = {69, 599, 1029, 2099}  # token n: cache length n + 1 when it attends
+        for n in range(2100):
+            hidden = rng.normal(0, 1, H).astype(np.float32)
+            d = to_dev(hidden)
+            if n in checks or n % 500 == 0:
+                say(f"attn_forward L=5 pos={n}")
+            fdm.attn_forward(5, d, n)
+            if n in checks:
+                got = to_host(d)
+                want = oracle.mla_forward(w, hidden, cache, n)
+                err = rel_l2(got, want.astype(np.float64))
+                err_attn = rel_l2(got.astype(np.float64) - hidden, want.astype(np.float64) - hidden)
+                print(f"cache {n + 1}: rel_l2 {err:.2e}, attention part {err_attn:.2e}")
+                assert err <= TOL and err_attn <= TOL, n
+            else:
+                oracle.mla_append(w, hidden, cache, n)
+        assert fdm.attn_len(5) == 2100
+    finally:
+        fdm.attn_release(5)
+
+
 def test_attn_errors(fdm, attn_layer):
     x = to_dev(np.zeros(H, np.float32))
     with pytest.raises(fdm.FdmError):

@@ -64,3 +64,18 @@ def test_mla_forward_matches_numpy(oracle):
         want, c, k = numpy_mla(w, hidden, c, k, pos, oracle)
         assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want)), pos
         assert np.array_equal(cache.c[:cache.len], c) and np.allclose(cache.k[:cache.len], k, rtol=1e-6, atol=1e-7)
+
+
+def test_mla_append_is_the_forward_cache_row(oracle):
+    """mla_append (the cache append alone) writes the same cache row as
+    mla_forward, bit for bit, at in-order and jumped positions."""
+    w = mla_weights(767)
+    rng = np.random.default_rng(2)
+    full, app = oracle.MlaCache(4), oracle.MlaCache(4)
+    for pos in (0, 5, 1999):
+        hidden = rng.normal(0, 1, H).astype(np.float32)
+        oracle.mla_forward(w, hidden, full, pos)
+        oracle.mla_append(w, hidden, app, pos)
+    assert app.len == full.len == 3
+    assert np.array_equal(app.c.view(np.uint32), full.c.view(np.uint32))
+    assert np.array_equal(app.k.view(np.uint32), full.k.view(np.uint32))
