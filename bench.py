@@ -187,7 +187,8 @@ def bench_matvec(F, torch, args, n_sets=64, calls=256):
     us = event_times(torch, run, calls)
     del W
     nbytes = nb * 144 + cols * 4 + rows * 4
-    r = {"workload": "Q4_K matvec 2048x7168, batch 1 (fdm_matvec_q4k: digits of x + fused dequant matvec)",
+    r = {"workload": "Q4_K matvec 2048x7168, batch 1 (fdm_matvec_q4k: one launch, x staged per workgroup, "
+                     "fp32 group dots)",
          "weight_sets": n_sets, "calls": calls, "bytes_per_call": nbytes}
     r.update(percentiles(us))
     r["gbps"] = round(nbytes / (r["median_us"] * 1e-6) / 1e9, 1)
