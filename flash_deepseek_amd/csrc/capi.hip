@@ -1024,10 +1024,8 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
     return fail(FDM_E_INVAL, "blob must be 4-byte and x 16-byte aligned");
   if (d_act && !aligned(d_act, 4)) return fail(FDM_E_INVAL, "act must be 4-byte aligned");
   hipStream_t s = as_stream(stream);
-  // one launch on the caller's packed blob: with a Q4_K down matrix the
-  // fp32 expert kernel (expert_kernels.hip); with Q6_K the layer kernel's
-  // work list without router or route (the expert as the shared slot of a
-  // zero-routed-expert layer)
+  // one launch of the fp32 expert kernel (expert_kernels.hip) on the
+  // caller's packed blob, Q4_K or Q6_K down
   Workspace* ws = nullptr;
   if (int rc = stream_workspace(s, &ws)) return rc;
   LayerArgs a;
@@ -1047,12 +1045,11 @@ int fdm_expert_ffn(const void* d_blob, size_t expert_size, const float* d_x, flo
   a.idx = ws->idx;
   a.w = ws->w;
   layer_workspace_args(a, ws);
-  a.expert_only = 1;
   a.act_out = d_act;
   {
     ProfScope p(FDM_PROF_GATEUP, s);
-    // Q4_K down: the fp32 expert kernel; Q6_K down: the layer kernel's list
-    FDM_HIP(q6 ? launch_layer(a, s) : launch_expert_f32(a, s));
+    // the fp32 expert kernel (gate/up items, one activation hand-off, down items)
+    FDM_HIP(launch_expert_f32(a, s));
   }
   return FDM_OK;
 }

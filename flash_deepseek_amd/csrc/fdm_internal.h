@@ -153,8 +153,7 @@ struct LayerArgs {
   unsigned* flags;         // kLayerFlags x kLayerStride, zero at first use
   unsigned epoch;          // non-zero, different from every earlier call's
   unsigned spin_limit;     // polls before a wait gives up (kLayerSpinLimit)
-  int expert_only = 0;     // one expert from the packed blob `shared` (K = 0, no router)
-  float* act_out = nullptr;  // expert_only: receives the SwiGLU activations [2048] (or null)
+  float* act_out = nullptr;  // launch_expert_f32: receives the SwiGLU activations [2048] (or null)
 };
 constexpr unsigned kLayerSpinLimit = 1u << 17;  // polls of one wait (each >= ~1 us)
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s);

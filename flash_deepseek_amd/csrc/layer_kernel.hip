@@ -16,9 +16,7 @@
 //   router row e (256)
 //   route: the expert set (1);  the exact route() (1)
 //   shared expert: gate/up items of both column parts, then the digit
-//     records of its activations (one item per part; in the expert-only
-//     list, where the final items are the next step, they make the records
-//     themselves)
+//     records of its activations (one item per part)
 //   routed experts, part-major: gate/up items of part q of every slot, then
 //     the down items of part q - lag of every slot, q = 0, 1, ...; a down
 //     item makes its part's activation records itself from the tagged
@@ -453,7 +451,7 @@ __device__ __forceinline__ void exact_item(const LayerArgs& a) {
 // 32-63 up, 16 lanes per row); SwiGLU in registers; the activations go out
 // tagged.  The route and the digits of h_post are waited for and staged
 // once per run, so their round trips are paid once for kGuPer tiles.
-template <bool PACKED, bool ROUTED>
+template <bool ROUTED>
 __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int tile0, LayerSmem& sm) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15, g = l16 & 3;
@@ -493,20 +491,17 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
   // then lead the memory queues and the route goes out sooner, while these
   // 16.5 MB still fill the time the route takes (measured on MI355X: 0.5,
   // 0.85 and 1.3 us all ~0.8 us faster than no hold).
-  if (!ROUTED && !PACKED) __builtin_amdgcn_s_sleep(32);
+  if (!ROUTED) __builtin_amdgcn_s_sleep(32);
   const uint8_t* blob = ROUTED ? expert_blob(a, sm.eid) : a.shared;
   const uint8_t* src = blob ? blob : a.experts;
   const Q4KScaleSel sel = q4k_scale_sel(g);
   for (int t = 0; t < kGuPer; ++t) {
     const int row = (tile0 + t) * kGuTileRows + 2 * wave + (q & 1);
     Q4KGroupLoad ld[7];
-    // resident expert layout: each half-wave load reads one 512-byte run;
-    // packed layout (a caller's blob): 16-byte slices of the row's blocks
+    // resident expert layout: each half-wave load reads one 512-byte run
     const uint8_t* mat = src + (q >= 2 ? kGateBytes : 0);
 #pragma unroll
-    for (int i = 0; i < 7; ++i)
-      ld[i] = PACKED ? q4k_load_group(mat + (size_t)row * kQ4KRowHidden + (size_t)(4 * i + (l16 >> 2)) * kQ4KBlock, g)
-                     : rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
+    for (int i = 0; i < 7; ++i) ld[i] = rel_load_group<false>(mat, row, 4 * i + (l16 >> 2), g);
     if (t == 0) {
       if (!ROUTED) {
         wait_route_xd(a, slot, false, true, sm);
@@ -526,7 +521,6 @@ __device__ __forceinline__ void gateup_run(const LayerArgs& a, int slot, int til
     if (lane == 0 || lane == 16) {
       const float av = silu_mul(acc, up);
       put_tagged(a.act + (size_t)slot * kFfn + row, a.epoch, __float_as_uint(av));
-      if (PACKED && a.act_out) a.act_out[row] = av;
     }
   }
 }
@@ -759,7 +753,7 @@ constexpr int kFinMaxRouted = kLayerMaxSlots - 1;             // routed slots (F
 constexpr int kFinWordsMax = 2 * kFinMaxRouted * kFinRowsQ4;  // routed part outputs of one item
 static_assert(kFinRowsQ4 >= kFinRowsQ6, "LDS of the final items sized for the Q4_K rows");
 
-template <bool Q6, bool PACKED>
+template <bool Q6>
 __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSmem& sm) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -776,29 +770,20 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
   const int H = 8 * p6 + 2 * b6 + h6;  // half block of the row
   Q4KGroupLoad ld0[kQ4M], ld1[kQ4M];
   constexpr int kQ6M = kFinRowsQ6 / 16;  // Q6_K rows per lane
-  Q6KHalfLoad l6p[kQ6M];  // packed blob
-  Q6KHalfW l6[kQ6M];      // resident layout
+  Q6KHalfW l6[kQ6M];
   if (dbase) {
     if (!Q6) {
 #pragma unroll
       for (int m = 0; m < kQ4M; ++m) {
         const int row = r0 + 4 * kQ4M * wave + 4 * m + rs;
-        if (PACKED) {
-          ld0[m] = q4k_load_group(dbase + (size_t)row * kQ4KRowFfn + (size_t)bq * kQ4KBlock, g);
-          ld1[m] = q4k_load_group(dbase + (size_t)row * kQ4KRowFfn + (size_t)(4 + bq) * kQ4KBlock, g);
-        } else {
-          ld0[m] = rel_load_group<true>(dbase, row, bq, g);
-          ld1[m] = rel_load_group<true>(dbase, row, 4 + bq, g);
-        }
+        ld0[m] = rel_load_group<true>(dbase, row, bq, g);
+        ld1[m] = rel_load_group<true>(dbase, row, 4 + bq, g);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kQ6M; ++j) {
         const int row = r0 + 4 * kQ6M * wave + 4 * j + r6;
-        if (PACKED)
-          l6p[j] = q6k_load_half(dbase + (size_t)row * kQ6KRowFfn + (H >> 1) * kQ6KBlock, h6);
-        else
-          l6[j] = q6k_rel_load_half(dbase, row, 4 * p6 + b6, h6);
+        l6[j] = q6k_rel_load_half(dbase, row, 4 * p6 + b6, h6);
       }
     }
   }
@@ -811,12 +796,6 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
   const int nE = 2 * a.K * R;  // word e: slot e / (2 R), part e / R % 2, row e % R
   const uint64_t* xsrc = act_xd_words(a, a.K, 0);
   uint32_t xw[kXPer];
-  // one expert (the expert-only list): its activations' records are made
-  // here from the 2048 tagged activations, no digit items
-  constexpr bool kDirect = PACKED && FDM_ACT_DIRECT;
-  constexpr int kAPer = kFfn / 256;
-  const uint64_t* sact = a.act + (size_t)a.K * kFfn;
-  float av[kDirect ? kAPer : 1];
   float ev[kEPer];
   uint64_t tw = 0, tp = 0;
   bool e_ok = true;
@@ -852,44 +831,27 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
   };
   // the last word of each part's records (activations) as sentinels
   // (without a shared expert the first round always succeeds)
-  poll_record(a, kDirect ? sact + kPartCols - 1 : xsrc + kXW / 2 - 1, kDirect ? sact + kFfn - 1 : xsrc + kXW - 1, [&] {
+  poll_record(a, xsrc + kXW / 2 - 1, xsrc + kXW - 1, [&] {
     bool ok = true;
     if (dbase) {
-      if constexpr (kDirect) {
 #pragma unroll
-        for (int i = 0; i < kAPer; ++i) {
-          const uint64_t t = get_tagged(sact + threadIdx.x + 256 * i);
+      for (int i = 0; i < kXPer; ++i) {
+        const int k = threadIdx.x + 256 * i;
+        if (k < kXW) {
+          const uint64_t t = get_tagged(xsrc + k);
           ok = ok && tag_is(t, a.epoch);
-          av[i] = tagged_f(t);
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < kXPer; ++i) {
-          const int k = threadIdx.x + 256 * i;
-          if (k < kXW) {
-            const uint64_t t = get_tagged(xsrc + k);
-            ok = ok && tag_is(t, a.epoch);
-            xw[i] = (uint32_t)t;
-          }
+          xw[i] = (uint32_t)t;
         }
       }
     }
     load_routed();
     return ok;
   });
-  if constexpr (kDirect) {
-    // element 256 i + 64 w + lane lives in wave w's lanes: record 4 i + w
-    if (dbase) {
+  uint32_t* xdst = reinterpret_cast<uint32_t*>(sm.fin.xs);
 #pragma unroll
-      for (int i = 0; i < kAPer; ++i) digits_to_lds(av[i], sm.fin.xs[4 * i + wave]);
-    }
-  } else {
-    uint32_t* xdst = reinterpret_cast<uint32_t*>(sm.fin.xs);
-#pragma unroll
-    for (int i = 0; i < kXPer; ++i) {
-      const int k = threadIdx.x + 256 * i;
-      if (dbase && k < kXW) xdst[k] = xw[i];
-    }
+  for (int i = 0; i < kXPer; ++i) {
+    const int k = threadIdx.x + 256 * i;
+    if (dbase && k < kXW) xdst[k] = xw[i];
   }
   store_routed();
   const bool routed_ready = __syncthreads_and(e_ok);
@@ -923,7 +885,7 @@ __device__ __forceinline__ void final_item(const LayerArgs& a, int item, LayerSm
       for (int j = 0; j < kQ6M; ++j) {
         int gi = 2 * H;
         __asm__ volatile("" : "+v"(gi));
-        acc[j] = PACKED ? q6k_half_dot_ld(l6p[j], &sm.fin.xs[gi]) : q6k_half_dot_w(l6[j], &sm.fin.xs[gi]);
+        acc[j] = q6k_half_dot_w(l6[j], &sm.fin.xs[gi]);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -971,24 +933,20 @@ struct LayerList {
   int gup, dnp;  // gate/up and down items per (slot, part)
 };
 
-// Expert-only lists (one expert, no router: K = 0, the expert in the shared
-// slot) have no router rows and no route items.
-__host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6, bool norm,
-                                                         bool expert = false) {
+__host__ __device__ __forceinline__ LayerList layer_list(int K, int n_slots, bool q6, bool norm) {
   const int hs = n_slots - K;  // 1 with a shared expert
   LayerList l;
   l.gup = kGuPerPart;
   l.dnp = dn_per_part(q6);
   l.xd = norm ? 1 : 0;  // item 0: the fused rms_norm
   l.router = l.xd + kXdItems;
-  l.route = l.router + (expert ? 0 : kRows);
-  l.exact = l.route + (expert ? 0 : 1);
-  l.shared = l.exact + (expert ? 0 : 1);
+  l.route = l.router + kRows;
+  l.exact = l.route + 1;
+  l.shared = l.exact + 1;
   l.shadg = l.shared + hs * kParts * l.gup;
   // activation digit items: the shared expert's (at the head, off the
-  // critical path) unless the list has only it; routed slots' down items
-  // make their records themselves
-  l.routed = l.shadg + ((expert && FDM_ACT_DIRECT) ? 0 : hs * kParts);
+  // critical path); routed slots' down items make their records themselves
+  l.routed = l.shadg + hs * kParts;
   l.fin = l.routed + K * kParts * (l.gup + kAdgRouted + l.dnp);
   l.total = l.fin + fin_items(q6);
   return l;
@@ -1033,38 +991,36 @@ __device__ __forceinline__ void routed_item(const LayerList& l, int K, int off, 
 
 }  // namespace
 
-// EXPERT: one expert from a caller's packed blob (the shared slot, K = 0),
-// no router or route items.
-template <bool Q6, bool EXPERT>
+template <bool Q6>
 __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
-  const LayerList l = layer_list(a.K, a.n_slots, Q6, a.norm_w != nullptr, EXPERT);
+  const LayerList l = layer_list(a.K, a.n_slots, Q6, a.norm_w != nullptr);
   const int it = blockIdx.x;
   if (it < l.xd) {
     norm_item(a, sm);
   } else if (it < l.router) {
     xd_item(a, it - l.xd, sm);
-  } else if (!EXPERT && it < l.route) {
+  } else if (it < l.route) {
     router_row(a, it - l.router, sm);
-  } else if (!EXPERT && it == l.route) {
+  } else if (it == l.route) {
     route_item(a, sm);
-  } else if (!EXPERT && it == l.exact) {
+  } else if (it == l.exact) {
     exact_item(a);
   } else if (it < l.shadg) {
     const int off = it - l.shared;
-    gateup_run<EXPERT, false>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, sm);
+    gateup_run<false>(a, a.K, (off / l.gup) * (kPartCols / kGuTileRows) + (off % l.gup) * kGuPer, sm);
   } else if (it < l.routed) {
     adg_item(a, a.K, it - l.shadg, sm);
-  } else if (!EXPERT && it < l.fin) {
+  } else if (it < l.fin) {
     int kind, slot, part, idx;
     routed_item(l, a.K, it - l.routed, kind, slot, part, idx);
     if (kind == 0)
-      gateup_run<false, true>(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, sm);
+      gateup_run<true>(a, slot, part * (kPartCols / kGuTileRows) + idx * kGuPer, sm);
     else if (kind == 1)
       adg_item(a, slot, part, sm);
     else
       down_part<Q6>(a, slot, part, idx, sm);
   } else {
-    final_item<Q6, EXPERT>(a, it - l.fin, sm);
+    final_item<Q6>(a, it - l.fin, sm);
   }
 }
 
@@ -1072,34 +1028,20 @@ __device__ __forceinline__ void layer_item(const LayerArgs& a, LayerSmem& sm) {
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_layer_q4k(
     LayerArgs a) {
   __shared__ LayerSmem sm;
-  layer_item<false, false>(a, sm);
+  layer_item<false>(a, sm);
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_layer_q6k(LayerArgs a) {
   __shared__ LayerSmem sm;
-  layer_item<true, false>(a, sm);
-}
-
-// One expert FFN (fdm_expert_ffn) in one launch: digits | gate/up items |
-// down parts | combine tiles, on the caller's packed blob.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_q4k(
-    LayerArgs a) {
-  __shared__ LayerSmem sm;
-  layer_item<false, true>(a, sm);
-}
-
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void k_expert_q6k(LayerArgs a) {
-  __shared__ LayerSmem sm;
-  layer_item<true, true>(a, sm);
+  layer_item<true>(a, sm);
 }
 
 hipError_t launch_layer(const LayerArgs& a, hipStream_t s) {
-  const bool ex = a.expert_only != 0;
-  const LayerList l = layer_list(a.K, a.n_slots, a.down_q6 != 0, a.norm_w != nullptr, ex);
+  const LayerList l = layer_list(a.K, a.n_slots, a.down_q6 != 0, a.norm_w != nullptr);
   if (a.down_q6)
-    hipLaunchKernelGGL(ex ? k_expert_q6k : k_layer_q6k, dim3(l.total), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_layer_q6k, dim3(l.total), dim3(256), 0, s, a);
   else
-    hipLaunchKernelGGL(ex ? k_expert_q4k : k_layer_q4k, dim3(l.total), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_layer_q4k, dim3(l.total), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
