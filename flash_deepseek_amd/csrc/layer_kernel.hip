@@ -386,10 +386,12 @@ __device__ __forceinline__ void wait_scores_staggered(const LayerArgs& a, float 
 __device__ __forceinline__ void route_item(const LayerArgs& a, LayerSmem& sm) {
   const int lane = threadIdx.x & 63;
   __builtin_amdgcn_s_setprio(3);
-  float bj[4];
+  float bj[4], bj4[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) bj[j] = a.bias ? a.bias[64 * j + lane] : 0.0f;
-  float sc[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) bj4[m] = a.bias ? a.bias[4 * lane + m] : 0.0f;  // 4-byte aligned bias
+  float sc[4], sc4[4];
   // Two passes over one copy of the set code.  Pass 0 runs it on made-up
   // scores and publishes nothing, while the router rows are still
   // streaming: every launch starts with an empty instruction cache, and the
@@ -403,12 +405,22 @@ __device__ __forceinline__ void route_item(const LayerArgs& a, LayerSmem& sm) {
     __asm__ volatile("" : "+s"(p));  // opaque: the loop keeps one copy of the code
     if (p == 0) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) sc[j] = (float)(64 * j + lane) * (1.0f / 256.0f);
+      for (int j = 0; j < 4; ++j) {
+        sc[j] = (float)(64 * j + lane) * (1.0f / 256.0f);
+        sc4[j] = (float)(4 * lane + j) * (1.0f / 256.0f);
+      }
     } else {
       wait_scores_staggered(a, sc, sm);
+      if (threadIdx.x < 64) {
+        const f32x4 v = reinterpret_cast<const f32x4*>(sm.ssc)[lane];  // experts 4 lane .. 4 lane + 3
+        sc4[0] = v.x;
+        sc4[1] = v.y;
+        sc4[2] = v.z;
+        sc4[3] = v.w;
+      }
     }
     if (threadIdx.x < 64)
-      route_set_publish(sc, bj, a.K, [&](int slot, int id) {
+      route_set_publish(sc, bj, sc4, bj4, a.K, [&](int slot, int id) {
         if (p == 1 && slot >= 0) put_tagged(a.prov + slot, a.epoch, (uint32_t)id);
       });
   }

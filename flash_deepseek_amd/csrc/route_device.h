@@ -198,6 +198,59 @@ __device__ __forceinline__ void route_keys(const float score[4], const float bj[
   }
 }
 
+// route_keys in the "four consecutive experts" layout: lane l holds the
+// sigmoid scores of experts 4 l .. 4 l + 3 in score4[m] (their biases in
+// bj4[m]), so a group of 32 experts is the eight lanes 8 g .. 8 g + 7.  The
+// group's top-2 multiset (infer.m:933-941) is its lanes' local top-2 merged
+// by three DPP row shifts inside the eight lanes (a shifted-in value from
+// the group before is replaced by -1e30): one dependent chain of three
+// steps instead of five steps over four registers.  The top-2 is a multiset,
+// so the merge order does not change it, and each group's sum t1 + t2 is
+// the same float addition as in route_keys; the group choice and the masked
+// keys follow route_keys.  Keys vk4[m] belong to expert 4 l + m.
+__device__ __forceinline__ void route_keys4(const float score4[4], const float bj4[4], int vk4[4]) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  float choice[4], a[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    choice[m] = score4[m] + bj4[m];
+    a[m] = choice[m] > -1e30f ? choice[m] : -1e30f;
+  }
+  float t1 = fmaxf(a[0], a[1]), t2 = fminf(a[0], a[1]);
+  top2_merge(t1, t2, fmaxf(a[2], a[3]), fminf(a[2], a[3]));
+  const int gl = lane & 7;  // lane within the group
+  {
+    float o1 = row_shr<1>(t1, -1e30f), o2 = row_shr<1>(t2, -1e30f);
+    top2_merge(t1, t2, gl >= 1 ? o1 : -1e30f, gl >= 1 ? o2 : -1e30f);
+  }
+  {
+    float o1 = row_shr<2>(t1, -1e30f), o2 = row_shr<2>(t2, -1e30f);
+    top2_merge(t1, t2, gl >= 2 ? o1 : -1e30f, gl >= 2 ? o2 : -1e30f);
+  }
+  {
+    float o1 = row_shr<4>(t1, -1e30f), o2 = row_shr<4>(t2, -1e30f);
+    top2_merge(t1, t2, gl >= 4 ? o1 : -1e30f, gl >= 4 ? o2 : -1e30f);
+  }
+  const float gsum = t1 + t2;  // lane 8 g + 7: group g's sum
+  float gs[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) gs[g] = readlane_f(gsum, 8 * g + 7);
+  float mine = -1e30f;
+#pragma unroll
+  for (int G = 0; G < 8; ++G) mine = lane == G ? gs[G] : mine;
+  int rank = 0;
+#pragma unroll
+  for (int h = 0; h < 8; ++h) {
+    const bool oe = gs[h] > -1e30f;
+    rank += (oe && (gs[h] > mine || (gs[h] == mine && h < lane))) ? 1 : 0;
+  }
+  const unsigned selmask = (unsigned)__ballot(lane < 8 && mine > -1e30f && rank < 4);
+  const bool in_sel = (selmask >> (lane >> 3)) & 1u;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) vk4[m] = in_sel ? sort_key(choice[m]) : sort_key(-1e30f);
+}
+
 // route() for one token, executed by one full wave with the sigmoid scores
 // in registers: exact reference selection, tie rules and slot order.  Lane
 // k (k < K) receives slot k's expert id and weight.
@@ -361,7 +414,9 @@ __device__ __forceinline__ void top8_wave(const int (&k)[4], int (&t)[8]) {
   merge8<0x143, 0xC>(t);  // row_bcast:31 into rows 2 and 3
 }
 
-// The set route() selects.  Keys are PACKED: the order-preserving key's
+// The set route() selects (scores and biases in both layouts: score[j] /
+// bj[j] of expert 64 j + lane, score4[m] / bj4[m] of expert 4 lane + m).
+// Keys are PACKED: the order-preserving key's
 // upper 24 bits, then 255 - expert id, so the keys are unique and each
 // names its expert (the lowest id first among equal truncated keys).
 // Truncation is monotone, so the K largest packed keys are the reference's
@@ -381,20 +436,22 @@ __device__ __forceinline__ void top8_wave(const int (&k)[4], int (&t)[8]) {
 // In the ambiguous case the slots not yet published receive the rest of
 // the reference's (multi)set from the exact scan.
 template <typename Publish>
-__device__ __forceinline__ void route_set_publish(const float score[4], const float bj[4], int K,
-                                                  Publish&& publish) {
+__device__ __forceinline__ void route_set_publish(const float score[4], const float bj[4], const float score4[4],
+                                                  const float bj4[4], int K, Publish&& publish) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  int vk[4];
-  route_keys(score, bj, vk);
+  // the set from the four-consecutive-experts layout (route_keys4); the
+  // exact scan of the ambiguous case below takes the 64 j + lane layout
+  int vk4[4];
+  route_keys4(score4, bj4, vk4);
   const int floor = sort_key(-1e30f);
   int pk[4];
   bool near_floor = false;  // a candidate whose truncated key is the floor's
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool cand = vk[j] > floor;
-    near_floor = near_floor || (cand && (vk[j] >> 8) == (floor >> 8));
-    pk[j] = (cand && (vk[j] >> 8) != (floor >> 8)) ? ((vk[j] & ~255) | (255 - (64 * j + lane))) : INT_MIN;
+  for (int m = 0; m < 4; ++m) {
+    const bool cand = vk4[m] > floor;
+    near_floor = near_floor || (cand && (vk4[m] >> 8) == (floor >> 8));
+    pk[m] = (cand && (vk4[m] >> 8) != (floor >> 8)) ? ((vk4[m] & ~255) | (255 - (4 * lane + m))) : INT_MIN;
   }
   bool ambiguous = __ballot(near_floor) != 0;
   int ext = 0;    // extraction: lane k holds the k-th extracted expert
@@ -465,6 +522,8 @@ __device__ __forceinline__ void route_set_publish(const float score[4], const fl
   // published experts are strictly above the K-th key, so each is in it;
   // match each published slot to one exact slot and hand the unmatched
   // exact slots to the remaining slots.
+  int vk[4];
+  route_keys(score, bj, vk);
   int eid;
   float ew;
   slot_scan(vk, score, K, 2.5f, eid, ew);
