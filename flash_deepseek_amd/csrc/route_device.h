@@ -80,9 +80,9 @@ __device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float
 // Order-preserving int image of a non-NaN float (-0 and +0 map together);
 // NaN maps below every other key, so it never enters a slot.
 __device__ __forceinline__ int sort_key(float f) {
-  if (f != f) return INT_MIN;
   const int b = __float_as_int(f + 0.0f);
-  return b >= 0 ? b : b ^ 0x7FFFFFFF;
+  const int k = b >= 0 ? b : b ^ 0x7FFFFFFF;
+  return f != f ? INT_MIN : k;  // selects, no branch
 }
 
 // Minimum of an int over the whole wave.
@@ -187,8 +187,9 @@ __device__ __forceinline__ void route_keys(const float score[4], const float bj[
   int rank = 0;
 #pragma unroll
   for (int h = 0; h < 8; ++h) {
-    const bool oe = gs[h] > -1e30f;
-    rank += (oe && (gs[h] > mine || (gs[h] == mine && h < lane))) ? 1 : 0;
+    // bitwise, not short-circuit: the && / || form compiles to exec-mask branches
+    const int oe = (int)(gs[h] > -1e30f);
+    rank += oe & ((int)(gs[h] > mine) | ((int)(gs[h] == mine) & (int)(h < lane)));
   }
   const unsigned selmask = (unsigned)__ballot(lane < 8 && mine > -1e30f && rank < 4);
 #pragma unroll
@@ -242,13 +243,16 @@ __device__ __forceinline__ void route_keys4(const float score4[4], const float b
   int rank = 0;
 #pragma unroll
   for (int h = 0; h < 8; ++h) {
-    const bool oe = gs[h] > -1e30f;
-    rank += (oe && (gs[h] > mine || (gs[h] == mine && h < lane))) ? 1 : 0;
+    // bitwise, not short-circuit: the && / || form compiles to exec-mask branches
+    const int oe = (int)(gs[h] > -1e30f);
+    rank += oe & ((int)(gs[h] > mine) | ((int)(gs[h] == mine) & (int)(h < lane)));
   }
   const unsigned selmask = (unsigned)__ballot(lane < 8 && mine > -1e30f && rank < 4);
-  const bool in_sel = (selmask >> (lane >> 3)) & 1u;
+  // a bit blend, not a conditional: the compiler would branch on in_sel
+  const int sel = -(int)((selmask >> (lane >> 3)) & 1u);
+  const int kf = sort_key(-1e30f);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) vk4[m] = in_sel ? sort_key(choice[m]) : sort_key(-1e30f);
+  for (int m = 0; m < 4; ++m) vk4[m] = (sort_key(choice[m]) & sel) | (kf & ~sel);
 }
 
 // route() for one token, executed by one full wave with the sigmoid scores
@@ -467,17 +471,19 @@ __device__ __forceinline__ void route_set_publish(const float score[4], const fl
         tn = i == K ? t[i] : tn;
       }
       const int kth = __builtin_amdgcn_readlane(tk, 63);
-      int next;
       if (K < 8) {
-        next = __builtin_amdgcn_readlane(tn, 63);
+        const int next = __builtin_amdgcn_readlane(tn, 63);
+        ambiguous = kth == INT_MIN || (next != INT_MIN && (next >> 8) == (kth >> 8));
       } else {
-        // the ninth: the largest key below the eighth
-        int m = INT_MIN;
+        // no ninth key shares the eighth's truncated prefix: exactly eight
+        // keys have a prefix >= it (non-candidates, INT_MIN, lie below every
+        // candidate's prefix); ballots and counts instead of a wave maximum
+        const int kp = kth >> 8;
+        int cnt = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) m = max(m, pk[j] < kth ? pk[j] : INT_MIN);
-        next = wave_max_i32(m);
+        for (int j = 0; j < 4; ++j) cnt += __popcll(__ballot((pk[j] >> 8) >= kp));
+        ambiguous = kth == INT_MIN || cnt != 8;
       }
-      ambiguous = kth == INT_MIN || (next != INT_MIN && (next >> 8) == (kth >> 8));
       if (!ambiguous) {
         const int s = lane - 48;
         int v = t[0];
