@@ -32,6 +32,7 @@ constexpr int kMvChunk = 512;   // halves per wave load
 constexpr int kMvBatch = 8;     // loads in flight per wave
 constexpr int kMvWaves = 4;
 constexpr int kMvMaxCols = 16384;  // o_proj input: 128 heads x 128
+constexpr int kMvWideWaves = 6;    // waves per workgroup for rows wider than 8192 (o_proj)
 
 __device__ __forceinline__ float mv_dot8(u32x4 w, const float* x, float acc) {
   const f32x4 x0 = *reinterpret_cast<const f32x4*>(x), x1 = *reinterpret_cast<const f32x4*>(x + 4);
@@ -57,30 +58,31 @@ __device__ __forceinline__ float lane_sum(float v, int width) {
 }  // namespace
 
 // y[r] = (res ? res[r] : 0) + W[r] . x for rows r < rows; cols % 512 == 0,
-// cols <= 16384.  One wave per row (grid-stride), x staged in LDS (cols
-// floats of dynamic LDS: the narrow projections keep more workgroups per CU
-// than a fixed 64 KB would allow).
-__global__ __launch_bounds__(kMvWaves * 64) void k_mv_f16(const uint16_t* __restrict__ W,
-                                                          const float* __restrict__ x,
-                                                          const float* __restrict__ res,
-                                                          float* __restrict__ y, int rows, int cols) {
+// cols <= 16384.  One wave per row (grid-stride), WV waves per workgroup
+// sharing x staged in LDS (cols floats of dynamic LDS: the narrow
+// projections keep more workgroups per CU than a fixed 64 KB would allow),
+// NB 1 KB loads in flight per wave.
+template <int WV, int NB>
+__global__ __launch_bounds__(WV * 64) void k_mv_f16(const uint16_t* __restrict__ W, const float* __restrict__ x,
+                                                    const float* __restrict__ res, float* __restrict__ y, int rows,
+                                                    int cols) {
   extern __shared__ float xs[];  // cols floats
   for (int i = threadIdx.x; i < cols / 4; i += blockDim.x)
     reinterpret_cast<f32x4*>(xs)[i] = reinterpret_cast<const f32x4*>(x)[i];
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n_waves = gridDim.x * kMvWaves, chunks = cols / kMvChunk;
-  for (int r = blockIdx.x * kMvWaves + wave; r < rows; r += n_waves) {
+  const int n_waves = gridDim.x * WV, chunks = cols / kMvChunk;
+  for (int r = blockIdx.x * WV + wave; r < rows; r += n_waves) {
     const uint16_t* wr = W + (size_t)r * cols + 8 * lane;
     float acc = 0.0f;
-    for (int b = 0; b < chunks; b += kMvBatch) {
-      u32x4 w[kMvBatch];
+    for (int b = 0; b < chunks; b += NB) {
+      u32x4 w[NB];
 #pragma unroll
-      for (int i = 0; i < kMvBatch; ++i)
+      for (int i = 0; i < NB; ++i)
         if (b + i < chunks) w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + (b + i) * kMvChunk));
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < kMvBatch; ++i)
+      for (int i = 0; i < NB; ++i)
         if (b + i < chunks) acc = mv_dot8(w[i], xs + (b + i) * kMvChunk + 8 * lane, acc);
     }
     acc = wave_sum_lane0(acc);  // the butterfly's lane-0 sum, VALU only
@@ -522,8 +524,17 @@ hipError_t launch_mv_f16(const uint16_t* W, const float* x, const float* res, fl
   if (cols < 512 || cols % 512 != 0 || cols > kMvMaxCols) return hipErrorInvalidValue;
   const size_t lds = (size_t)cols * sizeof(float);
   const int per_cu = max(1, min(8, (int)((160u << 10) / lds)));  // workgroups per CU the LDS allows
-  const int wgs = min((rows + kMvWaves - 1) / kMvWaves, per_cu * g_num_cus);
-  k_mv_f16<<<wgs, kMvWaves * 64, lds, s>>>(W, x, res, y, rows, cols);
+  if (cols > 8192) {
+    // o_proj: 64 KB of x allow two workgroups per CU; six waves each share
+    // it (measured 97.0-97.3 against 97.6-97.7 us per token with four; five,
+    // seven, or sixteen loads in flight no better)
+    constexpr int WV = kMvWideWaves;
+    const int wgs = min((rows + WV - 1) / WV, per_cu * g_num_cus);
+    k_mv_f16<WV, kMvBatch><<<wgs, WV * 64, lds, s>>>(W, x, res, y, rows, cols);
+  } else {
+    const int wgs = min((rows + kMvWaves - 1) / kMvWaves, per_cu * g_num_cus);
+    k_mv_f16<kMvWaves, kMvBatch><<<wgs, kMvWaves * 64, lds, s>>>(W, x, res, y, rows, cols);
+  }
   return hipGetLastError();
 }
 
