@@ -126,10 +126,21 @@ __global__ __launch_bounds__(kMvWaves * 64) void k_mv_f16_xw(const uint16_t* __r
 #pragma unroll
     for (int i = 0; i < NT; ++i) w[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wr + i * kMvChunk));
   };
+  // x and nw (28 KB each, L2 hits after the first workgroups) are requested
+  // before the row, so they return first and are staged while the row's
+  // loads are in flight (the registers are free: workgroup 0's norm sets
+  // the kernel's VGPR count)
+  constexpr int kXv = kHidden / 4 / (kMvWaves * 64);  // 7 float4s per thread
+  f32x4 xv[kXv], nv[kXv];
+#pragma unroll
+  for (int k = 0; k < kXv; ++k) {
+    xv[k] = reinterpret_cast<const f32x4*>(x)[threadIdx.x + kMvWaves * 64 * k];
+    nv[k] = reinterpret_cast<const f32x4*>(nw)[threadIdx.x + kMvWaves * 64 * k];
+  }
   load_row(r0);
   f32x4* xs = reinterpret_cast<f32x4*>(sm.k);
-  for (int i = threadIdx.x; i < kHidden / 4; i += kMvWaves * 64)
-    xs[i] = reinterpret_cast<const f32x4*>(x)[i] * reinterpret_cast<const f32x4*>(nw)[i];
+#pragma unroll
+  for (int k = 0; k < kXv; ++k) xs[threadIdx.x + kMvWaves * 64 * k] = xv[k] * nv[k];
   __syncthreads();
   for (int r = r0; r < rows; r += n_waves) {
     if (r != r0) load_row(r);
