@@ -177,7 +177,7 @@ def moe_forward_host(L, h_post, exp_idx, exp_w, K, moe_out):
 
 
 BATCH_AUTO, BATCH_DOT4, BATCH_MFMA = 0, 1, 2
-BATCH_MFMA_MIN_T = 6
+BATCH_MFMA_MIN_T = 12
 NOALLOC_MAX_T = 32  # FDM_NOALLOC_MAX_T
 NOALLOC_MAX_PAIRS = 256  # FDM_NOALLOC_MAX_PAIRS
 

@@ -339,7 +339,7 @@ int fdm_moe_forward_batched_noalloc(int L, const float *d_X, const float *d_H_in
 #define FDM_BATCH_AUTO 0
 #define FDM_BATCH_DOT4 1
 #define FDM_BATCH_MFMA 2
-#define FDM_BATCH_MFMA_MIN_T 6
+#define FDM_BATCH_MFMA_MIN_T 12
 int fdm_set_batch_kernel(int mode, int *prev);
 
 /* ---- rms_norm on the device (infer.m:369-374, the h_post of infer.m:1850):

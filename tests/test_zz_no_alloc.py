@@ -46,7 +46,7 @@ def step(fdm, fn, L, X, H, T):
     return out, idx, w, nd
 
 
-@pytest.mark.parametrize("T", [8, 3], ids=["mfma_path", "dot4_path"])
+@pytest.mark.parametrize("T", [16, 3], ids=["mfma_path", "dot4_path"])
 def test_noalloc_captures_in_a_graph(fdm, layer, T):
     """The property the entry point exists for: it allocates nothing.  The
     call is captured into a HIP graph on a fresh stream in global capture
