@@ -199,16 +199,9 @@ __device__ __forceinline__ void wait_route_xd(const LayerArgs& a, int slot, bool
 // h_post = (h * inv) * w element by element as infer.m:372.  Whole
 // workgroup; h is 16-byte aligned.
 __device__ __forceinline__ float layer_inv(const LayerArgs& a, LayerSmem& sm) {
-  const f32x4* h4 = reinterpret_cast<const f32x4*>(a.h) + threadIdx.x * (kRmsMaxPer / 4);
   float xv[kRmsMaxPer];
-#pragma unroll
-  for (int k = 0; k < kRmsMaxPer / 4; ++k) {
-    const f32x4 v = h4[k];  // the thread's 28 consecutive elements
-    xv[4 * k] = v.x;
-    xv[4 * k + 1] = v.y;
-    xv[4 * k + 2] = v.z;
-    xv[4 * k + 3] = v.w;
-  }
+  f32x4 c[kRmsMaxPer / 4];
+  rms_stage_7168<false>(reinterpret_cast<const f32x4*>(a.h), 1.0f, xv, c, sm.rms);
   const float inv = rms_inv(rms_sumsq_exact(xv, kHidden, sm.rms), kHidden);
   __syncthreads();  // sm.rms is reused by the caller's next stage
   return inv;

@@ -305,6 +305,36 @@ __device__ __forceinline__ float rms_inv(float ss, int d) {
   return 1.0f / sqrtf(ss / (float)d + 1e-6f);
 }
 
+// The thread layout of rms_sumsq_exact at d = 7168 (thread t: elements
+// 28 t .. 28 t + 27) from coalesced 16-byte loads (thread t: vectors t,
+// t + 256, .., each wave instruction one contiguous 1 KB), turned around
+// through sm.k: loaded directly, a wave's 16-byte loads lie 112 bytes apart,
+// seven times the cache-line requests of the same bytes.  c receives the
+// coalesced vectors (times mul when MUL).  sm.k is free again once the
+// caller's rms_sumsq_exact passes its first barrier.
+template <bool MUL>
+__device__ __forceinline__ void rms_stage_7168(const f32x4* __restrict__ x4, float mul, float (&xv)[kRmsMaxPer],
+                                               f32x4 (&c)[kRmsMaxPer / 4], RmsSmem& sm) {
+  constexpr int kV = kRmsMaxPer / 4;
+#pragma unroll
+  for (int k = 0; k < kV; ++k) {
+    c[k] = x4[threadIdx.x + kRmsThreads * k];
+    if (MUL) c[k] = c[k] * mul;
+  }
+  f32x4* st = reinterpret_cast<f32x4*>(sm.k);
+#pragma unroll
+  for (int k = 0; k < kV; ++k) st[threadIdx.x + kRmsThreads * k] = c[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kV; ++k) {
+    const f32x4 v = st[threadIdx.x * kV + k];
+    xv[4 * k] = v.x;
+    xv[4 * k + 1] = v.y;
+    xv[4 * k + 2] = v.z;
+    xv[4 * k + 3] = v.w;
+  }
+}
+
 // ---- rms_norm: o = x * (1 / sqrt(sum x^2 / d + 1e-6)) * w -------------------------------
 // (x = xr * mul elementwise: mul = 1 leaves xr as it is; the attention
 // passes the scale its raw projections still owe)
@@ -327,15 +357,9 @@ __device__ __forceinline__ void rms_norm_row(const float* __restrict__ xr, const
     const f32x4* x4 = reinterpret_cast<const f32x4*>(xr);
     f32x4 xc[kV], wc[kV];
 #pragma unroll
-    for (int k = 0; k < kV; ++k) {
-      const f32x4 v = x4[i0 / 4 + k] * mul;  // the thread's 28 consecutive elements
-      xv[4 * k] = v.x;
-      xv[4 * k + 1] = v.y;
-      xv[4 * k + 2] = v.z;
-      xv[4 * k + 3] = v.w;
-      xc[k] = x4[threadIdx.x + kRmsThreads * k] * mul;  // coalesced, for the output
+    for (int k = 0; k < kV; ++k)
       wc[k] = w ? reinterpret_cast<const f32x4*>(w)[threadIdx.x + kRmsThreads * k] : f32x4{1.0f, 1.0f, 1.0f, 1.0f};
-    }
+    rms_stage_7168<true>(x4, mul, xv, xc, sm);  // xc: the coalesced vectors, for the output
     const float inv = rms_inv(rms_sumsq_exact(xv, d, sm), d);
 #pragma unroll
     for (int k = 0; k < kV; ++k) {
@@ -374,15 +398,8 @@ __device__ __forceinline__ float rms_norm_inv(const float* __restrict__ xr, int 
   const int i0 = threadIdx.x * n;
   float xv[kRmsMaxPer];
   if (d == kHidden && (reinterpret_cast<uintptr_t>(xr) & 15) == 0) {
-    const f32x4* x4 = reinterpret_cast<const f32x4*>(xr);
-#pragma unroll
-    for (int k = 0; k < kRmsMaxPer / 4; ++k) {
-      const f32x4 v = x4[i0 / 4 + k] * mul;
-      xv[4 * k] = v.x;
-      xv[4 * k + 1] = v.y;
-      xv[4 * k + 2] = v.z;
-      xv[4 * k + 3] = v.w;
-    }
+    f32x4 c[kRmsMaxPer / 4];
+    rms_stage_7168<true>(reinterpret_cast<const f32x4*>(xr), mul, xv, c, sm);
   } else {
 #pragma unroll
     for (int j = 0; j < kRmsMaxPer; ++j) {
